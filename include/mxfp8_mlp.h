@@ -1,0 +1,85 @@
+/*
+ * C-ABI of the MI355X (gfx950) MXFP8 fused SwiGLU-MLP library, libmxfp8_mlp.so.
+ *
+ * Plain pointers and sizes only.  Every pointer is a device pointer unless stated otherwise; `stream` is a
+ * hipStream_t (NULL = the default stream).  All launches are asynchronous on `stream`; nothing here
+ * allocates or frees device memory: callers own every buffer, including scratch.
+ *
+ * Return value: 0 on success, MXFP8_ERR_ARG (< 0) when an argument check fails (nothing was launched), or
+ * a positive hipError_t when a launch failed.  mxfp8_last_error() describes the last failure on the
+ * calling thread.
+ *
+ * MX layout shared by every entry point (reference: /root/reference/scripts/mxfp8.py:36-86):
+ *   codes   E4M3FN bytes, row-major with a row stride in elements (bytes);
+ *   scales  E8M0 bytes, one per 32 consecutive elements of a row, stored in the 128x4 blocked layout:
+ *           byte of (row i, block b) at ((i/128)*n_col_tiles + b/4)*512 + (i%32)*16 + ((i%128)/32)*4 + b%4,
+ *           where n_col_tiles = the number of 128-column tiles of the (destination) row; rows past the end up
+ *           to the next multiple of 128 hold scale 0.
+ */
+#ifndef MXFP8_MLP_H
+#define MXFP8_MLP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXFP8_MLP_ABI_VERSION 1
+#define MXFP8_OK 0
+#define MXFP8_ERR_ARG (-1)
+
+/* Returns MXFP8_MLP_ABI_VERSION of the built library (the Python loader refuses a mismatch). */
+int mxfp8_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* mxfp8_last_error(void);
+
+/*
+ * MX-quantize x[rows, cols] (bf16, row stride ld_x) along its rows (blocks of 32 columns).
+ * Replaces mx_quant / _quant_kernel (/root/reference/scripts/mxfp8.py:46-86) and, through the column-slice
+ * arguments, _mx_store's writes into a wider destination (/root/reference/scripts/fused_mlp.py:40-62):
+ *   codes  -> q[i * ld_q + c]            (q already points at the first destination column)
+ *   scales -> s, blocked with s_col_tiles tiles per tile row, starting at column tile s_tile0
+ * Padded rows rows..ceil(rows/128)*128 of the touched tiles get scale 0.
+ * Requires cols % 128 == 0, 16-byte aligned x/q rows (ld_x % 8 == 0, ld_q % 16 == 0).
+ */
+int mxfp8_quant_rows(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, int64_t ld_q, void* s,
+                     int64_t s_col_tiles, int64_t s_tile0, void* stream);
+
+/*
+ * One read of x[rows, cols] (bf16, row stride ld_x) producing both MX operands of a frozen weight:
+ *   q [rows, cols] + s   : along the rows (blocks of 32 columns), s_col_tiles = cols / 128
+ *   qt[cols, rows] + st  : quantization of xᵀ along its rows (blocks of 32 rows of x), st tiles = rows / 128
+ * Replaces quant_ref(w) + quant_ref(w.t().contiguous()) (/root/reference/scripts/mxfp8.py:40-43, :477-478,
+ * :488-490).  Either pair may be NULL to skip that axis.  Requires rows % 128 == 0 and cols % 128 == 0.
+ */
+int mxfp8_quant_dual(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, void* s, void* qt,
+                     void* st, void* stream);
+
+/*
+ * out[rows, cols] (fp32, dense) = E4M3(q) * 2^(e - 127), NaN where the scale byte is 0xFF.
+ * No reference counterpart as a function: the reference dequantizes only inside torch._scaled_mm
+ * (/root/reference/scripts/fused_mlp.py:279); this exposes the same arithmetic for checks.
+ */
+int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const void* s, int64_t s_col_tiles,
+                  float* out, void* stream);
+
+/*
+ * C[M, N] (bf16, row stride ldc) = bf16( A[M, K] · B[N, K]ᵀ ) with MX block scales on both operands, fp32
+ * accumulation, K-contiguous operands (row strides lda, ldb bytes), scales blocked with K/128 tiles per row.
+ * Replaces torch._scaled_mm(A, B.t(), sA, sB, out_dtype=bf16) (/root/reference/scripts/fused_mlp.py:279,
+ * :283, :309, :329).
+ * Optional rank-r epilogue (lora_p != NULL), replacing the addmm_ that follows (fused_mlp.py:284, :331):
+ *   C = bf16( bf16(A·Bᵀ) + alpha * P[M, r] · Q[N, r]ᵀ ),  P, Q bf16 with row strides ld_p, ld_q, r in {16, 32}.
+ * Requires K % 128 == 0, N % 128 == 0, lda/ldb % 16 == 0, ldc % 4 == 0.
+ */
+int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
+                  int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
+                  const void* lora_q, int64_t ld_q, int64_t r, float alpha, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXFP8_MLP_H */

@@ -1,0 +1,150 @@
+"""CPU oracle for the MXFP8 quantizer and its blocked scale layout.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker; the product path never imports it.
+
+Follows /root/reference/scripts/mxfp8.py:40-86 (quant_ref, _quant_kernel, mx_quant) and
+/root/reference/scripts/fused_mlp.py:40-62 (_mx_store).  The element arithmetic lives in mx_oracle.c
+(compiled to liboracle_mx.so by oracle/Makefile); this module adds the tensor plumbing, a second restatement of
+the blocked layout written the way torchao's ``to_blocked`` builds it (reshape/permute of padded tiles, torchao
+0.18.0 ``prototype/mx_formats/utils.py``), its inverse, and dequantization.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_mx.so")
+_lib = None
+
+
+def build():
+    """Compile liboracle_mx.so with the host C compiler (oracle/Makefile)."""
+    subprocess.run(["make", "-C", _HERE, "-s", "liboracle_mx.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i64, p = ctypes.c_int64, ctypes.c_void_p
+        L.oracle_e8m0_ieee.argtypes = [ctypes.c_float]
+        L.oracle_e8m0_ieee.restype = ctypes.c_int
+        L.oracle_e8m0_closed.argtypes = [ctypes.c_uint32]
+        L.oracle_e8m0_closed.restype = ctypes.c_int
+        L.oracle_e4m3_rne.argtypes = [ctypes.c_float]
+        L.oracle_e4m3_rne.restype = ctypes.c_uint8
+        L.oracle_e4m3_decode.argtypes = [ctypes.c_uint8]
+        L.oracle_e4m3_decode.restype = ctypes.c_float
+        L.oracle_blocked_offset.argtypes = [i64, i64, i64]
+        L.oracle_blocked_offset.restype = i64
+        L.oracle_mx_quant.argtypes = [p, i64, i64, i64, p, i64, i64, p, i64, i64]
+        L.oracle_mx_quant.restype = ctypes.c_int
+        L.oracle_mx_dequant.argtypes = [p, i64, i64, i64, p, i64, p]
+        L.oracle_mx_dequant.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def scale_bytes(rows, cols):
+    """Size of the blocked scale buffer of a [rows, cols] operand (mxfp8.py:83-84)."""
+    return -(-rows // 128) * (cols // 128) * 512
+
+
+def quant(x2d):
+    """[R, C] bf16 (C % 128 == 0) -> (codes uint8 [R, C], blocked scales uint8 [ceil(R/128)*(C/128)*512]).
+
+    Same contract as mxfp8.mx_quant (mxfp8.py:78-86) but on the CPU and returning raw bytes."""
+    assert x2d.dtype == torch.bfloat16 and x2d.dim() == 2 and x2d.shape[1] % 128 == 0, (x2d.dtype, x2d.shape)
+    x = x2d.detach().cpu().contiguous()
+    R, C = x.shape
+    q = torch.empty((R, C), dtype=torch.uint8)
+    s = torch.zeros(scale_bytes(R, C), dtype=torch.uint8)
+    rc = lib().oracle_mx_quant(x.data_ptr(), R, C, C, q.data_ptr(), C, 0, s.data_ptr(), C // 128, 0)
+    assert rc == 0
+    return q, s
+
+
+def quant_into(x2d, q, s, q_col0, s_col_tiles):
+    """Column-slice variant (fused_mlp.py:40-62): codes into q[:, q_col0:q_col0+C], scales into the blocked
+    layout of the destination width (s_col_tiles tiles per row of tiles) starting at tile q_col0 // 128."""
+    x = x2d.detach().cpu().contiguous()
+    R, C = x.shape
+    assert q.dtype == torch.uint8 and q.is_contiguous() and q_col0 % 128 == 0
+    rc = lib().oracle_mx_quant(x.data_ptr(), R, C, C, q.data_ptr(), q.shape[1], q_col0, s.data_ptr(),
+                               s_col_tiles, q_col0 // 128)
+    assert rc == 0
+
+
+def quant_t(x2d):
+    """Quantization of x2dᵀ along its last axis (mxfp8.py:478, :490: quant_ref(w.t().contiguous()))."""
+    return quant(x2d.t().contiguous())
+
+
+def e8m0_ieee(amax):
+    return lib().oracle_e8m0_ieee(float(amax))
+
+
+def e8m0_closed(bits):
+    return lib().oracle_e8m0_closed(int(bits))
+
+
+def e4m3_rne(x):
+    return int(lib().oracle_e4m3_rne(float(x)))
+
+
+def e4m3_lut():
+    """float32 [256]: value of every E4M3FN code (NaN for 0x7f / 0xff)."""
+    return np.array([lib().oracle_e4m3_decode(c) for c in range(256)], dtype=np.float32)
+
+
+def blocked_offset(i, b, n_col_tiles):
+    """Scale byte offset of (row i, block b): mxfp8.py:74 / fused_mlp.py:59-61."""
+    return ((i // 128) * n_col_tiles + b // 4) * 512 + (i % 32) * 16 + ((i % 128) // 32) * 4 + (b % 4)
+
+
+def to_blocked_torchao(scales):
+    """[R, nb] scale bytes (row-major, one per 32-block) -> flat blocked layout, built the way torchao 0.18.0's
+    ``to_blocked`` does it (pad to 128 x 4, split into 128x4 tiles, each tile rearranged as 32 x (4 x 4)).
+    An independent restatement of the same layout as ``blocked_offset``; padded entries are 0."""
+    R, nb = scales.shape
+    nr, nc = -(-R // 128), -(-nb // 4)
+    padded = torch.zeros((nr * 128, nc * 4), dtype=scales.dtype)
+    padded[:R, :nb] = scales
+    blocks = padded.view(nr, 128, nc, 4).permute(0, 2, 1, 3)  # [nr, nc, 128, 4]
+    rearranged = blocks.reshape(-1, 4, 32, 4).transpose(1, 2).reshape(-1, 32, 16)
+    return rearranged.flatten()
+
+
+def from_blocked(s_flat, rows, nblk, n_col_tiles=None):
+    """Inverse of the blocked layout: flat bytes -> [rows, nblk] (one byte per 32-block)."""
+    n_col_tiles = nblk // 4 if n_col_tiles is None else n_col_tiles
+    i = torch.arange(rows).view(-1, 1)
+    b = torch.arange(nblk).view(1, -1)
+    off = blocked_offset(i, b, n_col_tiles)
+    return s_flat.view(torch.uint8).reshape(-1)[off.reshape(-1)].view(rows, nblk)
+
+
+_LUT = None
+
+
+def dequant(q, s, rows, cols, n_col_tiles=None, ld=None):
+    """fp32 [rows, cols] = E4M3(q) * 2^(e - 127); NaN where the scale byte is 0xFF."""
+    global _LUT
+    if _LUT is None:
+        _LUT = torch.from_numpy(e4m3_lut())
+    qb = q.view(torch.uint8).cpu()
+    if ld is not None and ld != cols:
+        qb = qb.view(rows, ld)[:, :cols]
+    qb = qb.reshape(rows, cols)
+    n_col_tiles = cols // 128 if n_col_tiles is None else n_col_tiles
+    e = from_blocked(s.view(torch.uint8).cpu(), rows, cols // 32, n_col_tiles).to(torch.int32)
+    vals = _LUT[qb.long()].view(rows, cols // 32, 32)
+    out = torch.ldexp(vals, (e - 127).unsqueeze(-1).to(torch.float32))
+    out = torch.where((e == 255).unsqueeze(-1), torch.full_like(out, float("nan")), out)
+    return out.view(rows, cols)

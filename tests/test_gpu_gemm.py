@@ -1,0 +1,99 @@
+"""GPU parity of the MX GEMM (libmxfp8_mlp.so mxfp8_gemm_nt via mxfp8.mx_mm) against the oracle's
+dequantize -> matmul -> bf16 (the torch._scaled_mm contract, fused_mlp.py:279/283/309/329).
+
+Tolerances: the BASELINE bar is max|Δ| / max|ref| <= 2e-2.  Both sides form the same exact products and sum
+them in fp32 in different orders, so a tighter elementwise bound also holds and is asserted: one bf16 rounding
+step of the reference value (2^-8 relative) plus fp32 reordering slack (1e-3 of max|ref|)."""
+import pytest
+import torch
+
+import mxfp8
+from oracle import mlp as omlp
+from oracle import mx
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _ref_gemm_f64(qa, sa, qb, sb, M, N, K):
+    a = mx.dequant(qa.view(torch.uint8).cpu(), sa.view(torch.uint8).cpu(), M, K).double()
+    b = mx.dequant(qb.view(torch.uint8).cpu(), sb.view(torch.uint8).cpu(), N, K).double()
+    return a @ b.t()
+
+
+def _assert_close(got, ref):
+    got = got.float().cpu().double()
+    err = (got - ref).abs()
+    scale = ref.abs().max().item()
+    assert err.max().item() <= TOL * scale, (err.max().item(), scale)
+    bound = ref.abs() * 2.0 ** -8 + 1e-3 * scale
+    bad = (err > bound).nonzero()
+    assert bad.numel() == 0, (bad[:5].tolist(), err.max().item())
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (300, 384, 256), (1, 128, 128), (513, 640, 1152),
+                                   (256, 7168, 1024), (1000, 1024, 3584)])
+def test_gemm_random(M, N, K, gpu):
+    g = torch.Generator().manual_seed(M * 31 + N * 7 + K)
+    a = (torch.randn(M, K, generator=g) * torch.exp2(torch.randint(-6, 6, (M, 1), generator=g).float()))
+    b = torch.randn(N, K, generator=g) * 0.02
+    qa, sa = mxfp8.mx_quant(a.to(torch.bfloat16).to(gpu))
+    qb, sb = mxfp8.mx_quant(b.to(torch.bfloat16).to(gpu))
+    c = mxfp8.mx_mm(qa, sa, qb, sb)
+    _assert_close(c, _ref_gemm_f64(qa, sa, qb, sb, M, N, K))
+
+
+def test_gemm_matches_oracle_bf16(gpu):
+    # against the oracle's own fp32-accumulated bf16 result (what the fused-MLP oracle uses)
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 384, 512, 2048
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    qa, sa = mx.quant(a)
+    qb, sb = mx.quant(b)
+    ref = omlp.mx_gemm(qa, sa, qb, sb, M, N, K).float()
+    c = mxfp8.mx_mm(qa.view(torch.float8_e4m3fn).to(gpu), sa.to(gpu), qb.view(torch.float8_e4m3fn).to(gpu),
+                    sb.to(gpu)).float().cpu()
+    ulp = (ref.abs() * 2.0 ** -7).clamp_min(1e-30)
+    assert ((c - ref).abs() <= ulp + 1e-3 * ref.abs().max()).all()
+
+
+def test_gemm_strided_weight_half(gpu):
+    # B operand as a column half of W_guᵀ [K, 2N] (row stride 2N): mx_wt's gate/up view (mxfp8.py:410-415)
+    g = torch.Generator().manual_seed(9)
+    T, K, N = 256, 256, 384
+    w = (torch.randn(2 * N, K, generator=g) * 0.02).to(torch.bfloat16)
+    dy = torch.randn(T, N, generator=g).to(torch.bfloat16).to(gpu)
+    q, s, qt, st = mxfp8.quant_both(w.to(gpu))
+    import types
+    hold = types.SimpleNamespace(n=N, half_t=[None, None], w=q, ws=s, wt=qt, wts=st)
+
+    class _Lin:
+        pass
+
+    lin = _Lin()
+    lin._mx_gu = (hold, 1)
+    qd, sd = mxfp8.mx_quant(dy)
+    wt, wts = mxfp8.mx_wt(lin)
+    assert wt.stride(0) == 2 * N
+    dx = mxfp8.mx_mm(qd, sd, wt, wts)
+    qtr, str_ = mx.quant_t(w[N:])
+    _assert_close(dx, _ref_gemm_f64(qd, sd, qtr, str_, T, K, N))
+
+
+@pytest.mark.parametrize("r", [16, 32])
+def test_gemm_lora_epilogue(r, gpu):
+    # C = bf16(bf16(A·Bᵀ) + alpha · P·Qᵀ): the y.addmm_(xsd, bdᵀ, alpha=s_d) of fused_mlp.py:284
+    g = torch.Generator().manual_seed(r)
+    M, N, K = 300, 1024, 512
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    P = torch.randn(M, r, generator=g).to(torch.bfloat16)
+    Q = (torch.randn(N, r, generator=g) * 0.5).to(torch.bfloat16)
+    qa, sa = mxfp8.mx_quant(a)
+    qb, sb = mxfp8.mx_quant(b)
+    c0 = mxfp8.mx_mm(qa, sa, qb, sb)
+    c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P.to(gpu), Q.to(gpu)), alpha=2.0)
+    ref = (c0.float().cpu() + 2.0 * (P.float() @ Q.float().t())).to(torch.bfloat16).float()
+    err = (c.float().cpu() - ref).abs()
+    assert (err <= ref.abs() * 2.0 ** -7 + 1e-4).all(), err.max()

@@ -1,0 +1,110 @@
+"""ctypes binding of libmxfp8_mlp.so, the gfx950 HIP library behind mxfp8.py and fused_mlp.py.
+
+The C-ABI is declared in include/mxfp8_mlp.h.  Every call passes raw device pointers, sizes and the current
+HIP stream of the tensors' device, so launches stay asynchronous and ordered with PyTorch's own work.  There
+is no fallback: if the library is missing or does not match this module's ABI version, the first call raises.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
+ABI_VERSION = 1
+
+_i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
+
+# name -> argument types, in the order of include/mxfp8_mlp.h
+SIGNATURES = {
+    "mxfp8_abi_version": [],
+    "mxfp8_last_error": [],
+    "mxfp8_quant_rows": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr],
+    "mxfp8_quant_dual": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr],
+    "mxfp8_dequant": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr],
+    "mxfp8_gemm_nt": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
+                      _i64, _f32, _ptr],
+}
+
+_lib = None
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def load(path=LIB_PATH):
+    """Load and type the library (no GPU work)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise NativeError(f"{path} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
+                          "or `make -C train-model-template_amd/csrc`; the MXFP8 path has no CPU fallback")
+    L = ctypes.CDLL(path)
+    for name, args in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_char_p if name == "mxfp8_last_error" else _int
+    v = L.mxfp8_abi_version()
+    if v != ABI_VERSION:
+        raise NativeError(f"{path}: ABI version {v}, expected {ABI_VERSION}; rebuild the library")
+    _lib = L
+    return L
+
+
+def _check(rc, name):
+    if rc != 0:
+        raise NativeError(f"{name} failed with code {rc}: {_lib.mxfp8_last_error().decode()}")
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _gpu(t, what):
+    if not t.is_cuda:
+        raise NativeError(f"{what}: tensors must be on the GPU (the MXFP8 path has no CPU implementation)")
+
+
+def call(name, *args, like):
+    """Call entry point `name` with `args` followed by the current stream of tensor `like`'s device."""
+    L = load()
+    _gpu(like, name)
+    rc = getattr(L, name)(*args, _stream(like))
+    _check(rc, name)
+
+
+def quant_rows(x, q, s, ld_q=None, s_col_tiles=None, s_tile0=0):
+    """x [R, C] bf16 (row stride x.stride(0)) -> codes into q (a [R, >=C] uint8 view, row stride ld_q) and
+    blocked scales into s."""
+    R, C = x.shape
+    ld_q = q.stride(0) if ld_q is None else ld_q
+    s_col_tiles = C // 128 if s_col_tiles is None else s_col_tiles
+    call("mxfp8_quant_rows", _p(x), R, C, x.stride(0), _p(q), ld_q, _p(s), s_col_tiles, s_tile0, like=x)
+
+
+def quant_dual(x, q, s, qt, st):
+    R, C = x.shape
+    call("mxfp8_quant_dual", _p(x), R, C, x.stride(0), _p(q), _p(s), _p(qt), _p(st), like=x)
+
+
+def dequant(q, s, rows, cols, ld_q, s_col_tiles, out):
+    call("mxfp8_dequant", _p(q), rows, cols, ld_q, _p(s), s_col_tiles, _p(out), like=out)
+
+
+def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0):
+    """c[M, N] = bf16(A·Bᵀ) [+ alpha · P·Qᵀ with lora = (P [M, r], Q [N, r])]."""
+    if lora is None:
+        p = q = None
+        ldp = ldq = r = 0
+    else:
+        p, q = lora
+        r = p.shape[1]
+        ldp, ldq = p.stride(0), q.stride(0)
+    call("mxfp8_gemm_nt", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(p), ldp,
+         _p(q), ldq, r, float(alpha), like=c)

@@ -1,0 +1,90 @@
+// Device helpers shared by the MXFP8 kernels (gfx950 only).
+//
+// Numeric contract (reference: /root/reference/scripts/mxfp8.py:46-75, fused_mlp.py:40-62):
+//   amax  = max |v| over a 32-element block, NaN if any element is NaN
+//   e     = E8M0 round-up of amax / 448 (satfinite): 255 for NaN, 254 for inf, 0 for amax <= 448 * 2^-127
+//   code  = RNE E4M3FN of clamp(v * 2^(127 - e), -448, 448)   (e == 0 scales by 1, e == 255 -> code 0x7F)
+// The exponent uses the division-free closed form on the amax bit pattern: with amax = (1 + m/2^23) 2^(E-127)
+// and 448 = 1.75 * 2^8, ceil(log2(amax / 448)) = E - 135 + [m > 0x600000]; the fp32 quotient of the reference
+// never rounds across a power of two, so both routes agree for every fp32 amax.
+//
+// Register layouts of the gfx950 matrix instructions used here (measured on the device):
+//   v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 x e4m3): operand lane l, byte j holds row l%32 and
+//     k = 32*(j/16) + 16*(l/32) + j%16; the E8M0 scale of (row r, 32-block kb) is read from lane r + 32*kb,
+//     byte op_sel of the 32-bit scale register.
+//   v_mfma_f32_32x32x16_bf16: operand lane l, element i holds row l%32, k = 8*(l/32) + i.
+//   32x32 f32 accumulators: lane l, register i holds row (i/4)*8 + (l/32)*4 + i%4, column l%32.
+//   v_cvt_pk_fp8_f32 converts to OCP E4M3FN with round-to-nearest-even (bit-exact with an RNE reference for
+//     every bf16 input in [-448, 448]); NaN converts to 0x7F / 0xFF.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxk {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) { return __uint_as_float(f32_to_bf16_bits(f) << 16); }
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// |v| bit pattern: for non-negative floats the unsigned order is the float order and every NaN pattern is
+// above +inf, so an unsigned max over these propagates NaN (tl.maximum(..., propagate_nan=ALL)).
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
+
+// E8M0 exponent from the amax bit pattern (sign already cleared).
+__device__ __forceinline__ uint32_t e8m0_from_amax_bits(uint32_t b) {
+  uint32_t E = b >> 23, m = b & 0x7fffffu;
+  int e = (int)E - 8 + (m > 0x600000u ? 1 : 0);
+  e = e < 0 ? 0 : e;
+  if (E == 255u) e = m ? 255 : 254;
+  return (uint32_t)e;
+}
+
+// Exponent shift applied to the elements of a block with scale byte e (e != 255).
+__device__ __forceinline__ int e8m0_shift(uint32_t e) { return e == 0u ? 0 : 127 - (int)e; }
+
+__device__ __forceinline__ float scale_clamp(float v, int sh) {
+  float t = __builtin_ldexpf(v, sh);
+  return __builtin_fminf(__builtin_fmaxf(t, -448.0f), 448.0f);
+}
+
+// Four block elements -> four E4M3 codes packed little-endian in one dword.
+__device__ __forceinline__ uint32_t encode4(float a, float b, float c, float d, uint32_t e) {
+  if (e == 255u) return 0x7f7f7f7fu;
+  int sh = e8m0_shift(e);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(scale_clamp(a, sh), scale_clamp(b, sh), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(scale_clamp(c, sh), scale_clamp(d, sh), w, true);
+  return (uint32_t)w;
+}
+
+// Byte offset of the scale of (row i, 32-block b) in the 128x4 blocked layout with n_col_tiles tiles of
+// 128 columns per row of tiles.
+__device__ __forceinline__ int64_t blocked_offset(int64_t i, int64_t b, int64_t n_col_tiles) {
+  return ((i >> 7) * n_col_tiles + (b >> 2)) * 512 + (i & 31) * 16 + ((i & 127) >> 5) * 4 + (b & 3);
+}
+
+// Unsigned max over a 4-lane group (the 4 lanes that share one 32-element block).
+__device__ __forceinline__ uint32_t quad_umax(uint32_t v) {
+  v = max(v, (uint32_t)__shfl_xor((int)v, 1));
+  v = max(v, (uint32_t)__shfl_xor((int)v, 2));
+  return v;
+}
+
+}  // namespace mxk

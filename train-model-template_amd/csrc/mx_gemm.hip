@@ -1,0 +1,249 @@
+// MX block-scaled GEMM for gfx950: C[M, N] = bf16(A[M, K] · B[N, K]ᵀ), E4M3 operands with E8M0 scales per 32
+// elements along K, fp32 accumulation on v_mfma_scale_f32_32x32x64_f8f6f4, optional rank-r bf16 epilogue.
+//
+// Replaces torch._scaled_mm (cuBLAS block-scaled GEMM) at /root/reference/scripts/fused_mlp.py:279, :283, :309,
+// :329 and the addmm_ epilogues at :284 and :331.
+//
+// Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile in K steps of 64 (two scale blocks).
+// The eight waves form a 2 (N) x 4 (M) grid of 128 x 64 sub-tiles, each a 4 x 2 grid of 32 x 32 MFMA tiles
+// (128 accumulators per lane); two waves share each SIMD so one's LDS reads overlap the other's MFMAs.
+// The matrix instruction takes the weight (B) fragment as its first operand, so each lane's accumulators
+// cover one output row m and 16 columns n in runs of 4.
+//
+// Operand staging: global memory goes straight into LDS with global_load_lds_dwordx4 (no VGPR round trip)
+// through a ring of 4 stages of 34 KB: A codes 256 x 64 B, B codes 256 x 64 B, and the two 128-row blocked
+// scale tiles of each operand for the current 128-wide K tile.  Every wave issues exactly five DMA
+// instructions per stage (four 1 KB code slices and one 256 B scale slice), so a fixed vmcnt bounds the wait
+// for a stage while the next two stay in flight.  Lane i of a DMA lands at base + 16 i; a row's 16-byte
+// chunk c is stored at chunk c ^ ((row >> 1) & 3) so the 8 lanes served together by a ds_read_b128
+// (8 consecutive rows, same chunk) hit 8 distinct bank groups.
+// Scale words: for a 32-row group the 16 bytes at (row % 32) * 16 of a blocked tile hold the four 32-row
+// groups' scales for one 128-wide K tile; a lane shifts its word by 8 * (lane / 32) so that op_sel 0 / 2
+// selects block 2P + lane/32 of the current half-tile P.
+#include <type_traits>
+
+#include "abi_common.h"
+#include "mx_device.h"
+
+using namespace mxk;
+
+namespace {
+
+constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4, kThreads = 512;
+constexpr int kCodeBytes = kBM * kBK;                 // 16 KB per operand per stage
+constexpr int kOffA = 0, kOffB = kCodeBytes, kOffSA = 2 * kCodeBytes, kOffSB = 2 * kCodeBytes + 1024;
+constexpr int kStageBytes = 2 * kCodeBytes + 2048;    // 34 KB
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// global_load_lds_dwordx4: lane i's 16 bytes land at LDS address m0 + 16 i.  Issued from inline assembly so
+// the compiler does not treat every later LDS read as dependent on every outstanding DMA (it cannot tell the
+// ring stages apart and would drain the ring with vmcnt(0)); the kernel orders them itself with explicit
+// vmcnt waits and barriers.  m0 is written here and nowhere else in the kernels of this file.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr_t)p; }
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N) leaving the other counters unconstrained (gfx9 encoding: vmcnt[3:0] at bits 3:0,
+// vmcnt[5:4] at bits 15:14, expcnt at 6:4, lgkmcnt at 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+struct Lora {
+  const uint16_t* p;  // [M, r] bf16
+  int64_t ld_p;
+  const uint16_t* q;  // [N, r] bf16
+  int64_t ld_q;
+  float alpha;
+};
+
+// 32 bytes of one operand row for the stage's 64-wide K step: chunk c0 (k 16*(l/32)..) and c0 + 2 (k 32 + ..)
+__device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw) {
+  uint4 lo = *reinterpret_cast<const uint4*>(base + row * kBK + ((c0 ^ sw) << 4));
+  uint4 hi = *reinterpret_cast<const uint4*>(base + row * kBK + (((c0 + 2) ^ sw) << 4));
+  v8i r;
+  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+  return r;
+}
+
+template <int kR>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restrict__ A,
+                                                        const uint8_t* __restrict__ SA, int64_t lda,
+                                                        const uint8_t* __restrict__ B,
+                                                        const uint8_t* __restrict__ SB, int64_t ldb, int M, int N,
+                                                        int K, uint16_t* __restrict__ C, int64_t ldc, Lora lora) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageBytes];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int wn = wave >> 2, wm = wave & 3;  // compute sub-tile: n rows wn*128 + [0,128), m rows wm*64 + [0,64)
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int ns = K / kBK;  // even: K % 128 == 0
+  const int nkt = K / 128;
+
+  // DMA roles: waves 0-3 stage A, waves 4-7 stage B; wave slot w4 = wave & 3 covers rows w4*64 + [0, 64)
+  // in four 1 KB slices (16 rows x 64 B), lane -> row slice*16 + lane/4, physical chunk lane & 3.
+  const bool dB = wave >= 4;
+  const int w4 = wave & 3;
+  const int R0 = dB ? n0 : m0, Rn = dB ? N : M;
+  const int64_t ldd = dB ? ldb : lda;
+  const uint8_t* gb = (dB ? B : A) + (int64_t)R0 * ldd;
+  const int lchunk = (lane & 3) ^ ((lane >> 3) & 3);  // (row >> 1) & 3 == (lane >> 3) & 3 for these rows
+  uint32_t goff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = w4 * 64 + j * 16 + (lane >> 2);
+    goff[j] = (uint32_t)((min(R0 + row, Rn - 1) - R0) * ldd) + lchunk * 16;  // clamp rows past the end
+  }
+  const int stile = min((R0 >> 7) + (w4 >> 1), (Rn - 1) >> 7);
+  const uint8_t* sgp = (dB ? SB : SA) + (int64_t)stile * nkt * 512 + (w4 & 1) * 256 + (lane & 15) * 16;
+  const int dma_code_off = (dB ? kOffB : kOffA) + w4 * 4096;
+  const int dma_scale_off = (dB ? kOffSB : kOffSA) + w4 * 256;
+
+  const uint32_t lds0 = lds_addr(lds);
+  auto issue = [&](int s) {
+    const uint32_t st = lds0 + (s & (kStages - 1)) * kStageBytes;
+    const uint8_t* g = gb + s * kBK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(g + goff[j], st + dma_code_off + j * 1024);
+    if (lane < 16) dma16(sgp + (s >> 1) * 512, st + dma_scale_off);
+  };
+
+  v16f acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i][0] = v16f{};
+    acc[i][1] = v16f{};
+  }
+
+  const int sshift = (lane >> 5) * 8;
+  const int sw = (lane >> 1) & 3;   // swizzle of rows base + lane % 32 (base a multiple of 32)
+  const int c0 = lane >> 5;
+  auto compute = [&](int s, auto pc) {
+    constexpr int P = decltype(pc)::value;  // half of the 128-wide K tile: blocks 2P, 2P + 1
+    const uint8_t* st = lds + (s & (kStages - 1)) * kStageBytes;
+    const uint2 sa2 = *reinterpret_cast<const uint2*>(st + kOffSA + (wm >> 1) * 512 + (lane & 31) * 16 + (wm & 1) * 8);
+    const uint4 sb4 = *reinterpret_cast<const uint4*>(st + kOffSB + wn * 512 + (lane & 31) * 16);
+    const int sa0 = (int)(sa2.x >> sshift), sa1 = (int)(sa2.y >> sshift);
+    const int sb0 = (int)(sb4.x >> sshift), sb1 = (int)(sb4.y >> sshift);
+    const int sb2 = (int)(sb4.z >> sshift), sb3 = (int)(sb4.w >> sshift);
+    const uint8_t* la = st + kOffA;
+    const uint8_t* lb = st + kOffB;
+    const v8i fa0 = frag(la, wm * 64 + (lane & 31), c0, sw);
+    const v8i fa1 = frag(la, wm * 64 + 32 + (lane & 31), c0, sw);
+    const v8i fb0 = frag(lb, wn * 128 + (lane & 31), c0, sw);
+    const v8i fb1 = frag(lb, wn * 128 + 32 + (lane & 31), c0, sw);
+    const v8i fb2 = frag(lb, wn * 128 + 64 + (lane & 31), c0, sw);
+    const v8i fb3 = frag(lb, wn * 128 + 96 + (lane & 31), c0, sw);
+    acc[0][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb0, fa0, acc[0][0], 0, 0, 2 * P, sb0, 2 * P, sa0);
+    acc[0][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb0, fa1, acc[0][1], 0, 0, 2 * P, sb0, 2 * P, sa1);
+    acc[1][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb1, fa0, acc[1][0], 0, 0, 2 * P, sb1, 2 * P, sa0);
+    acc[1][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb1, fa1, acc[1][1], 0, 0, 2 * P, sb1, 2 * P, sa1);
+    acc[2][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb2, fa0, acc[2][0], 0, 0, 2 * P, sb2, 2 * P, sa0);
+    acc[2][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb2, fa1, acc[2][1], 0, 0, 2 * P, sb2, 2 * P, sa1);
+    acc[3][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb3, fa0, acc[3][0], 0, 0, 2 * P, sb3, 2 * P, sa0);
+    acc[3][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb3, fa1, acc[3][1], 0, 0, 2 * P, sb3, 2 * P, sa1);
+  };
+  auto step = [&](int s, auto pc) {
+    // stage s was issued three iterations ago; the stages after it that are already in flight may stay so
+    if (s + 2 < ns) wait_vmcnt<10>();
+    else if (s + 1 < ns) wait_vmcnt<5>();
+    else wait_vmcnt<0>();
+    // Bare s_barrier: __syncthreads() adds a workgroup fence that waits for every outstanding DMA (vmcnt(0)),
+    // which would drain the ring.  The explicit vmcnt above already covers this wave's stage-s DMA.
+    __builtin_amdgcn_s_barrier();  // stage s visible to all waves; every wave is done with stage s-1's buffer
+    if (s + 3 < ns) issue(s + 3);
+    compute(s, pc);
+  };
+
+  issue(0);
+  if (ns > 1) issue(1);
+  if (ns > 2) issue(2);
+  for (int s = 0; s < ns; s += 2) {
+    step(s, std::integral_constant<int, 0>{});
+    step(s + 1, std::integral_constant<int, 1>{});
+  }
+
+  // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
+  // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int m = m0 + wm * 64 + mt * 32 + (lane & 31);
+    v8bf pf[2];
+    if constexpr (kR > 0) {
+      const int mc = min(m, M - 1);
+#pragma unroll
+      for (int h = 0; h < kR / 16; ++h)
+        pf[h] = *reinterpret_cast<const v8bf*>(lora.p + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8);
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int nb = n0 + wn * 128 + nt * 32;
+      v16f o = acc[nt][mt];
+      if constexpr (kR > 0) {
+        const int nr = min(nb + (lane & 31), N - 1);
+        v16f l = v16f{};
+#pragma unroll
+        for (int h = 0; h < kR / 16; ++h) {
+          v8bf qf = *reinterpret_cast<const v8bf*>(lora.q + (int64_t)nr * lora.ld_q + h * 16 + (lane >> 5) * 8);
+          l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf, pf[h], l, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = round_bf16(o[i]) + lora.alpha * l[i];
+      }
+      if (m < M) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = nb + g * 8 + (lane >> 5) * 4;
+          if (n < N) {
+            uint2 w = make_uint2(pack_bf16x2(o[4 * g], o[4 * g + 1]), pack_bf16x2(o[4 * g + 2], o[4 * g + 3]));
+            *reinterpret_cast<uint2*>(C + (int64_t)m * ldc + n) = w;
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
+                             int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
+                             const void* lora_q, int64_t ld_q, int64_t r, float alpha, void* stream) {
+  MX_CHECK_ARG(a && sa && b && sb && c, "mxfp8_gemm_nt: null pointer");
+  MX_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 128 == 0 && N % 128 == 0,
+               "mxfp8_gemm_nt: need K %% 128 == 0 and N %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
+               (long long)N, (long long)K);
+  MX_CHECK_ARG(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "mxfp8_gemm_nt: dimension too large");
+  MX_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0 && ldc >= N && ldc % 4 == 0,
+               "mxfp8_gemm_nt: bad strides");
+  MX_CHECK_ARG(256LL * lda < (1LL << 32) && 256LL * ldb < (1LL << 32), "mxfp8_gemm_nt: stride too large");
+  MX_CHECK_ARG(mx_aligned(a, 16) && mx_aligned(b, 16) && mx_aligned(sa, 16) && mx_aligned(sb, 16) &&
+                   mx_aligned(c, 8),
+               "mxfp8_gemm_nt: misaligned buffer");
+  if (lora_p) {
+    MX_CHECK_ARG(lora_q && (r == 16 || r == 32), "mxfp8_gemm_nt: epilogue needs P, Q and r in {16, 32}");
+    MX_CHECK_ARG(ld_p >= r && ld_q >= r && ld_p % 8 == 0 && ld_q % 8 == 0 && mx_aligned(lora_p, 16) &&
+                     mx_aligned(lora_q, 16),
+                 "mxfp8_gemm_nt: bad epilogue strides/alignment");
+  }
+  if (M == 0) return MXFP8_OK;
+  dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
+  Lora lo{(const uint16_t*)lora_p, ld_p, (const uint16_t*)lora_q, ld_q, alpha};
+  hipStream_t stm = (hipStream_t)stream;
+  const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
+  if (!lora_p)
+    gemm_kernel<0><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+  else if (r == 16)
+    gemm_kernel<16><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+  else
+    gemm_kernel<32><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+  MX_CHECK_LAUNCH("mxfp8_gemm_nt");
+  return MXFP8_OK;
+}

@@ -1,0 +1,216 @@
+// MXFP8 block-32 quantizer kernels for gfx950: along the rows (K axis), along the columns of a frozen weight
+// (transposed axis) in the same pass, and dequantization.
+//
+// Reference behaviour: /root/reference/scripts/mxfp8.py:46-86 (_quant_kernel, mx_quant), :40-43 (quant_ref),
+// /root/reference/scripts/fused_mlp.py:40-62 (_mx_store column slices).  Bytes are identical to the
+// reference arithmetic described in mx_device.h.
+//
+// Work decomposition: one 256-thread workgroup per 128 x 128 tile, which is exactly one 512-byte scale tile.
+// Each thread owns 8 consecutive columns (one 16-byte load) of 8 rows; the 4 threads of a 32-column block
+// reduce their amax with two lane swaps.  The tile's scale bytes are assembled in LDS and leave as one
+// coalesced 512-byte store.
+#include "abi_common.h"
+#include "mx_device.h"
+
+using namespace mxk;
+
+namespace {
+
+constexpr int kTile = 128;
+constexpr int kThreads = 256;
+constexpr int kLdT = kTile + 8;  // bf16 row stride of the LDS copy used by the transposed axis (16-B aligned)
+
+// Quantize 8 consecutive bf16 (one uint4) whose 4-lane group forms one 32-block; returns the codes and the
+// block's scale byte.
+__device__ __forceinline__ uint2 quant8(uint4 v, uint32_t& e_out) {
+  float f[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
+                bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
+  uint32_t am = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) am = max(am, abs_bits(f[k]));
+  am = quad_umax(am);
+  uint32_t e = e8m0_from_amax_bits(am);
+  e_out = e;
+  return make_uint2(encode4(f[0], f[1], f[2], f[3], e), encode4(f[4], f[5], f[6], f[7], e));
+}
+
+template <bool kRows, bool kCols>
+__global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                         int64_t ld_x, uint8_t* __restrict__ q, int64_t ld_q,
+                                                         uint8_t* __restrict__ s, int64_t s_col_tiles,
+                                                         int64_t s_tile0, uint8_t* __restrict__ qt,
+                                                         uint8_t* __restrict__ st) {
+  __shared__ uint32_t stile[kTile];                          // row-axis scale tile (512 B)
+  __shared__ uint32_t sttile[kTile];                         // transposed-axis scale tile
+  __shared__ __attribute__((aligned(16))) uint16_t xt[kCols ? kTile * kLdT : 1];
+  const int tid = threadIdx.x;
+  const int64_t ct = blockIdx.x;  // column tile
+  const int64_t rt = blockIdx.y;  // row tile
+  if (tid < kTile) {
+    stile[tid] = 0;
+    sttile[tid] = 0;
+  }
+  __syncthreads();
+  const int c8 = (tid & 15) * 8;  // first of this thread's 8 columns within the tile
+  const int rsub = tid >> 4;      // 0..15
+  const int64_t col = ct * kTile + c8;
+  uint4 v[8];
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int64_t r = rt * kTile + rsub + 16 * it;
+    v[it] = r < rows ? *reinterpret_cast<const uint4*>(x + r * ld_x + col) : make_uint4(0, 0, 0, 0);
+  }
+  uint8_t* sb = reinterpret_cast<uint8_t*>(stile);
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int rl = rsub + 16 * it;  // row within the tile
+    const int64_t r = rt * kTile + rl;
+    if (kRows) {
+      uint32_t e;
+      uint2 codes = quant8(v[it], e);
+      if (r < rows) {
+        *reinterpret_cast<uint2*>(q + r * ld_q + col) = codes;
+        if ((tid & 3) == 0) sb[(rl & 31) * 16 + (rl >> 5) * 4 + (c8 >> 5)] = (uint8_t)e;
+      }
+    }
+    if (kCols) *reinterpret_cast<uint4*>(xt + rl * kLdT + c8) = v[it];
+  }
+  if (kCols) {
+    __syncthreads();
+    // Transposed axis: wave w owns columns 32w..32w+31; lane l takes the column pair 2*(l%16) and the
+    // 8-row group l/16 of each 32-row block, so a column's 32-block sits in lanes l, l^16, l^32, l^48.
+    const int lane = tid & 63, wv = tid >> 6;
+    const int cl = wv * 32 + (lane & 15) * 2;  // first of the 2 columns within the tile
+    const int rg = lane >> 4;                   // 8-row group within a 32-row block
+    uint8_t* stb = reinterpret_cast<uint8_t*>(sttile);
+    const int64_t n_rows_t = rows;              // row count of x = column count of xᵀ
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      float a0[8], a1[8];
+      uint32_t m0 = 0, m1 = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int rl = rb * 32 + rg * 8 + i;
+        uint32_t w = *reinterpret_cast<const uint32_t*>(xt + rl * kLdT + cl);
+        a0[i] = bf16_lo(w);
+        a1[i] = bf16_hi(w);
+        m0 = max(m0, abs_bits(a0[i]));
+        m1 = max(m1, abs_bits(a1[i]));
+      }
+      m0 = max(m0, (uint32_t)__shfl_xor((int)m0, 16));
+      m0 = max(m0, (uint32_t)__shfl_xor((int)m0, 32));
+      m1 = max(m1, (uint32_t)__shfl_xor((int)m1, 16));
+      m1 = max(m1, (uint32_t)__shfl_xor((int)m1, 32));
+      const uint32_t e0 = e8m0_from_amax_bits(m0), e1 = e8m0_from_amax_bits(m1);
+      const int64_t c0 = ct * kTile + cl;                 // row of xᵀ
+      const int64_t r0 = rt * kTile + rb * 32 + rg * 8;   // first column of xᵀ
+      *reinterpret_cast<uint2*>(qt + c0 * n_rows_t + r0) =
+          make_uint2(encode4(a0[0], a0[1], a0[2], a0[3], e0), encode4(a0[4], a0[5], a0[6], a0[7], e0));
+      *reinterpret_cast<uint2*>(qt + (c0 + 1) * n_rows_t + r0) =
+          make_uint2(encode4(a1[0], a1[1], a1[2], a1[3], e1), encode4(a1[4], a1[5], a1[6], a1[7], e1));
+      if (rg == 0) {
+        stb[(cl & 31) * 16 + (cl >> 5) * 4 + rb] = (uint8_t)e0;
+        stb[((cl + 1) & 31) * 16 + ((cl + 1) >> 5) * 4 + rb] = (uint8_t)e1;
+      }
+    }
+  }
+  __syncthreads();
+  if (kRows && tid < 32)
+    reinterpret_cast<uint4*>(s + (rt * s_col_tiles + s_tile0 + ct) * 512)[tid] =
+        reinterpret_cast<const uint4*>(stile)[tid];
+  if (kCols && tid >= 64 && tid < 96) {
+    // tile (row tile ct, column tile rt) of xᵀ's blocked scales, rows/128 tiles per tile row
+    const int64_t n_tiles_t = rows / kTile;
+    reinterpret_cast<uint4*>(st + (ct * n_tiles_t + rt) * 512)[tid - 64] =
+        reinterpret_cast<const uint4*>(sttile)[tid - 64];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t* __restrict__ q, int64_t rows,
+                                                           int64_t cols, int64_t ld_q,
+                                                           const uint8_t* __restrict__ s, int64_t s_col_tiles,
+                                                           float* __restrict__ out) {
+  const int64_t idx = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+  const int64_t n = rows * cols;
+  if (idx >= n) return;
+  const int64_t i = idx / cols, c = idx % cols;  // cols % 128 == 0: the 4 elements share row and block
+  const uint32_t e = s[blocked_offset(i, c >> 5, s_col_tiles)];
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(q + i * ld_q + c);
+  float4 o;
+  float* po = reinterpret_cast<float*>(&o);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t code = (w >> (8 * k)) & 0xffu;
+    const uint32_t E = (code >> 3) & 0xfu, M = code & 7u;
+    float v = E == 0 ? __builtin_ldexpf((float)M, -9) : __builtin_ldexpf((float)(8u + M), (int)E - 10);
+    v = (code & 0x80u) ? -v : v;
+    if ((code & 0x7fu) == 0x7fu || e == 255u) v = __uint_as_float(0x7fc00000u);
+    else v = __builtin_ldexpf(v, (int)e - 127);
+    po[k] = v;
+  }
+  *reinterpret_cast<float4*>(out + idx) = o;
+}
+
+}  // namespace
+
+extern "C" int mxfp8_quant_rows(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, int64_t ld_q,
+                                void* s, int64_t s_col_tiles, int64_t s_tile0, void* stream) {
+  MX_CHECK_ARG(x && q && s, "mxfp8_quant_rows: null pointer");
+  MX_CHECK_ARG(rows >= 0 && cols > 0 && cols % 128 == 0, "mxfp8_quant_rows: need cols %% 128 == 0 (cols=%lld)",
+               (long long)cols);
+  MX_CHECK_ARG(ld_x >= cols && ld_x % 8 == 0 && ld_q >= cols && ld_q % 16 == 0,
+               "mxfp8_quant_rows: bad strides ld_x=%lld ld_q=%lld", (long long)ld_x, (long long)ld_q);
+  MX_CHECK_ARG(s_tile0 >= 0 && s_tile0 + cols / 128 <= s_col_tiles, "mxfp8_quant_rows: scale tiles out of range");
+  MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(q, 16) && mx_aligned(s, 16), "mxfp8_quant_rows: misaligned buffer");
+  if (rows == 0) return MXFP8_OK;
+  MX_CHECK_ARG((rows + 127) / 128 <= 0x7fffffff, "mxfp8_quant_rows: too many rows");
+  dim3 grid((unsigned)(cols / 128), (unsigned)((rows + 127) / 128));
+  quant_kernel<true, false><<<grid, kThreads, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, rows, ld_x, (uint8_t*)q, ld_q, (uint8_t*)s, s_col_tiles, s_tile0, nullptr, nullptr);
+  MX_CHECK_LAUNCH("mxfp8_quant_rows");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_quant_dual(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, void* s, void* qt,
+                                void* st, void* stream) {
+  MX_CHECK_ARG(x, "mxfp8_quant_dual: null input");
+  MX_CHECK_ARG((q == nullptr) == (s == nullptr) && (qt == nullptr) == (st == nullptr) && (q || qt),
+               "mxfp8_quant_dual: each axis needs both codes and scales");
+  MX_CHECK_ARG(rows > 0 && cols > 0 && rows % 128 == 0 && cols % 128 == 0,
+               "mxfp8_quant_dual: need rows, cols %% 128 == 0 (rows=%lld cols=%lld)", (long long)rows,
+               (long long)cols);
+  MX_CHECK_ARG(ld_x >= cols && ld_x % 8 == 0, "mxfp8_quant_dual: bad ld_x");
+  MX_CHECK_ARG(mx_aligned(x, 16) && (!q || (mx_aligned(q, 16) && mx_aligned(s, 16))) &&
+                   (!qt || (mx_aligned(qt, 16) && mx_aligned(st, 16))),
+               "mxfp8_quant_dual: misaligned buffer");
+  dim3 grid((unsigned)(cols / 128), (unsigned)(rows / 128));
+  hipStream_t stm = (hipStream_t)stream;
+  if (q && qt)
+    quant_kernel<true, true><<<grid, kThreads, 0, stm>>>((const uint16_t*)x, rows, ld_x, (uint8_t*)q, cols,
+                                                         (uint8_t*)s, cols / 128, 0, (uint8_t*)qt, (uint8_t*)st);
+  else if (q)
+    quant_kernel<true, false><<<grid, kThreads, 0, stm>>>((const uint16_t*)x, rows, ld_x, (uint8_t*)q, cols,
+                                                          (uint8_t*)s, cols / 128, 0, nullptr, nullptr);
+  else
+    quant_kernel<false, true><<<grid, kThreads, 0, stm>>>((const uint16_t*)x, rows, ld_x, nullptr, 0, nullptr, 0,
+                                                          0, (uint8_t*)qt, (uint8_t*)st);
+  MX_CHECK_LAUNCH("mxfp8_quant_dual");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const void* s,
+                             int64_t s_col_tiles, float* out, void* stream) {
+  MX_CHECK_ARG(q && s && out, "mxfp8_dequant: null pointer");
+  MX_CHECK_ARG(rows >= 0 && cols > 0 && cols % 128 == 0 && ld_q >= cols && ld_q % 4 == 0,
+               "mxfp8_dequant: bad shape");
+  MX_CHECK_ARG(s_col_tiles >= cols / 128, "mxfp8_dequant: bad s_col_tiles");
+  MX_CHECK_ARG(mx_aligned(q, 4) && mx_aligned(out, 16), "mxfp8_dequant: misaligned buffer");
+  if (rows == 0) return MXFP8_OK;
+  const int64_t n4 = rows * cols / 4;
+  const int64_t blocks = (n4 + kThreads - 1) / kThreads;
+  MX_CHECK_ARG(blocks <= 0x7fffffff, "mxfp8_dequant: too large");
+  dequant_kernel<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>((const uint8_t*)q, rows, cols, ld_q,
+                                                                         (const uint8_t*)s, s_col_tiles, out);
+  MX_CHECK_LAUNCH("mxfp8_dequant");
+  return MXFP8_OK;
+}

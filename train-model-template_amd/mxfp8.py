@@ -1,0 +1,247 @@
+"""MXFP8 GEMMs (E4M3 codes, one E8M0 scale per 32 elements) for the FROZEN weights of LoRA layers, on MI355X.
+
+Drop-in for /root/reference/scripts/mxfp8.py: same names, arguments, return types and layouts.  Every
+quantization and MX GEMM runs in the hand-written gfx950 kernels of libmxfp8_mlp.so (see _native.py); there is
+no CPU or Triton path, and a CPU tensor is an error.
+
+Layouts (identical to the reference's cuBLAS-compatible ones):
+  codes   float8_e4m3fn, row-major, quantized along the last dimension in blocks of 32;
+  scales  float8_e8m0fnu, flat, 128x4 blocked: byte of (row i, block b) at
+          ((i // 128) * (C // 128) + b // 4) * 512 + (i % 32) * 16 + ((i % 128) // 32) * 4 + b % 4,
+          padded rows (up to a multiple of 128) hold 0.
+
+gate_proj + up_proj of one MLP share one quantized copy W_gu = [W_gate; W_up] [2N, K] and its transposed copy
+W_guᵀ [K, 2N] (fused_mlp.py runs one forward GEMM and one K = 2N dgrad GEMM).  32-blocks never straddle the
+gate/up boundary, so codes and scales equal those of separate copies byte for byte (mxfp8.py:20-23).
+"""
+import os
+import types
+import weakref
+
+import torch
+
+import _native
+
+F8, E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
+STATS = {"quant": 0, "reuse": 0}  # how often an activation was quantized / reused (for checks)
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def scale_numel(rows, cols):
+    """Bytes of the blocked scale buffer of a [rows, cols] operand (mxfp8.py:83-84)."""
+    return _cdiv(rows, 128) * (cols // 128) * 512
+
+
+def mx_quant(x2d):
+    """[R, K] contiguous bf16 (K % 128 == 0) -> (fp8 [R, K], flat e8m0 scales in the blocked layout).
+
+    Replaces the Triton _quant_kernel launch of mxfp8.py:78-86."""
+    R, K = x2d.shape
+    assert x2d.dtype == torch.bfloat16 and x2d.is_contiguous() and K % 128 == 0, (x2d.dtype, x2d.shape)
+    q = torch.empty((R, K), dtype=F8, device=x2d.device)
+    s = torch.empty(scale_numel(R, K), dtype=torch.uint8, device=x2d.device)
+    if R:
+        _native.quant_rows(x2d, q, s)
+    return q, s.view(E8)
+
+
+def quant_ref(x2d):
+    """Quantization of a frozen weight (mxfp8.py:40-43: torchao to_mx RCEIL + to_blocked).  Same arithmetic
+    and layout as mx_quant, which is what runs here."""
+    x = x2d.contiguous()
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    return mx_quant(x)
+
+
+def quant_both(w):
+    """One read of a bf16 weight [R, C] -> (q [R, C], s) along C and (qt [C, R], st) along R, i.e.
+    quant_ref(w) and quant_ref(w.t().contiguous()) of mxfp8.py:477-478 / :488-490 in one pass."""
+    w = w.contiguous()
+    R, C = w.shape
+    assert w.dtype == torch.bfloat16 and R % 128 == 0 and C % 128 == 0, (w.dtype, w.shape)
+    q = torch.empty((R, C), dtype=F8, device=w.device)
+    s = torch.empty(scale_numel(R, C), dtype=torch.uint8, device=w.device)
+    qt = torch.empty((C, R), dtype=F8, device=w.device)
+    st = torch.empty(scale_numel(C, R), dtype=torch.uint8, device=w.device)
+    _native.quant_dual(w, q, s, qt, st)
+    return q, s.view(E8), qt, st.view(E8)
+
+
+def dequant(q, s, shape):
+    """fp32 tensor of `shape` [R, C] = E4M3(q) · 2^(e - 127) (NaN where e = 0xFF).  The reference has no such
+    function; it dequantizes only inside torch._scaled_mm."""
+    R, C = shape
+    out = torch.empty((R, C), dtype=torch.float32, device=q.device)
+    if R:
+        _native.dequant(q, s, R, C, q.stride(0), C // 128, out)
+    return out
+
+
+def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0):
+    """bf16 [M, N] = MX(q [M, K]) · MX(wq [N, K])ᵀ, i.e. torch._scaled_mm(q, wq.t(), s, ws, out_dtype=bf16).
+    wq may be a row slice/stride view (row stride wq.stride(0)); optional rank-r epilogue
+    out = bf16(out + alpha · P · Qᵀ) with lora = (P [M, r], Q [N, r]) (the addmm_ after the GEMM)."""
+    M, K = q.shape
+    N = wq.shape[0]
+    assert wq.shape[1] == K and q.stride(1) == 1 and wq.stride(1) == 1, (q.shape, wq.shape)
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=q.device)
+    if M:
+        _native.gemm_nt(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, out, lora=lora, alpha=alpha)
+    return out
+
+
+# ---------------------------------------------------------------- generic MX linear (mxfp8.py:296-341)
+_last = [None, 0, None, None]  # (weakref tensor, _version, q, s) of the last quantized activation
+
+
+def _quant_act(x):
+    """Quantize the input of a linear layer, reusing the last result if x is the same live tensor at the
+    same version (qkv/z, q/k/v and gate/up share one input) (mxfp8.py:299-312)."""
+    if _last[0] is not None and _last[0]() is x and _last[1] == x._version:
+        STATS["reuse"] += 1
+        return _last[2], _last[3]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != torch.bfloat16 or not x2.is_contiguous():
+        x2 = x2.to(torch.bfloat16).contiguous()
+    q, s = mx_quant(x2)
+    STATS["quant"] += 1
+    _last[:] = [weakref.ref(x), x._version, q, s]
+    return q, s
+
+
+class _MXLinear(torch.autograd.Function):
+    """x @ Wᵀ of a frozen MX weight, backward dx = MX(dy) @ W (mxfp8.py:315-333)."""
+
+    @staticmethod
+    def forward(ctx, x, q, s, lin):
+        out = mx_mm(q, s, lin._mx_w, lin._mx_ws)
+        ctx.lin = lin
+        return out.view(*x.shape[:-1], out.shape[-1])
+
+    @staticmethod
+    def backward(ctx, dy):
+        lin = ctx.lin
+        n = dy.shape[-1]
+        dy2 = dy.reshape(-1, n)
+        if dy2.dtype != torch.bfloat16 or not dy2.is_contiguous():
+            dy2 = dy2.to(torch.bfloat16).contiguous()
+        q, s = mx_quant(dy2)
+        STATS["quant"] += 1
+        wt, wts = mx_wt(lin)
+        dx = mx_mm(q, s, wt, wts)
+        return dx.view(*dy.shape[:-1], dx.shape[-1]), None, None, None
+
+
+@torch.compiler.disable
+def _forward(self, x):
+    q, s = _quant_act(x)
+    return _MXLinear.apply(x, q, s, self)
+
+
+_NAMES = {"q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "in_proj_qkv", "in_proj_z",
+          "out_proj"}
+
+
+def _base_linears(model):
+    """Frozen base linears of the decoder layers (mxfp8.py:347-356)."""
+    for name, m in model.named_modules():
+        if not isinstance(m, torch.nn.Linear) or m.weight.requires_grad or ".layers." not in name:
+            continue
+        parts = name.split(".")
+        leaf = parts[-2] if parts[-1] == "base_layer" else parts[-1]
+        if leaf in _NAMES:
+            yield name, m
+
+
+def _leaf_parent(name):
+    parts = name.split(".")
+    if parts[-1] == "base_layer":
+        return parts[-2], ".".join(parts[:-2])
+    return parts[-1], ".".join(parts[:-1])
+
+
+def is_mx(lin):
+    return getattr(lin, "_mx_w", None) is not None
+
+
+def mx_wt(lin):
+    """(fp8 Wᵀ [K, N] as the B operand of dx = dy @ W, scales).  For a gate/up pair: a column view of W_guᵀ
+    (row stride 2N) plus that half's scale tiles cut out contiguously, made on first use and kept
+    (mxfp8.py:402-415)."""
+    gu = lin.__dict__.get("_mx_gu")
+    if gu is None:
+        return lin._mx_wt, lin._mx_wts
+    hold, i = gu
+    if hold.half_t[i] is None:
+        n, k = hold.n, hold.wt.shape[0]
+        s3 = hold.wts.view(torch.uint8).view(k // 128, 2 * n // 128, 512)
+        hold.half_t[i] = (hold.wt[:, i * n:(i + 1) * n],
+                          s3[:, i * (n // 128):(i + 1) * (n // 128)].reshape(-1).view(E8))
+    return hold.half_t[i]
+
+
+def wt_of(lin):
+    """(mat2, scale) of dy @ W in torch._scaled_mm form: mat2 = Wᵀ codes as an [N, K] column-major view
+    (mxfp8.py:418-426)."""
+    wt, s = mx_wt(lin)
+    return wt.t(), s
+
+
+FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
+
+
+def enable_mxfp8(model):
+    """Quantize every frozen base linear of the decoder layers along both axes, pair gate/up into one shared
+    copy, move the bf16 weights to host memory and patch forward (mxfp8.py:452-498).  Both axes of each weight
+    come from one read (quant_both)."""
+    lins = list(_base_linears(model))
+    fam = {}
+    for name, lin in lins:
+        assert lin.bias is None
+        w = lin.weight.data
+        assert w.is_cuda and w.shape[0] % 128 == 0 and w.shape[1] % 128 == 0, w.shape
+        leaf, parent = _leaf_parent(name)
+        fam.setdefault(parent, {})[leaf] = lin
+    paired = set()
+    for d in fam.values():
+        gb, ub = d.get("gate_proj"), d.get("up_proj")
+        if FUSE_GU and gb is not None and ub is not None and gb.weight.shape == ub.weight.shape:
+            w = torch.cat([gb.weight.data, ub.weight.data]).to(torch.bfloat16)  # [2N, K]
+            n = gb.weight.shape[0]
+            hold = types.SimpleNamespace(n=n, half_t=[None, None])
+            hold.w, hold.ws, hold.wt, hold.wts = quant_both(w)
+            del w
+            ns = hold.ws.numel() // 2  # forward scales are ordered by tile row: first half = gate
+            for i, lin in enumerate((gb, ub)):
+                lin._mx_w, lin._mx_ws = hold.w[i * n:(i + 1) * n], hold.ws[i * ns:(i + 1) * ns]
+                lin._mx_gu = (hold, i)
+                paired.add(id(lin))
+    for name, lin in lins:
+        w = lin.weight.data
+        if id(lin) not in paired:
+            lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(w.to(torch.bfloat16))
+        lin._mx_fbwd = False  # the grouped LoRA backward of the non-MLP linears is not part of this library
+        lin._bf16_cpu = w.to("cpu", copy=True)
+        lin.weight.data = torch.empty((0,), dtype=w.dtype, device=w.device)
+        lin.forward = types.MethodType(_forward, lin)
+    torch.cuda.empty_cache()
+    print(f"MXFP8: {len(lins)} frozen linears on MX GEMMs (bf16 weights moved to host memory;"
+          f" {len(paired) // 2} gate/up pairs shared)", flush=True)
+    return len(lins)
+
+
+def disable_mxfp8(model):
+    """Restore the bf16 weights and the original forward (mxfp8.py:501-509)."""
+    for _, lin in _base_linears(model):
+        if hasattr(lin, "_bf16_cpu"):
+            lin.weight.data = lin._bf16_cpu.to(lin.weight.device)
+            for a in ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_cat", "_mx_gu", "_mx_fbwd", "_bf16_cpu", "forward"):
+                if a in lin.__dict__:
+                    delattr(lin, a)
+    _last[:] = [None, 0, None, None]
+    torch.cuda.empty_cache()

@@ -1,0 +1,142 @@
+"""Seeded synthetic inputs for the five benchmark/parity configurations of the MXFP8 SwiGLU-MLP path.
+
+Every tensor is drawn on the CPU from its own ``torch.Generator`` (seed = 1000 * config + 100 * layer + index)
+in fp32 and rounded to bf16 (RNE) where the path takes bf16, so the same bits can be copied to the GPU.
+LoRA A/B stay fp32, as PEFT keeps them (the path casts them to bf16 once per step).
+
+Config 5 ("outliers") draws x and dy from a Student-t(3) with NumPy's PCG64, scales 0.1% of the channels by
+100 and injects blocks that exercise the E8M0 scale choice, the +-448 saturation boundary and E4M3 RNE ties.
+
+"N(0, 1e-2)" for the upstream gradient is read as standard deviation 1e-2.
+"""
+import numpy as np
+import torch
+
+CONFIGS = {
+    1: dict(name="c1", T=256, K=1024, N=3584, r=16, alpha=32, backward=False, layers=1),
+    2: dict(name="c2", T=4096, K=1024, N=3584, r=16, alpha=32, backward=True, layers=1),
+    3: dict(name="c3", T=10752, K=2048, N=6144, r=16, alpha=32, backward=True, layers=1),
+    4: dict(name="c4", T=142336, K=2048, N=6144, r=16, alpha=32, backward=True, layers=24),
+    5: dict(name="c5", T=10752, K=2048, N=6144, r=16, alpha=32, backward=True, layers=1, outliers=True),
+}
+DESCRIPTIONS = {
+    1: "MXFP8 SwiGLU MLP fwd, M=256 d_model=1024 d_ffn=3584, LoRA r16 a32",
+    2: "Qwen3.5-0.8B-shaped MLP fwd+bwd, M=4096 d_model=1024 d_ffn=3584, LoRA r16 a32",
+    3: "Qwen3.5-2B-shaped MLP fwd+bwd, M=10752 d_model=2048 d_ffn=6144, LoRA r16 a32",
+    4: "24-layer stack of Qwen3.5-2B-shaped MLPs fwd+bwd, M=142336 (16x8896) d_model=2048 d_ffn=6144, LoRA r16",
+    5: "outlier stress fwd+bwd, M=10752 d_model=2048 d_ffn=6144, Student-t(3) + injected MX edge blocks",
+}
+# tensor index in the seed table
+_IDX = dict(x=0, Wg=1, Wu=2, Wd=3, Ag=4, Bg=5, Au=6, Bu=7, Ad=8, Bd=9, dy=10)
+
+
+def seed_of(cfg, name, layer=0):
+    return 1000 * cfg + 100 * layer + _IDX[name]
+
+
+def _normal(shape, std, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32) * std
+
+
+def flops(T, K, N, backward=True):
+    """Algorithmic MX GEMM work: forward 6·T·K·N (gate|up 4TKN + down 2TKN), backward 6·T·K·N (dh 2TKN + dx
+    4TKN).  The frozen base weights have no weight gradient; LoRA bf16 flops are not counted."""
+    return (12 if backward else 6) * T * K * N
+
+
+def quant_bytes(rows, cols, dual=False):
+    """Algorithmic HBM bytes of one MX quantization of a bf16 [rows, cols] tensor: read 2 B, write a 1 B code
+    and one scale byte per 32 elements (blocked tiles, padded rows included); the dual-axis variant writes
+    codes and scales for both axes."""
+    s = -(-rows // 128) * (cols // 128) * 512
+    if not dual:
+        return rows * cols * 3 + s
+    st = -(-cols // 128) * (rows // 128) * 512
+    return rows * cols * 4 + s + st
+
+
+def _outlier_blocks(x, rng):
+    """Inject MX edge cases into a bf16-valued fp32 [T, C] tensor in place (config 5)."""
+    T, C = x.shape
+    nb = C // 32
+    # 0.1% of channels scaled x100 (round(0.001 * C) channels)
+    nch = max(1, round(0.001 * C))
+    ch = rng.choice(C, size=nch, replace=False)
+    x[:, ch] *= 100.0
+    rows = rng.permutation(T)
+    k = 0
+
+    def take(n):
+        nonlocal k
+        r = rows[k:k + n]
+        k += n
+        return r
+
+    # all-zero blocks (+0.0) and -0.0 blocks
+    for r in take(64):
+        b = rng.integers(nb)
+        x[r, 32 * b:32 * b + 32] = 0.0
+    for r in take(16):
+        b = rng.integers(nb)
+        x[r, 32 * b:32 * b + 32] = -0.0
+    # amax exactly +-448 * 2^k for k in [-20, 20]: the block max lands on the top code 0x7E / 0xFE
+    for kk in range(-20, 21):
+        for r in take(2):
+            b = rng.integers(nb)
+            blk = x[r, 32 * b:32 * b + 32]
+            m = np.abs(blk).max()
+            if m > 0:
+                blk *= (224.0 * 2.0 ** kk) / m  # keep every other element below the boundary
+            j = rng.integers(32)
+            blk[j] = (448.0 if rng.random() < 0.5 else -448.0) * 2.0 ** kk
+    # E4M3 RNE midpoints after scaling: amax 448·2^k fixes the scale to 2^k, then values m·2^k with m a tie
+    ties = np.array([17.0, 19.0, 2.0 ** -10, 3 * 2.0 ** -10, 9.5, 10.5, 100.0, 116.0, 232.0, 432.0, 0.53125,
+                     0.59375])
+    for kk in (-6, 0, 3):
+        for r in take(8):
+            b = rng.integers(nb)
+            blk = x[r, 32 * b:32 * b + 32]
+            vals = rng.choice(ties, size=32) * np.where(rng.random(32) < 0.5, -1.0, 1.0)
+            vals[0] = 448.0
+            blk[:] = vals * 2.0 ** kk
+    return x
+
+
+def _student_t(shape, seed, scale=1.0):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = rng.standard_t(3.0, size=shape).astype(np.float32) * scale
+    return x, rng
+
+
+def make_inputs(cfg, T=None, layer=0, dy=True):
+    """CPU tensors for one layer of configuration ``cfg`` (1..5).  ``T`` overrides the token count (row
+    subsets of the same shape).  Returns dict(x, Wg, Wu, Wd, Ag, Bg, Au, Bu, Ad, Bd, dy, s, T, K, N, r)."""
+    c = CONFIGS[cfg]
+    T = c["T"] if T is None else T
+    K, N, r = c["K"], c["N"], c["r"]
+    s = c["alpha"] / r
+    out = dict(T=T, K=K, N=N, r=r, s=s)
+    if c.get("outliers"):
+        xf, rng = _student_t((T, K), seed_of(cfg, "x", layer))
+        xf = torch.from_numpy(_outlier_blocks(xf, rng))
+    else:
+        xf = _normal((T, K), 1.0, seed_of(cfg, "x", layer))
+    out["x"] = xf.to(torch.bfloat16)
+    out["Wg"] = _normal((N, K), 0.02, seed_of(cfg, "Wg", layer)).to(torch.bfloat16)
+    out["Wu"] = _normal((N, K), 0.02, seed_of(cfg, "Wu", layer)).to(torch.bfloat16)
+    out["Wd"] = _normal((K, N), 0.02, seed_of(cfg, "Wd", layer)).to(torch.bfloat16)
+    out["Ag"] = _normal((r, K), 0.02, seed_of(cfg, "Ag", layer))
+    out["Bg"] = _normal((N, r), 0.02, seed_of(cfg, "Bg", layer))
+    out["Au"] = _normal((r, K), 0.02, seed_of(cfg, "Au", layer))
+    out["Bu"] = _normal((N, r), 0.02, seed_of(cfg, "Bu", layer))
+    out["Ad"] = _normal((r, N), 0.02, seed_of(cfg, "Ad", layer))
+    out["Bd"] = _normal((K, r), 0.02, seed_of(cfg, "Bd", layer))
+    if dy:
+        if c.get("outliers"):
+            dyf, rng = _student_t((T, K), seed_of(cfg, "dy", layer), 1e-2)
+            dyf = torch.from_numpy(_outlier_blocks(dyf, rng))
+        else:
+            dyf = _normal((T, K), 1e-2, seed_of(cfg, "dy", layer))
+        out["dy"] = dyf.to(torch.bfloat16)
+    return out
