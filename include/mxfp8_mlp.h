@@ -71,12 +71,53 @@ int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
  * Replaces torch._scaled_mm(A, B.t(), sA, sB, out_dtype=bf16) (/root/reference/scripts/fused_mlp.py:279,
  * :283, :309, :329).
  * Optional rank-r epilogue (lora_p != NULL), replacing the addmm_ that follows (fused_mlp.py:284, :331):
- *   C = bf16( bf16(A·Bᵀ) + alpha * P[M, r] · Q[N, r]ᵀ ),  P, Q bf16 with row strides ld_p, ld_q, r in {16, 32}.
+ *   C = bf16( bf16(A·Bᵀ) + alpha * P[M, r] · Q[N, r]ᵀ ),  P, Q bf16 with row strides ld_p, ld_q,
+ *   r in {16, 32, 64}.
  * Requires K % 128 == 0, N % 128 == 0, lda/ldb % 16 == 0, ldc % 4 == 0.
  */
 int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
                   int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
                   const void* lora_q, int64_t ld_q, int64_t r, float alpha, void* stream);
+
+/*
+ * Fused SwiGLU forward of the MLP after the gate|up MX GEMM (replaces _fwd_kernel / mlp_fwd,
+ * /root/reference/scripts/fused_mlp.py:81-109, :198-215):
+ *   gu [T, 2N] bf16 (gate | up), xs [T, 2r] bf16 (xa_gate | xa_up), bg, bu [N, r] bf16, ad [r, N] bf16
+ *   g = bf16(gu[:, j] + s_g xs_g·bgᵀ), u = bf16(gu[:, N+j] + s_u xs_u·buᵀ), h = bf16(g / (exp(-g) + 1) * u)
+ *   q_h [T, N] + s_h (blocked, N/128 tiles per row, padded rows 0)   = MX(h)       (skipped if q_h == NULL)
+ *   part [n_groups, T, r] fp32: xS_down partial sums h·adᵀ over the columns of each of n_groups groups
+ *   h_out [T, N] bf16 (optional, may be NULL): h itself, for checks
+ * Requires N % 128 == 0, (N / 32) % n_groups == 0, r in {16, 32}, T * 2N < 2^31.
+ */
+int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu, const void* ad, int64_t T,
+                  int64_t N, int64_t r, float s_g, float s_u, void* q_h, void* s_h, float* part, int64_t n_groups,
+                  void* h_out, void* stream);
+
+/*
+ * Fused SwiGLU backward (replaces _bwd_kernel / mlp_bwd, /root/reference/scripts/fused_mlp.py:112-175,
+ * :218-259).  Inputs as in the forward plus dhm [T, N] bf16 (MX(dy)·W_down), dxd [T, r] bf16 (s_d·dy·B_d) and
+ * the small transposed copies xsT [2r, Tpad], dxdT [r, Tpad] (zero past T; Tpad = ceil(T/128)*128),
+ * bgT, buT [r, N], adT [N, r].  Grid: super-blocks of SB rows (SB % 128 == 0) x column groups of CG columns
+ * (CG % 256 == 0, N % CG == 0).  Outputs:
+ *   q [T, 2N] + s (2N/128 tiles per row): MX(dg) in columns 0..N-1, MX(du) in N..2N-1  (skipped if q == NULL)
+ *   dxa_part [N/CG, T, 3r] fp32: dxa_g | dxa_u | xS_down partial sums over each column group (unscaled)
+ *   dbg_part, dbu_part [ceil(Tpad/SB), N, r] fp32 and dad_part [ceil(Tpad/SB), r, N]: per super-block sums of
+ *     dgᵀ·xs_g, duᵀ·xs_u and (hᵀ·dxd)ᵀ (unscaled)
+ *   dgu_out [T, 2N] bf16 (optional, may be NULL): dg | du themselves, for checks
+ */
+int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, const void* dhm, const void* dxd,
+                  const void* dxdT, const void* bg, const void* bu, const void* bgT, const void* buT, const void* ad,
+                  const void* adT, int64_t T, int64_t N, int64_t r, float s_g, float s_u, int64_t SB, int64_t CG,
+                  void* q, void* s, float* dxa_part, float* dbg_part, float* dbu_part, float* dad_part,
+                  void* dgu_out, void* stream);
+
+/*
+ * out[i] = scale * Σ_{p=0..n_parts-1} part[p * count + i], summed in ascending p (deterministic), stored as
+ * fp32 or, if out_bf16, rounded to bf16 (RNE).  Replaces the partial-sum reductions part.sum(0) of
+ * /root/reference/scripts/fused_mlp.py:214, :258.
+ */
+int mxfp8_sum_parts(const float* part, int64_t n_parts, int64_t count, float scale, void* out, int out_bf16,
+                    void* stream);
 
 #ifdef __cplusplus
 }

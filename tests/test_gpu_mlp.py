@@ -1,0 +1,197 @@
+"""GPU parity of the fused MXFP8 SwiGLU MLP (fused_mlp.mlp / _MLP on libmxfp8_mlp.so) against the CPU oracle.
+
+Bars (north star):
+  - quantized codes and scales bit-exact: x and dy directly; h and dg|du given the same bf16 values (the GPU's
+    own h / dg / du are quantized by the oracle and compared byte for byte);
+  - h, dg, du themselves within one bf16 ulp of the oracle on identical inputs (they differ only by fp32
+    summation order of the rank-r products and exp/division ulps);
+  - GEMM/MLP outputs and LoRA gradients: max|Δ| / max|ref| <= 2e-2 against the oracle's dequantize-then-
+    matmul path (TOL below)."""
+import pytest
+import torch
+
+import fused_linear
+import fused_mlp
+import mxfp8
+import workloads
+from oracle import mlp as omlp
+from oracle import mx
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _rel(got, ref):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    return ((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+def _ulp_ok(got, ref):
+    """bf16 tensors computed from identical inputs: g and u can land one ulp apart when the fp32 rank-r LoRA sum
+    (different summation order) sits on a bf16 rounding boundary, and silu / its derivative amplify that into
+    a few ulps of h, dg, du.  Bar: at most 1e-4 of the elements differ by more than one bf16 ulp and none by
+    more than 2^-4 relative (plus 2^-20 of max|ref| absolute).  Returns the fraction of inexact elements."""
+    got, ref = got.float().cpu(), ref.float().cpu()
+    d = (got - ref).abs()
+    mag = torch.maximum(got.abs(), ref.abs())
+    ulp = torch.exp2(torch.floor(torch.log2(mag.clamp_min(2.0 ** -126))) - 7)
+    beyond = (d > ulp).float().mean().item()
+    assert beyond <= 1e-4, beyond
+    assert bool((d <= 2.0 ** -4 * mag + 2.0 ** -20 * ref.abs().max()).all()), d.max().item()
+    return (got != ref).float().mean().item()
+
+
+def _oracle_all(inp, backward=True):
+    W = omlp.prepare_weights(inp["Wg"], inp["Wu"], inp["Wd"])
+    S, bg, bu, ad, bd = omlp.lora_cast(inp["Ag"], inp["Bg"], inp["Au"], inp["Bu"], inp["Ad"], inp["Bd"])
+    s = inp["s"]
+    f = omlp.forward(inp["x"], W, S, bg, bu, ad, bd, s, s, s)
+    b = omlp.backward(inp["x"], f["xs"], f["gu"], W, S, bg, bu, ad, bd, s, s, s, inp["dy"]) if backward else None
+    return W, (S, bg, bu, ad, bd), f, b
+
+
+def _run_model(cfg, T, gpu, backward=True, need_out=True):
+    model, inps = workloads.build_model(cfg, T=T, device=gpu)
+    mxfp8.enable_mxfp8(model)
+    fused_linear.new_step()
+    inp = inps[0]
+    mod = model.layers[0].mlp
+    x = inp["x"].to(gpu).requires_grad_(backward)
+    y = fused_mlp.mlp(mod, x, need_out)
+    assert y is not None
+    out = dict(y=y.detach())
+    if backward:
+        y.backward(inp["dy"].to(gpu))
+        out.update(dx=x.grad, dA_g=mod.gate_proj.lora_A["default"].weight.grad,
+                   dB_g=mod.gate_proj.lora_B["default"].weight.grad,
+                   dA_u=mod.up_proj.lora_A["default"].weight.grad, dB_u=mod.up_proj.lora_B["default"].weight.grad,
+                   dA_d=mod.down_proj.lora_A["default"].weight.grad,
+                   dB_d=mod.down_proj.lora_B["default"].weight.grad)
+    return model, inp, out
+
+
+def _check_e2e(out, ref_f, ref_b):
+    errs = {"y": _rel(out["y"], ref_f["y"])}
+    if ref_b is not None:
+        for k in ("dx", "dA_g", "dB_g", "dA_u", "dB_u", "dA_d", "dB_d"):
+            errs[k] = _rel(out[k], ref_b[k])
+    print(" ".join(f"{k}={v:.2e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if not v <= TOL}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("cfg,T", [(1, None), (2, 1024), (2, 300), (3, 512), (5, 1024)])
+def test_mlp_end_to_end(cfg, T, gpu):
+    bwd = workloads.CONFIGS[cfg]["backward"]
+    print(f"config {cfg} T={T}", flush=True)
+    _, inp, out = _run_model(cfg, T, gpu, backward=bwd)
+    _, _, f, b = _oracle_all(inp, backward=bwd)
+    _check_e2e(out, f, b)
+
+
+def test_mlp_end_to_end_config2_full(gpu):
+    _, inp, out = _run_model(2, None, gpu)
+    _, _, f, b = _oracle_all(inp)
+    _check_e2e(out, f, b)
+
+
+def _kernel_inputs(cfg, T, gpu):
+    inp = workloads.make_inputs(cfg, T=T)
+    W, (S, bg, bu, ad, bd), f, b = _oracle_all(inp)
+    g = lambda t: t.to(gpu).contiguous()  # noqa: E731
+    return inp, W, (S, bg, bu, ad, bd), f, b, g
+
+
+@pytest.mark.parametrize("cfg,T", [(2, 512), (3, 300), (5, 1024)])
+def test_fwd_kernel_elementwise_and_codes(cfg, T, gpu):
+    inp, W, (S, bg, bu, ad, bd), f, b, g = _kernel_inputs(cfg, T, gpu)
+    N, s = inp["N"], inp["s"]
+    h = torch.empty(T, N, dtype=torch.bfloat16, device=gpu)
+    qh, sh, xsd = fused_mlp.mlp_fwd(g(f["gu"]), g(f["xs"]), g(bg), g(bu), g(ad), s, s, True, h_out=h)
+    frac = _ulp_ok(h, f["h"])
+    print(f"h: {frac:.2e} of elements differ by one ulp", flush=True)
+    assert frac < 1e-3
+    # codes and scales of h bit-exact given the same bf16 h
+    qr, sr = mx.quant(h.cpu())
+    assert torch.equal(qh.view(torch.uint8).cpu(), qr) and torch.equal(sh.view(torch.uint8).cpu(), sr)
+    # xS_down = bf16(h · adᵀ) from the GPU's own h
+    ref = (h.cpu().double() @ ad.double().t())
+    assert _rel(xsd, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("cfg,T", [(2, 512), (3, 300), (5, 1024)])
+def test_bwd_kernel_elementwise_and_codes(cfg, T, gpu):
+    inp, W, (S, bg, bu, ad, bd), f, b, g = _kernel_inputs(cfg, T, gpu)
+    N, R, s = inp["N"], inp["r"], inp["s"]
+    dgu = torch.empty(T, 2 * N, dtype=torch.bfloat16, device=gpu)
+    q, sc, dxa, dbg, dbu, dad = fused_mlp.mlp_bwd(g(f["gu"]), g(f["xs"]), g(b["dhm"]), g(b["dxd"]), g(bg), g(bu),
+                                                  g(ad), s, s, True, dgu_out=dgu)
+    fg = _ulp_ok(dgu[:, :N], b["dg"])
+    fu = _ulp_ok(dgu[:, N:], b["du"])
+    print(f"dg: {fg:.2e}, du: {fu:.2e} of elements differ by one ulp", flush=True)
+    assert fg < 1e-2 and fu < 1e-2
+    qr, sr = mx.quant(dgu.cpu())
+    assert torch.equal(q.view(torch.uint8).cpu(), qr) and torch.equal(sc.view(torch.uint8).cpu(), sr)
+    # partial-sum products from the GPU's own dg / du and the oracle's h, in float64
+    dg64, du64 = dgu[:, :N].cpu().double(), dgu[:, N:].cpu().double()
+    h64 = b["h"].double()
+    xs64, dxd64 = f["xs"].double(), b["dxd"].double()
+    assert _rel(dxa[:, :R], dg64 @ bg.double()) <= 1e-2
+    assert _rel(dxa[:, R:2 * R], du64 @ bu.double()) <= 1e-2
+    assert _rel(dxa[:, 2 * R:], h64 @ ad.double().t()) <= 1e-2
+    assert _rel(dbg, dg64.t() @ xs64[:, :R]) <= 1e-2
+    assert _rel(dbu, du64.t() @ xs64[:, R:]) <= 1e-2
+    assert _rel(dad, (h64.t() @ dxd64).t()) <= 1e-2
+    # and against the oracle's own unscaled partials
+    assert _rel(dxa, b["dxa_raw"]) <= TOL and _rel(dbg, b["dBg_raw"]) <= TOL and _rel(dad, b["dAd"]) <= TOL
+
+
+def test_need_out_false_saves_same_and_backward_matches(gpu):
+    # checkpoint recompute: need_out=False leaves the saved set and therefore every gradient unchanged
+    _, _, out1 = _run_model(2, 384, gpu, need_out=True)
+    _, _, out2 = _run_model(2, 384, gpu, need_out=False)
+    for k in ("dx", "dA_g", "dB_g", "dA_u", "dB_u", "dA_d", "dB_d"):
+        assert torch.equal(out1[k], out2[k]), k
+
+
+def test_deterministic(gpu):
+    _, _, o1 = _run_model(3, 640, gpu)
+    _, _, o2 = _run_model(3, 640, gpu)
+    for k, v in o1.items():
+        assert torch.equal(v, o2[k]), k
+
+
+def test_lora_b_zero_gives_zero_a_grads(gpu):
+    # with every LoRA B = 0: dA_g = dA_u = dA_d = 0 exactly, and y equals the plain MX SwiGLU of the oracle
+    model, inps = workloads.build_model(2, T=256, device=gpu)
+    mod = model.layers[0].mlp
+    with torch.no_grad():
+        for name in ("gate_proj", "up_proj", "down_proj"):
+            getattr(mod, name).lora_B["default"].weight.zero_()
+    mxfp8.enable_mxfp8(model)
+    fused_linear.new_step()
+    inp = inps[0]
+    x = inp["x"].to(gpu).requires_grad_(True)
+    y = fused_mlp.mlp(mod, x)
+    y.backward(inp["dy"].to(gpu))
+    for name in ("gate_proj", "up_proj", "down_proj"):
+        assert int(torch.count_nonzero(getattr(mod, name).lora_A["default"].weight.grad)) == 0
+    zero = {k: torch.zeros_like(inp[k]) for k in ("Bg", "Bu", "Bd")}
+    _, _, f, _ = _oracle_all({**inp, **zero}, backward=False)
+    assert _rel(y, f["y"]) <= TOL
+
+
+def test_mlp_gating_returns_none(gpu):
+    model, inps = workloads.build_model(1, T=64, device=gpu)
+    mod = model.layers[0].mlp
+    x = inps[0]["x"].to(gpu)
+    assert fused_mlp.mlp(mod, x) is None  # weights not prepared by enable_mxfp8
+    mxfp8.enable_mxfp8(model)
+    assert fused_mlp.mlp(mod, x.float()) is None  # not bf16
+    assert fused_mlp.mlp(mod, inps[0]["x"]) is None  # CPU tensor
+    fused_mlp.ENABLED[0] = False
+    try:
+        assert fused_mlp.mlp(mod, x) is None
+    finally:
+        fused_mlp.ENABLED[0] = True
+    assert fused_mlp.mlp(mod, x) is not None

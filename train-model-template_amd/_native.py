@@ -24,6 +24,10 @@ SIGNATURES = {
     "mxfp8_dequant": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr],
     "mxfp8_gemm_nt": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
                       _i64, _f32, _ptr],
+    "mxfp8_mlp_fwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _i64, _ptr, _ptr],
+    "mxfp8_mlp_bwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32,
+                      _f32, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
+    "mxfp8_sum_parts": [_ptr, _i64, _i64, _f32, _ptr, _int, _ptr],
 }
 
 _lib = None
@@ -108,3 +112,22 @@ def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0):
         ldp, ldq = p.stride(0), q.stride(0)
     call("mxfp8_gemm_nt", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(p), ldp,
          _p(q), ldq, r, float(alpha), like=c)
+
+
+def mlp_fwd(gu, xs, bg, bu, ad, T, N, r, s_g, s_u, q, s, part, n_groups, h_out=None):
+    call("mxfp8_mlp_fwd", _p(gu), _p(xs), _p(bg), _p(bu), _p(ad), T, N, r, float(s_g), float(s_u), _p(q), _p(s),
+         _p(part), n_groups, _p(h_out), like=gu)
+
+
+def mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, r, s_g, s_u, SB, CG, q, s, dxa_part,
+            dbg_part, dbu_part, dad_part, dgu_out=None):
+    call("mxfp8_mlp_bwd", _p(gu), _p(xs), _p(xsT), _p(dhm), _p(dxd), _p(dxdT), _p(bg), _p(bu), _p(bgT), _p(buT),
+         _p(ad), _p(adT), T, N, r, float(s_g), float(s_u), SB, CG, _p(q), _p(s), _p(dxa_part), _p(dbg_part),
+         _p(dbu_part), _p(dad_part), _p(dgu_out), like=gu)
+
+
+def sum_parts(part, n_parts, count, out, scale=1.0):
+    """out (fp32 or bf16, `count` elements) = scale * Σ_p part[p] in ascending p."""
+    assert out.dtype in (torch.float32, torch.bfloat16) and part.dtype == torch.float32
+    call("mxfp8_sum_parts", _p(part), n_parts, count, float(scale), _p(out), int(out.dtype == torch.bfloat16),
+         like=part)

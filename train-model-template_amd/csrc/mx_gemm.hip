@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const int m = m0 + wm * 64 + mt * 32 + (lane & 31);
-    v8bf pf[2];
+    v8bf pf[kR > 0 ? kR / 16 : 1];
     if constexpr (kR > 0) {
       const int mc = min(m, M - 1);
 #pragma unroll
@@ -228,7 +228,7 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
                    mx_aligned(c, 8),
                "mxfp8_gemm_nt: misaligned buffer");
   if (lora_p) {
-    MX_CHECK_ARG(lora_q && (r == 16 || r == 32), "mxfp8_gemm_nt: epilogue needs P, Q and r in {16, 32}");
+    MX_CHECK_ARG(lora_q && (r == 16 || r == 32 || r == 64), "mxfp8_gemm_nt: epilogue needs P, Q and r in {16, 32, 64}");
     MX_CHECK_ARG(ld_p >= r && ld_q >= r && ld_p % 8 == 0 && ld_q % 8 == 0 && mx_aligned(lora_p, 16) &&
                      mx_aligned(lora_q, 16),
                  "mxfp8_gemm_nt: bad epilogue strides/alignment");
@@ -242,8 +242,10 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
     gemm_kernel<0><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
   else if (r == 16)
     gemm_kernel<16><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
-  else
+  else if (r == 32)
     gemm_kernel<32><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+  else
+    gemm_kernel<64><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
   MX_CHECK_LAUNCH("mxfp8_gemm_nt");
   return MXFP8_OK;
 }

@@ -1,0 +1,236 @@
+"""Fused MXFP8 SwiGLU MLP with LoRA on gate/up/down in one autograd.Function, on MI355X (gfx950).
+
+Drop-in for /root/reference/scripts/fused_mlp.py: same module names (ENABLED, ACTIVE, SAVED_LESS, mlp, _MLP,
+mlp_fwd, mlp_bwd), same saved-tensor set, same return dtypes and the same None fallback contract of mlp().
+
+  forward : xs = x·[A_g; A_u]ᵀ (bf16) -> MX(x) -> MX GEMM gate|up (W_gu [2N, K]) -> fused kernel reading gu
+            once: LoRA-B of gate and up, bf16 rounding, h = silu(g)·u, MX(h) and the xS_down partials ->
+            MX GEMM down with the LoRA epilogue y = bf16(y + s_d · xS_down · B_dᵀ) inside the GEMM.
+            h is not stored (backward recomputes it from gu).
+  backward: MX(dy) -> MX GEMM dh = dy·W_down -> fused kernel reading gu and dh once: recompute g, u, h;
+            dh += dxd·A_d; SwiGLU backward; MX(dg | du) into one [T, 2N] buffer; dxa, dB, dA_d partials ->
+            one K = 2N MX GEMM dx = [dg | du]·W_gu with the LoRA epilogue dx = bf16(dx + dxa·S).
+  need_out=False (checkpoint recompute): only xs, MX(x) and the gate|up GEMM run (fused_mlp.py:286-288).
+The heavy kernels are hand-written HIP (libmxfp8_mlp.so, _native.py); the rank-r LoRA products that are plain
+skinny GEMMs (xs, dxd, dB_d, dA) use PyTorch's bf16 GEMM on the same stream.
+"""
+import torch
+
+import _native
+import mxfp8
+from fused_linear import STATS, _cast, _part
+
+_F8, _E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
+ENABLED = [True]  # set False to compare against the unfused path in the same process
+ACTIVE = [False]  # the fused path ran at least once (read by the step engine to shrink per-layer activations)
+SAVED_LESS = 12288  # bytes per token per layer not saved compared with the unfused path (h [T, 6144] bf16)
+
+_CUS = [None]
+LAST = {}  # launch parameters of the last fused kernels (for inspection)
+
+
+def _n_cu():
+    if _CUS[0] is None:
+        _CUS[0] = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    return _CUS[0]
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _divisors(n):
+    return [d for d in range(1, n + 1) if n % d == 0]
+
+
+def _fwd_groups(T, N):
+    """Column groups of the forward kernel: the fewest (smallest partial buffer) that still give >= 4
+    workgroups per CU, each group keeping at least 4 column tiles (one per wave)."""
+    nt = N // 32
+    nrb = _cdiv(T, 128) * 4
+    ok = [d for d in _divisors(nt) if nt // d >= 4] or [1]
+    return next((d for d in ok if nrb * d >= 4 * _n_cu()), ok[-1])
+
+
+def _bwd_grid(T, N, R):
+    """(SB, CG) of the backward kernel: the fewest partial-sum bytes (per super-block dB/dA partials plus per
+    column-group dxa partials, as in fused_mlp.py:218-232) with at least 2 workgroups per CU."""
+    tpad = _cdiv(T, 128) * 128
+    best = None
+    for cg in [256 * d for d in _divisors(N // 256)]:
+        ncg = N // cg
+        for sb in range(128, tpad + 128, 128):
+            nsb = _cdiv(tpad, sb)
+            if nsb * ncg < 2 * _n_cu() and not (sb == 128 and cg == 256):
+                continue
+            cost = nsb * N * R * 3 * 4 + ncg * T * 3 * R * 4
+            if best is None or cost < best[0]:
+                best = (cost, sb, cg)
+    return best[1], best[2]
+
+
+def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None):
+    """gu [T, 2N] bf16, xs [T, 2R] bf16 (xa_gate | xa_up), bg/bu [N, R], ad [R, N] bf16 -> (q_h, s_h, xS_down
+    bf16) (fused_mlp.py:198-215).  h_out (optional [T, N] bf16) receives h for checks."""
+    T, N2 = gu.shape
+    N, R = N2 // 2, ad.shape[0]
+    dev = gu.device
+    ng = _fwd_groups(T, N)
+    if write_q:
+        q = torch.empty((T, N), dtype=_F8, device=dev)
+        s = torch.empty(_cdiv(T, 128) * (N // 128) * 512, dtype=torch.uint8, device=dev)
+    else:
+        q = s = None
+    part = torch.empty((ng, T, R), dtype=torch.float32, device=dev)
+    LAST["fwd"] = dict(n_groups=ng)
+    _native.mlp_fwd(gu, xs, bg, bu, ad, T, N, R, s_g, s_u, q, s, part, ng, h_out)
+    xsd = torch.empty((T, R), dtype=torch.bfloat16, device=dev)
+    _native.sum_parts(part, ng, T * R, xsd)
+    return (q, s.view(_E8), xsd) if write_q else (None, None, xsd)
+
+
+def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None):
+    """-> (q_dgu [T, 2N] fp8, s_dgu, [dxa_gate | dxa_up | xS_down] [T, 3R] fp32 (dxa not yet scaled by s),
+    dBg, dBu [N, R] fp32 (not scaled), dAd [R, N] fp32) (fused_mlp.py:235-259)."""
+    T, N2 = gu.shape
+    N, R = N2 // 2, ad.shape[0]
+    dev = gu.device
+    tpad = _cdiv(T, 128) * 128
+    SB, CG = _bwd_grid(T, N, R)
+    nsb, ncg = _cdiv(tpad, SB), N // CG
+    LAST["bwd"] = dict(SB=SB, CG=CG, nsb=nsb, ncg=ncg)
+    # small transposed copies the kernel reads as matrix-instruction operands
+    xsT = torch.zeros((2 * R, tpad), dtype=torch.bfloat16, device=dev)
+    xsT[:, :T] = xs.t()
+    dxdT = torch.zeros((R, tpad), dtype=torch.bfloat16, device=dev)
+    dxdT[:, :T] = dxd.t()
+    bgT, buT, adT = bg.t().contiguous(), bu.t().contiguous(), ad.t().contiguous()
+    if need_q:
+        q = torch.empty((T, N2), dtype=_F8, device=dev)
+        s = torch.empty(_cdiv(T, 128) * (N2 // 128) * 512, dtype=torch.uint8, device=dev)
+    else:
+        q = s = None
+    dxa_p = torch.empty((ncg, T, 3 * R), dtype=torch.float32, device=dev)
+    dbg_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
+    dbu_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
+    dad_p = torch.empty((nsb, R, N), dtype=torch.float32, device=dev)
+    _native.mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, R, s_g, s_u, SB, CG, q, s,
+                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out)
+    dxa = torch.empty((T, 3 * R), dtype=torch.float32, device=dev)
+    dbg = torch.empty((N, R), dtype=torch.float32, device=dev)
+    dbu = torch.empty((N, R), dtype=torch.float32, device=dev)
+    dad = torch.empty((R, N), dtype=torch.float32, device=dev)
+    _native.sum_parts(dxa_p, ncg, T * 3 * R, dxa)
+    _native.sum_parts(dbg_p, nsb, N * R, dbg)
+    _native.sum_parts(dbu_p, nsb, N * R, dbu)
+    _native.sum_parts(dad_p, nsb, R * N, dad)
+    return (q if need_q else None, s.view(_E8) if need_q else None, dxa, dbg, dbu, dad)
+
+
+class _MLP(torch.autograd.Function):
+    """fused_mlp.py:262-336."""
+
+    @staticmethod
+    def forward(ctx, x, meta, need_out, Ag, Bg, Au, Bu, Ad, Bd):
+        ctx.set_materialize_grads(False)
+        hold, down, (s_g, s_u, s_d), dt = meta
+        lead, K = x.shape[:-1], x.shape[-1]
+        x2 = x.reshape(-1, K)
+        if x2.dtype != dt or not x2.is_contiguous():
+            x2 = x2.to(dt).contiguous()
+        # same cache keys as the grouped linears so both paths share one bf16 copy per step
+        S = _cast(((id(Ag), id(Au)), dt), lambda: torch.cat([Ag.detach().to(dt), Au.detach().to(dt)]))
+        bg = _cast((id(Bg), dt), lambda: Bg.detach().to(dt))
+        bu = _cast((id(Bu), dt), lambda: Bu.detach().to(dt))
+        ad = _cast(((id(Ad),), dt), lambda: torch.cat([Ad.detach().to(dt)]))
+        bd = _cast((id(Bd), dt), lambda: Bd.detach().to(dt))
+        xs = x2 @ S.t()  # [T, 2R] = xa_gate | xa_up
+        q, sc = mxfp8.mx_quant(x2)
+        gu = mxfp8.mx_mm(q, sc, hold.w, hold.ws)  # [T, 2N] gate | up
+        del q, sc
+        if need_out:
+            qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True)
+            # y = bf16(bf16(MX(h)·W_downᵀ) + s_d · xS_down · B_dᵀ): the addmm_ of fused_mlp.py:284 in the epilogue
+            y = mxfp8.mx_mm(qh, sh, down._mx_w, down._mx_ws, lora=(xsd, bd), alpha=s_d)
+            del qh, sh, xsd
+        else:  # graph only (checkpoint recompute / prefix backward): nobody reads y
+            STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
+            y = x2.new_empty(x2.shape[0], down.out_features)
+        # the same saved set in both modes (non-reentrant checkpointing compares metadata on recompute)
+        ctx.save_for_backward(x2, xs, gu, S, bg, bu, ad, bd)
+        ctx.meta = (hold, down, (s_g, s_u, s_d), dt, lead, K, x.dtype)
+        return y.view(*lead, y.shape[-1])
+
+    @staticmethod
+    def backward(ctx, dy):
+        if dy is None:
+            return (None,) * 9
+        x2, xs, gu, S, bg, bu, ad, bd = ctx.saved_tensors
+        hold, down, (s_g, s_u, s_d), dt, lead, K, xdt = ctx.meta
+        need_x = ctx.needs_input_grad[0]
+        R = ad.shape[0]
+        dy2 = dy.reshape(-1, dy.shape[-1]).to(dt)
+        if not dy2.is_contiguous():
+            dy2 = dy2.contiguous()
+        qd, sd = mxfp8.mx_quant(dy2)
+        wt, wts = mxfp8.mx_wt(down)
+        dhm = mxfp8.mx_mm(qd, sd, wt, wts)  # [T, N] = MX(dy) · W_down
+        del qd, sd
+        dxd = dy2 @ bd
+        if s_d != 1:
+            dxd.mul_(s_d)
+        qg, sg, dxa, dB_g, dB_u, dA_d = mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_x)
+        del dhm
+        dB_d = dy2.t() @ dxa[:, 2 * R:].to(dt)  # xS_down in bf16, as the unfused path saved it
+        if s_d != 1:
+            dB_d.mul_(s_d)
+        dxa = dxa[:, :2 * R]
+        if s_g != 1:
+            dxa[:, :R].mul_(s_g)
+            dB_g.mul_(s_g)
+        if s_u != 1:
+            dxa[:, R:].mul_(s_u)
+            dB_u.mul_(s_u)
+        dxa = dxa.to(dt)  # [T, 2R] contiguous
+        dx = None
+        if need_x:
+            # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
+            # fused_mlp.py:331 in its epilogue
+            dx = mxfp8.mx_mm(qg, sg, hold.wt, hold.wts, lora=(dxa, S.t().contiguous()), alpha=1.0)
+            del qg, sg
+            dx = dx.view(*lead, K).to(xdt)
+        dA = dxa.t() @ x2
+        grads = [dA[:R], dB_g, dA[R:], dB_u, dA_d, dB_d]
+        ws_in = ctx.needs_input_grad[3:]
+        return (dx, None, None, *[g if ws_in[k] else None for k, g in enumerate(grads)])
+
+
+def _r_ok(r):
+    return r in (16, 32)
+
+
+def mlp(mlp_mod, x, need_out=True):
+    """down(silu(gate(x)) * up(x)) through _MLP when gate/up/down are PEFT LoRA layers over MX weights with gate
+    and up paired by mxfp8.enable_mxfp8, computing in bf16 on the GPU; otherwise None (the caller takes the
+    unfused path) (fused_mlp.py:343-366)."""
+    if not ENABLED[0]:
+        return None
+    parts = [_part(m) for m in (mlp_mod.gate_proj, mlp_mod.up_proj, mlp_mod.down_proj)]
+    if any(p is None or p[1] is None for p in parts):
+        return None
+    (gb, Ag, Bg, s_g), (ub, Au, Bu, s_u), (db, Ad, Bd, s_d) = parts
+    dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else x.dtype
+    if dt != torch.bfloat16 or not x.is_cuda:
+        return None
+    pg, pu = getattr(gb, "_mx_gu", None), getattr(ub, "_mx_gu", None)
+    if pg is None or pu is None or pg[0] is not pu[0] or (pg[1], pu[1]) != (0, 1) or not mxfp8.is_mx(db):
+        return None
+    hold = pg[0]
+    r = Ag.shape[0]
+    T = x.numel() // x.shape[-1]
+    if not (_r_ok(r) and Au.shape[0] == r and Ad.shape[0] == r and x.shape[-1] == hold.w.shape[1]
+            and hold.n % 256 == 0 and Ad.shape[1] == hold.n and T > 0 and T * 2 * hold.n < 2 ** 31):
+        return None  # (32-bit element indexing in the kernels; the backward kernel tiles N by 256)
+    STATS["mlp gộp"] = STATS.get("mlp gộp", 0) + 1
+    ACTIVE[0] = True
+    return _MLP.apply(x, (hold, db, (s_g, s_u, s_d), dt), need_out, Ag, Bg, Au, Bu, Ad, Bd)

@@ -140,3 +140,93 @@ def make_inputs(cfg, T=None, layer=0, dy=True):
             dyf = _normal((T, K), 1e-2, seed_of(cfg, "dy", layer))
         out["dy"] = dyf.to(torch.bfloat16)
     return out
+
+
+class LoraLinear(torch.nn.Module):
+    """The attribute surface of a PEFT LoRA Linear that fused_linear._part reads (base_layer, lora_A/B
+    ModuleDicts, scaling, active_adapters, lora_dropout, use_dora, merged, disable_adapters).  peft is not
+    installed here; this stands in for it so the drop-in API can be driven as the training script drives it."""
+
+    def __init__(self, base, A, B, alpha):
+        super().__init__()
+        r = A.shape[0]
+        self.base_layer = base
+        self.lora_A = torch.nn.ModuleDict({"default": torch.nn.Linear(A.shape[1], r, bias=False)})
+        self.lora_B = torch.nn.ModuleDict({"default": torch.nn.Linear(r, B.shape[0], bias=False)})
+        with torch.no_grad():
+            self.lora_A["default"].weight.copy_(A)
+            self.lora_B["default"].weight.copy_(B)
+        self.lora_dropout = torch.nn.ModuleDict({"default": torch.nn.Identity()})
+        self.scaling = {"default": alpha / r}
+        self.active_adapters = ["default"]
+        self.use_dora = {"default": False}
+        self.merged = False
+        self.disable_adapters = False
+
+    def forward(self, x):
+        a, b = self.lora_A["default"], self.lora_B["default"]
+        return self.base_layer(x) + self.scaling["default"] * b(a(x))
+
+
+class SwiGLUMLP(torch.nn.Module):
+    """gate_proj / up_proj / down_proj with a SiLU act_fn, the shape of a Qwen3.5 MLP."""
+
+    def __init__(self, inp, alpha):
+        super().__init__()
+        K, N = inp["K"], inp["N"]
+
+        def lin(w):
+            m = torch.nn.Linear(w.shape[1], w.shape[0], bias=False)
+            with torch.no_grad():
+                m.weight.copy_(w)
+            m.weight.requires_grad_(False)
+            return m
+
+        self.gate_proj = LoraLinear(lin(inp["Wg"]), inp["Ag"], inp["Bg"], alpha)
+        self.up_proj = LoraLinear(lin(inp["Wu"]), inp["Au"], inp["Bu"], alpha)
+        self.down_proj = LoraLinear(lin(inp["Wd"]), inp["Ad"], inp["Bd"], alpha)
+        self.act_fn = torch.nn.SiLU()
+
+    def forward(self, x):
+        return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+
+
+class _Layer(torch.nn.Module):
+    def __init__(self, mlp):
+        super().__init__()
+        self.mlp = mlp
+
+
+class _Decoder(torch.nn.Module):
+    def __init__(self, mlps):
+        super().__init__()
+        self.layers = torch.nn.ModuleList([_Layer(m) for m in mlps])
+
+
+class MLPStack(torch.nn.Module):
+    """model.layers[i].mlp, named like a Hugging Face decoder ('model.layers.<i>.mlp.gate_proj...'): the module
+    path mxfp8.enable_mxfp8 walks (names containing '.layers.')."""
+
+    def __init__(self, mlps):
+        super().__init__()
+        self.model = _Decoder(mlps)
+
+    @property
+    def layers(self):
+        return self.model.layers
+
+
+def build_model(cfg, T=None, layers=1, device="cuda"):
+    """(model, inputs) for `layers` independent seeded layers of configuration cfg, bf16 frozen weights and
+    fp32 LoRA parameters on `device`; inputs of layer 0 (x, dy) are returned on the CPU."""
+    c = CONFIGS[cfg]
+    mlps, inps = [], []
+    for layer in range(layers):
+        inp = make_inputs(cfg, T=T, layer=layer, dy=(layer == 0))
+        m = SwiGLUMLP(inp, c["alpha"])
+        for name in ("gate_proj", "up_proj", "down_proj"):
+            getattr(m, name).base_layer.to(dtype=torch.bfloat16)
+        mlps.append(m)
+        inps.append(inp)
+    model = MLPStack(mlps).to(device)
+    return model, inps
