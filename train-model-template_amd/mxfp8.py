@@ -81,6 +81,9 @@ def dequant(q, s, shape):
     return out
 
 
+GEMM_EVENTS = None  # set to a list to record (start event, end event, flops) around every MX GEMM launch
+
+
 def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0):
     """bf16 [M, N] = MX(q [M, K]) · MX(wq [N, K])ᵀ, i.e. torch._scaled_mm(q, wq.t(), s, ws, out_dtype=bf16).
     wq may be a row slice/stride view (row stride wq.stride(0)); optional rank-r epilogue
@@ -91,7 +94,14 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0):
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=q.device)
     if M:
+        ev = GEMM_EVENTS
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
         _native.gemm_nt(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, out, lora=lora, alpha=alpha)
+        if ev is not None:
+            e1.record()
+            ev.append((e0, e1, 2 * M * N * K))
     return out
 
 
