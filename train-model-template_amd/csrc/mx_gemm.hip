@@ -13,10 +13,11 @@
 // Operand staging: global memory goes straight into LDS with global_load_lds_dwordx4 (no VGPR round trip)
 // through a ring of 4 stages of 34 KB: A codes 256 x 64 B, B codes 256 x 64 B, and the two 128-row blocked
 // scale tiles of each operand for the current 128-wide K tile.  Every wave issues exactly five DMA
-// instructions per stage (four 1 KB code slices and one 256 B scale slice), so a fixed vmcnt bounds the wait
+// instructions per stage (four 1 KB code slices plus a scale tile or a duplicate), so a fixed vmcnt bounds the wait
 // for a stage while the next two stay in flight.  Lane i of a DMA lands at base + 16 i; a row's 16-byte
-// chunk c is stored at chunk c ^ ((row >> 1) & 3) so the 8 lanes served together by a ds_read_b128
-// (8 consecutive rows, same chunk) hit 8 distinct bank groups.
+// chunk c is stored at chunk c ^ ((row >> 2) & 3): the gfx950 LDS serves a ds_read_b128 16 lanes (16
+// consecutive rows, same chunk) at a time over 64 banks, and with 64-byte rows rows r, r+4, r+8, r+12 share
+// bank groups unless their chunks differ (measured: 48% bank-conflict cycles with a (row >> 1) swizzle).
 // Scale words: for a 32-row group the 16 bytes at (row % 32) * 16 of a blocked tile hold the four 32-row
 // groups' scales for one 128-wide K tile; a lane shifts its word by 8 * (lane / 32) so that op_sel 0 / 2
 // selects block 2P + lane/32 of the current half-tile P.
@@ -94,25 +95,29 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   const int R0 = dB ? n0 : m0, Rn = dB ? N : M;
   const int64_t ldd = dB ? ldb : lda;
   const uint8_t* gb = (dB ? B : A) + (int64_t)R0 * ldd;
-  const int lchunk = (lane & 3) ^ ((lane >> 3) & 3);  // (row >> 1) & 3 == (lane >> 3) & 3 for these rows
+  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3 for these rows
   uint32_t goff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = w4 * 64 + j * 16 + (lane >> 2);
     goff[j] = (uint32_t)((min(R0 + row, Rn - 1) - R0) * ldd) + lchunk * 16;  // clamp rows past the end
   }
-  const int stile = min((R0 >> 7) + (w4 >> 1), (Rn - 1) >> 7);
-  const uint8_t* sgp = (dB ? SB : SA) + (int64_t)stile * nkt * 512 + (w4 & 1) * 256 + (lane & 15) * 16;
+  // Fifth DMA of the stage, without divergence: waves 0 and 4 copy the two 128-row scale tiles of their
+  // operand (1 KB, lane -> tile lane / 32, bytes (lane % 32) * 16 of it); the other waves repeat their fourth
+  // code slice (same source, same destination: a harmless duplicate).
+  const bool scl = w4 == 0;
+  const int stile = min((R0 >> 7) + (lane >> 5), (Rn - 1) >> 7);
+  const uint8_t* sgp = (dB ? SB : SA) + (int64_t)stile * nkt * 512 + (lane & 31) * 16;
   const int dma_code_off = (dB ? kOffB : kOffA) + w4 * 4096;
-  const int dma_scale_off = (dB ? kOffSB : kOffSA) + w4 * 256;
+  const int dma5_off = scl ? (dB ? kOffSB : kOffSA) : dma_code_off + 3 * 1024;
 
   const uint32_t lds0 = lds_addr(lds);
-  auto issue = [&](int s) {
-    const uint32_t st = lds0 + (s & (kStages - 1)) * kStageBytes;
+  auto issue_to = [&](int s, int slot) {  // DMA stage s into ring slot `slot`
+    const uint32_t st = lds0 + slot * kStageBytes;
     const uint8_t* g = gb + s * kBK;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(g + goff[j], st + dma_code_off + j * 1024);
-    if (lane < 16) dma16(sgp + (s >> 1) * 512, st + dma_scale_off);
+    dma16(scl ? sgp + (s >> 1) * 512 : g + goff[3], st + dma5_off);
   };
 
   v16f acc[4][2];
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   }
 
   const int sshift = (lane >> 5) * 8;
-  const int sw = (lane >> 1) & 3;   // swizzle of rows base + lane % 32 (base a multiple of 32)
+  const int sw = (lane >> 2) & 3;  // swizzle of rows base + lane % 32 (base a multiple of 32)
   const int c0 = lane >> 5;
   auto compute = [&](int s, auto pc) {
     constexpr int P = decltype(pc)::value;  // half of the 128-wide K tile: blocks 2P, 2P + 1
@@ -150,25 +155,29 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
     acc[3][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb3, fa0, acc[3][0], 0, 0, 2 * P, sb3, 2 * P, sa0);
     acc[3][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb3, fa1, acc[3][1], 0, 0, 2 * P, sb3, 2 * P, sa1);
   };
+  // Steady state is branch-free so that each stage's MFMAs stay between its barrier and the next one (with
+  // conditional DMA blocks the compiler sinks the MFMAs of stage s below the barrier of stage s + 1).  Every
+  // step issues five DMA instructions per wave: stages past the end re-load the last stage into the ring slot
+  // just consumed (slot (s + 3) % 4 held stage s - 1, which every wave finished before this barrier; no later
+  // step reads it), so exactly two stages are always in flight behind the one waited for.
   auto step = [&](int s, auto pc) {
-    // stage s was issued three iterations ago; the stages after it that are already in flight may stay so
-    if (s + 2 < ns) wait_vmcnt<10>();
-    else if (s + 1 < ns) wait_vmcnt<5>();
-    else wait_vmcnt<0>();
-    // Bare s_barrier: __syncthreads() adds a workgroup fence that waits for every outstanding DMA (vmcnt(0)),
-    // which would drain the ring.  The explicit vmcnt above already covers this wave's stage-s DMA.
+    wait_vmcnt<10>();  // this wave's stage-s DMA has landed
+    // Bare s_barrier: __syncthreads() adds a workgroup fence that waits for every outstanding DMA
+    // (vmcnt(0)), which would drain the ring.
     __builtin_amdgcn_s_barrier();  // stage s visible to all waves; every wave is done with stage s-1's buffer
-    if (s + 3 < ns) issue(s + 3);
+    issue_to(min(s + 3, ns - 1), (s + 3) & (kStages - 1));
     compute(s, pc);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  issue(0);
-  if (ns > 1) issue(1);
-  if (ns > 2) issue(2);
+  issue_to(0, 0);
+  issue_to(min(1, ns - 1), 1);
+  issue_to(min(2, ns - 1), 2);
   for (int s = 0; s < ns; s += 2) {
     step(s, std::integral_constant<int, 0>{});
     step(s + 1, std::integral_constant<int, 1>{});
   }
+  wait_vmcnt<0>();  // drain the redundant tail loads before the workgroup can exit
 
   // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
   // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]
