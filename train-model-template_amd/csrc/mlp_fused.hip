@@ -33,6 +33,26 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int tile_col(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// Round a pair to bf16 with v_cvt_pk_bf16_f32 (round to nearest even, verified bit-exact against a software
+// RNE on the device); returns the packed pair and leaves the bf16-valued floats in a, b.
+__device__ __forceinline__ uint32_t rnd2(float& a, float& b) {
+  const v2f f = {a, b};
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+  return w;
+}
+
+// sigmoid(g) = 1 / (1 + exp(-g)) with the hardware exp2 and reciprocal (about 1 ulp each; the reference's
+// Triton fp32 division is approximate as well); silu(g) = g * sigmoid(g).  exp(-g) overflowing to +inf
+// gives sigmoid 0 and silu -0, as g / (exp(-g) + 1) does.
+__device__ __forceinline__ float fast_sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
 __device__ __forceinline__ v8bf as_bf8(uint4 u) {
   u32x4 v = {u.x, u.y, u.z, u.w};
   return __builtin_bit_cast(v8bf, v);
@@ -79,23 +99,29 @@ __device__ __forceinline__ v16f lora_tile(const uint16_t* wrow, const v8bf* xf) 
   return d;
 }
 
-// Quantize one 32-column block of the lane's row held in v[0..15] (+ the other 16 in lane ^ 32): codes into
-// q[m, jb..jb+31] (4-byte pieces), scale byte into the blocked layout (lanes < 32), or scale 0 for padded rows.
-__device__ __forceinline__ void quant_tile(const float* v, int lane, int m, bool live, uint8_t* qrow, int jb,
+// Quantize one 32-column block of the lane's row held as 8 packed bf16 pairs w[0..7] (columns
+// tile_col(2k), tile_col(2k+1)) plus the other 16 values in lane ^ 32: codes into q[m, jb..jb+31] (4-byte
+// pieces), scale byte into the blocked layout (lanes < 32), or scale 0 for padded rows.
+__device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, bool live, uint8_t* qrow, int jb,
                                            uint8_t* s, int64_t s_col_tiles) {
-  uint32_t am = 0;
+  u16x2 mm = {0, 0};
 #pragma unroll
-  for (int i = 0; i < 16; ++i) am = max(am, abs_bits(v[i]));
+  for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
+  uint32_t am = amax_bits(mm);
   am = max(am, (uint32_t)__shfl_xor((int)am, 32));
   const uint32_t e = e8m0_from_amax_bits(am);
+  uint32_t c[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) c[g] = encode4_bf16(w[2 * g], w[2 * g + 1], e);
   if (live) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<uint32_t*>(qrow + jb + g * 8 + (lane >> 5) * 4) =
-          encode4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3], e);
+    for (int g = 0; g < 4; ++g) *reinterpret_cast<uint32_t*>(qrow + jb + g * 8 + (lane >> 5) * 4) = c[g];
   }
   if (lane < 32) s[blocked_offset(m, jb >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
 }
+
+// registers 8s..8s+7 of an element tile held as packed words w[4s..4s+3], as an MFMA operand
+__device__ __forceinline__ v8bf words_bf8(const uint32_t* w) { return as_bf8(make_uint4(w[0], w[1], w[2], w[3])); }
 
 // ---------------------------------------------------------------------------------------------- forward
 // grid (row blocks of 32 up to Tpad, column groups); 4 waves share the row block, wave w takes the group's
@@ -129,25 +155,29 @@ __global__ __launch_bounds__(256) void fwd_kernel(const uint16_t* __restrict__ g
     const v16f lgd = lora_tile<R>(bg + (int64_t)(jb + (lane & 31)) * R + lg * 8, xg);
     const v16f lud = lora_tile<R>(bu + (int64_t)(jb + (lane & 31)) * R + lg * 8, xu);
     float hv[16];
+    uint32_t hw[8];  // h as packed bf16 pairs (columns i, i+1)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float g = round_bf16(gv[i] + s_g * lgd[i]);
-      const float u = round_bf16(uv[i] + s_u * lud[i]);
-      hv[i] = round_bf16((g / (expf(-g) + 1.0f)) * u);
+    for (int i = 0; i < 16; i += 2) {
+      float g0 = gv[i] + s_g * lgd[i], g1 = gv[i + 1] + s_g * lgd[i + 1];
+      float u0 = uv[i] + s_u * lud[i], u1 = uv[i + 1] + s_u * lud[i + 1];
+      rnd2(g0, g1);
+      rnd2(u0, u1);
+      hv[i] = (g0 * fast_sigmoid(g0)) * u0;
+      hv[i + 1] = (g1 * fast_sigmoid(g1)) * u1;
+      hw[i / 2] = rnd2(hv[i], hv[i + 1]);
     }
-    if (kWriteQ) quant_tile(hv, lane, m, live, q + (int64_t)mc * N, jb, s, N / 128);
+    if (kWriteQ) quant_tile(hw, lane, m, live, q + (int64_t)mc * N, jb, s, N / 128);
     if (h_out && live) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<uint2*>(h_out + (int64_t)m * N + jb + g * 8 + lg * 4) =
-            make_uint2(pack_bf16x2(hv[4 * g], hv[4 * g + 1]), pack_bf16x2(hv[4 * g + 2], hv[4 * g + 3]));
+        *reinterpret_cast<uint2*>(h_out + (int64_t)m * N + jb + g * 8 + lg * 4) = make_uint2(hw[2 * g], hw[2 * g + 1]);
     }
     // xS_down: D[ρ][m] += Σ_j ad[ρ, j] h[m, j]; A operand rows ρ = lane % 32 (zero past r)
     const int rho = lane & 31;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       v8bf af = rho < R ? load_bf8_perm(ad + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, regs_bf8(hv + 8 * ks), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, words_bf8(hw + 4 * ks), acc, 0, 0, 0);
     }
   }
   // acc lane l: m = l % 32, ρ = (i/4)*8 + (l/32)*4 + i%4
@@ -192,7 +222,13 @@ __global__ __launch_bounds__(512) void bwd_kernel(
     const uint16_t* bgrow = bg + (int64_t)(jb + (lane & 31)) * R + lg * 8;
     const uint16_t* burow = bu + (int64_t)(jb + (lane & 31)) * R + lg * 8;
     const uint16_t* adtrow = adT + (int64_t)(jb + (lane & 31)) * R + lg * 8;
-    v16f dbg = v16f{}, dbu = v16f{}, dad = v16f{};  // D[ρ][j]
+    // dB_g, dB_u, dA_d of this tile as D[j][ρ] on the 16x16x32 bf16 MFMA (A = transposed tile rows j, k = m;
+    // B = xsᵀ / dxdᵀ rows ρ): lane l holds ρ = l % 16 (+16 h) and j = jb + 16 jh + (l / 16) * 4 + i
+    v4f dbg[2][R / 16], dbu[2][R / 16], dad[2][R / 16];
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+      for (int h = 0; h < R / 16; ++h) dbg[jh][h] = dbu[jh][h] = dad[jh][h] = v4f{};
     for (int rb = r0; rb < r1; rb += 32) {
       const int m = rb + (lane & 31);
       const bool live = m < T;
@@ -212,35 +248,43 @@ __global__ __launch_bounds__(512) void bwd_kernel(
       const v16f lud = lora_tile<R>(burow, xu);
       const v16f ldd = lora_tile<R>(adtrow, xd);
       float dgv[16], duv[16], hv[16];
+      uint32_t dgw[8], duw[8], hw[8];  // the same as packed bf16 pairs
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float g = round_bf16(gv[i] + s_g * lgd[i]);
-        const float u = round_bf16(uv[i] + s_u * lud[i]);
-        const float sl = g / (expf(-g) + 1.0f);
-        hv[i] = round_bf16(sl * u);
-        const float dh = round_bf16(dv[i] + ldd[i]);
-        duv[i] = round_bf16(dh * sl);
-        const float sig = 1.0f / (1.0f + expf(-g));
-        dgv[i] = round_bf16(((dh * u) * sig) * (g * (1.0f - sig) + 1.0f));
+      for (int i = 0; i < 16; i += 2) {
+        float g0 = gv[i] + s_g * lgd[i], g1 = gv[i + 1] + s_g * lgd[i + 1];
+        float u0 = uv[i] + s_u * lud[i], u1 = uv[i + 1] + s_u * lud[i + 1];
+        float d0 = dv[i] + ldd[i], d1 = dv[i + 1] + ldd[i + 1];
+        rnd2(g0, g1);
+        rnd2(u0, u1);
+        rnd2(d0, d1);  // dh
+        const float sg0 = fast_sigmoid(g0), sg1 = fast_sigmoid(g1);
+        const float sl0 = g0 * sg0, sl1 = g1 * sg1;
+        hv[i] = sl0 * u0;
+        hv[i + 1] = sl1 * u1;
+        hw[i / 2] = rnd2(hv[i], hv[i + 1]);
+        duv[i] = d0 * sl0;
+        duv[i + 1] = d1 * sl1;
+        duw[i / 2] = rnd2(duv[i], duv[i + 1]);
+        dgv[i] = ((d0 * u0) * sg0) * (g0 * (1.0f - sg0) + 1.0f);
+        dgv[i + 1] = ((d1 * u1) * sg1) * (g1 * (1.0f - sg1) + 1.0f);
+        dgw[i / 2] = rnd2(dgv[i], dgv[i + 1]);
       }
       if (!live) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dgv[i] = duv[i] = hv[i] = 0.0f;
+        for (int i = 0; i < 8; ++i) dgw[i] = duw[i] = hw[i] = 0u;
       }
       if (dgu_out && live) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           uint16_t* o = dgu_out + (int64_t)m * 2 * N + jb + g * 8 + lg * 4;
-          *reinterpret_cast<uint2*>(o) =
-              make_uint2(pack_bf16x2(dgv[4 * g], dgv[4 * g + 1]), pack_bf16x2(dgv[4 * g + 2], dgv[4 * g + 3]));
-          *reinterpret_cast<uint2*>(o + N) =
-              make_uint2(pack_bf16x2(duv[4 * g], duv[4 * g + 1]), pack_bf16x2(duv[4 * g + 2], duv[4 * g + 3]));
+          *reinterpret_cast<uint2*>(o) = make_uint2(dgw[2 * g], dgw[2 * g + 1]);
+          *reinterpret_cast<uint2*>(o + N) = make_uint2(duw[2 * g], duw[2 * g + 1]);
         }
       }
       if (kQuant) {
         uint8_t* qrow = q + (int64_t)mc * 2 * N;
-        quant_tile(dgv, lane, m, live, qrow, jb, s, 2 * N / 128);
-        quant_tile(duv, lane, m, live, qrow, N + jb, s, 2 * N / 128);
+        quant_tile(dgw, lane, m, live, qrow, jb, s, 2 * N / 128);
+        quant_tile(duw, lane, m, live, qrow, N + jb, s, 2 * N / 128);
       }
       // dxa_g | dxa_u | xS_down products over this tile's 32 columns: D[ρ][m]
       v16f pg = v16f{}, pu = v16f{}, px = v16f{};
@@ -250,9 +294,9 @@ __global__ __launch_bounds__(512) void bwd_kernel(
         const v8bf fg = ok ? load_bf8_perm(bgT + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
         const v8bf fu = ok ? load_bf8_perm(buT + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
         const v8bf fa = ok ? load_bf8_perm(ad + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
-        pg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fg, regs_bf8(dgv + 8 * ks), pg, 0, 0, 0);
-        pu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fu, regs_bf8(duv + 8 * ks), pu, 0, 0, 0);
-        px = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, regs_bf8(hv + 8 * ks), px, 0, 0, 0);
+        pg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fg, words_bf8(dgw + 4 * ks), pg, 0, 0, 0);
+        pu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fu, words_bf8(duw + 4 * ks), pu, 0, 0, 0);
+        px = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, words_bf8(hw + 4 * ks), px, 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -265,28 +309,33 @@ __global__ __launch_bounds__(512) void bwd_kernel(
       }
       // transpose dg, du, h to [j][m] for the products that reduce over m
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 16; i += 2) {
         const int j = tile_col(i, lane);
-        tr[w][0][j][lane & 31] = (uint16_t)(__float_as_uint(dgv[i]) >> 16);
-        tr[w][1][j][lane & 31] = (uint16_t)(__float_as_uint(duv[i]) >> 16);
-        tr[w][2][j][lane & 31] = (uint16_t)(__float_as_uint(hv[i]) >> 16);
+        tr[w][0][j][lane & 31] = (uint16_t)dgw[i / 2];
+        tr[w][0][j + 1][lane & 31] = (uint16_t)(dgw[i / 2] >> 16);
+        tr[w][1][j][lane & 31] = (uint16_t)duw[i / 2];
+        tr[w][1][j + 1][lane & 31] = (uint16_t)(duw[i / 2] >> 16);
+        tr[w][2][j][lane & 31] = (uint16_t)hw[i / 2];
+        tr[w][2][j + 1][lane & 31] = (uint16_t)(hw[i / 2] >> 16);
       }
       __syncthreads();
-      // D[ρ][j] += Σ_m xs_g[m, ρ] dg[m, j] etc.: A = xsᵀ / dxdᵀ rows ρ (k = m), B = transposed tile rows j
+      // D[j][ρ] += Σ_m dg[m, j] xs_g[m, ρ] etc. over the 32 rows of this block (one K = 32 step)
+      {
+        const int mo = (lane >> 4) * 8;  // this lane's 8 rows of the block
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int mk = rb + 16 * ks + lg * 8;  // first of this lane's 8 rows
-        const bool ok = rho < R;
-        v8bf ag = v8bf{}, au = v8bf{}, axd = v8bf{};
-        if (ok) {
-          ag = load_bf8(xsT + (int64_t)rho * Tpad + mk);
-          au = load_bf8(xsT + (int64_t)(R + rho) * Tpad + mk);
-          axd = load_bf8(dxdT + (int64_t)rho * Tpad + mk);
+        for (int h = 0; h < R / 16; ++h) {
+          const int rr = h * 16 + (lane & 15);
+          const v8bf bgx = load_bf8(xsT + (int64_t)rr * Tpad + rb + mo);
+          const v8bf bux = load_bf8(xsT + (int64_t)(R + rr) * Tpad + rb + mo);
+          const v8bf bdx = load_bf8(dxdT + (int64_t)rr * Tpad + rb + mo);
+#pragma unroll
+          for (int jh = 0; jh < 2; ++jh) {
+            const int jl = jh * 16 + (lane & 15);
+            dbg[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(load_bf8(&tr[w][0][jl][mo]), bgx, dbg[jh][h], 0, 0, 0);
+            dbu[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(load_bf8(&tr[w][1][jl][mo]), bux, dbu[jh][h], 0, 0, 0);
+            dad[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(load_bf8(&tr[w][2][jl][mo]), bdx, dad[jh][h], 0, 0, 0);
+          }
         }
-        const int jl = lane & 31, mo = 16 * ks + lg * 8;
-        dbg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ag, load_bf8(&tr[w][0][jl][mo]), dbg, 0, 0, 0);
-        dbu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(au, load_bf8(&tr[w][1][jl][mo]), dbu, 0, 0, 0);
-        dad = __builtin_amdgcn_mfma_f32_32x32x16_bf16(axd, load_bf8(&tr[w][2][jl][mo]), dad, 0, 0, 0);
       }
       // sum the 8 waves' dxa | xS products and accumulate into the column group's partial
       for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 512) {
@@ -302,17 +351,19 @@ __global__ __launch_bounds__(512) void bwd_kernel(
       }
       __syncthreads();
     }
-    // dB partials of this super-block: D[ρ][j], lane l: j = jb + l % 32, ρ = tile_col(i, l)
+    // dB partials of this super-block: D[j][ρ], lane l: ρ = 16 h + l % 16, j = jb + 16 jh + (l / 16) * 4 + i
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int rr = tile_col(i, lane);
-      if (rr < R) {
-        const int j = jb + (lane & 31);
-        dbg_part[((int64_t)blockIdx.x * N + j) * R + rr] = dbg[i];
-        dbu_part[((int64_t)blockIdx.x * N + j) * R + rr] = dbu[i];
-        dad_part[((int64_t)blockIdx.x * R + rr) * N + j] = dad[i];
-      }
-    }
+    for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+      for (int h = 0; h < R / 16; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = h * 16 + (lane & 15);
+          const int j = jb + jh * 16 + (lane >> 4) * 4 + i;
+          dbg_part[((int64_t)blockIdx.x * N + j) * R + rr] = dbg[jh][h][i];
+          dbu_part[((int64_t)blockIdx.x * N + j) * R + rr] = dbu[jh][h][i];
+          dad_part[((int64_t)blockIdx.x * R + rr) * N + j] = dad[jh][h][i];
+        }
   }
 }
 

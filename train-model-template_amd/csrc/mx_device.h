@@ -80,6 +80,36 @@ __device__ __forceinline__ int64_t blocked_offset(int64_t i, int64_t b, int64_t 
   return ((i >> 7) * n_col_tiles + (b >> 2)) * 512 + (i & 31) * 16 + ((i & 127) >> 5) * 4 + (b & 3);
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Running max of the bf16 magnitudes of a packed pair (v_pk_max_u16): for bf16 bit patterns with the sign
+// cleared, unsigned 16-bit order is magnitude order and every NaN sorts above +inf, so the max propagates NaN.
+__device__ __forceinline__ u16x2 absmax2(u16x2 acc, uint32_t w) {
+  return __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, w & 0x7fff7fffu));
+}
+// fp32 bit pattern of the larger half (the block amax as fp32 bits)
+__device__ __forceinline__ uint32_t amax_bits(u16x2 m) { return (uint32_t)max(m.x, m.y) << 16; }
+
+// Four bf16 (two packed words) of a block with scale byte e -> four E4M3 codes.  Finite blocks (e <= 253)
+// use v_cvt_scalef32_pk_fp8_bf16, which computes RNE_E4M3(x / scale) (verified bit-exact on the device for
+// every finite bf16 input and power-of-two scale); x / 2^(e-127) = x * 2^(127-e) exactly, and e == 0 scales
+// by 1.  RCEIL guarantees |x| / scale <= 448 there, so no clamp is needed.  Blocks with NaN (e = 255) or inf
+// (e = 254) take encode4, which clamps inf to +-448 and writes 0x7F for NaN blocks; the choice is made per
+// wave (ballot) so the common path stays branch- and select-free.
+__device__ __forceinline__ uint32_t encode4_bf16(uint32_t w0, uint32_t w1, uint32_t e) {
+  const float sc = __uint_as_float(e == 0u ? 0x3f800000u : e << 23);
+  s16x2 r = {0, 0};
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2, w0), sc, false);
+  r = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(r, __builtin_bit_cast(bf16x2, w1), sc, true);
+  uint32_t c = __builtin_bit_cast(uint32_t, r);
+  if (__builtin_amdgcn_ballot_w64(e >= 254u)) {
+    if (e >= 254u) c = encode4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), e);
+  }
+  return c;
+}
+
 // Unsigned max over a 4-lane group (the 4 lanes that share one 32-element block).
 __device__ __forceinline__ uint32_t quad_umax(uint32_t v) {
   v = max(v, (uint32_t)__shfl_xor((int)v, 1));

@@ -23,15 +23,15 @@ constexpr int kLdT = kTile + 8;  // bf16 row stride of the LDS copy used by the 
 // Quantize 8 consecutive bf16 (one uint4) whose 4-lane group forms one 32-block; returns the codes and the
 // block's scale byte.
 __device__ __forceinline__ uint2 quant8(uint4 v, uint32_t& e_out) {
-  float f[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
-                bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
-  uint32_t am = 0;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) am = max(am, abs_bits(f[k]));
-  am = quad_umax(am);
-  uint32_t e = e8m0_from_amax_bits(am);
+  u16x2 m = {0, 0};
+  m = absmax2(m, v.x);
+  m = absmax2(m, v.y);
+  m = absmax2(m, v.z);
+  m = absmax2(m, v.w);
+  const uint32_t am = quad_umax(amax_bits(m));
+  const uint32_t e = e8m0_from_amax_bits(am);
   e_out = e;
-  return make_uint2(encode4(f[0], f[1], f[2], f[3], e), encode4(f[4], f[5], f[6], f[7], e));
+  return make_uint2(encode4_bf16(v.x, v.y, e), encode4_bf16(v.z, v.w, e));
 }
 
 template <bool kRows, bool kCols>
