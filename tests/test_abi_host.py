@@ -1,0 +1,116 @@
+"""CPU checks of the boundary and the host logic: the C-ABI library loads, exports every function that
+include/mxfp8_mlp.h declares, reports the ABI version the Python side expects, and rejects bad arguments
+before launching anything; the launch-grid choices and the workload generators behave as documented.
+No GPU compute is called."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import _native
+import fused_mlp
+import workloads
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mxfp8_mlp.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mxfp8_\w+)\s*\(", txt, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libmxfp8_mlp.so not built")
+    return _native.load()
+
+
+def test_header_declares_the_abi():
+    names = _declared()
+    assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
+    assert len(names) == 9, names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert set(_declared()) == set(_native.SIGNATURES)
+
+
+def test_abi_version(lib):
+    assert lib.mxfp8_abi_version() == _native.ABI_VERSION
+    txt = open(HEADER).read()
+    assert f"#define MXFP8_MLP_ABI_VERSION {_native.ABI_VERSION}" in txt
+
+
+def test_argument_checks_reject_before_launch(lib):
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
+    # cols not a multiple of 128
+    assert lib.mxfp8_quant_rows(p, 4, 100, 100, p, 112, p, 1, 0, None) == -1
+    assert b"cols" in lib.mxfp8_last_error()
+    # null pointer
+    assert lib.mxfp8_quant_rows(None, 4, 128, 128, p, 128, p, 1, 0, None) == -1
+    # GEMM K not a multiple of 128
+    assert lib.mxfp8_gemm_nt(p, p, 96, p, p, 96, 4, 128, 96, p, 128, None, 0, None, 0, 0, 1.0, None) == -1
+    # GEMM epilogue rank not supported
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, p, 8, p, 8, 8, 1.0, None) == -1
+    # backward column group must divide N and be a multiple of 256
+    args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, None]
+    assert lib.mxfp8_mlp_bwd(*args) == -1
+    assert lib.mxfp8_sum_parts(None, 1, 4, 1.0, p, 0, None) == -1
+
+
+def test_native_refuses_cpu_tensors(lib):
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    q = torch.empty(4, 128, dtype=torch.uint8)
+    s = torch.empty(512, dtype=torch.uint8)
+    with pytest.raises(_native.NativeError):
+        _native.quant_rows(x, q, s)
+
+
+def test_bwd_grid_choice():
+    fused_mlp._CUS[0] = 256
+    for T, N in [(10752, 6144), (4096, 3584), (256, 3584), (142336, 6144), (8896, 6144)]:
+        sb, cg = fused_mlp._bwd_grid(T, N, 16)
+        tpad = -(-T // 128) * 128
+        assert sb % 128 == 0 and cg % 256 == 0 and N % cg == 0 and sb <= tpad
+        nsb, ncg = -(-tpad // sb), N // cg
+        assert nsb * ncg >= 2 * 256 or (sb == 128 and cg == 256)
+
+
+def test_fwd_groups_choice():
+    fused_mlp._CUS[0] = 256
+    for T, N in [(10752, 6144), (256, 3584), (4096, 3584)]:
+        ng = fused_mlp._fwd_groups(T, N)
+        assert (N // 32) % ng == 0 and (N // 32) // ng >= 4
+
+
+def test_mlp_gating_on_cpu_returns_none():
+    model, inps = workloads.build_model(1, T=8, device="cpu")
+    assert fused_mlp.mlp(model.layers[0].mlp, inps[0]["x"]) is None
+
+
+def test_workloads_shapes_and_seeds():
+    a = workloads.make_inputs(1, T=64)
+    b = workloads.make_inputs(1, T=64)
+    assert torch.equal(a["x"], b["x"]) and a["x"].dtype == torch.bfloat16 and a["x"].shape == (64, 1024)
+    assert a["Wg"].shape == (3584, 1024) and a["Wd"].shape == (1024, 3584)
+    assert a["Ag"].shape == (16, 1024) and a["Bg"].shape == (3584, 16) and a["Ad"].shape == (16, 3584)
+    assert a["Ag"].dtype == torch.float32 and a["s"] == 2.0
+    assert workloads.flops(10752, 2048, 6144) == 1623497637888
+    assert workloads.quant_bytes(10752, 2048) == 10752 * 2048 * 3 + 84 * 16 * 512
+
+
+def test_outlier_config_contains_edge_blocks():
+    x = workloads.make_inputs(5, T=512, dy=False)["x"].float()
+    blocks = x.view(512, -1, 32)
+    amax = blocks.abs().amax(-1)
+    assert bool((amax == 0).any())  # all-zero blocks
+    k = torch.log2(amax[amax > 0] / 448.0)
+    assert bool((k == torch.round(k)).any())  # blocks whose amax is exactly 448 * 2^k
+    assert bool(torch.signbit(blocks[(amax == 0)]).any())  # a -0.0 block
