@@ -130,52 +130,67 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   const int sshift = (lane >> 5) * 8;
   const int sw = (lane >> 2) & 3;  // swizzle of rows base + lane % 32 (base a multiple of 32)
   const int c0 = lane >> 5;
-  auto compute = [&](int s, auto pc) {
-    constexpr int P = decltype(pc)::value;  // half of the 128-wide K tile: blocks 2P, 2P + 1
-    const uint8_t* st = lds + (s & (kStages - 1)) * kStageBytes;
-    const uint2 sa2 = *reinterpret_cast<const uint2*>(st + kOffSA + (wm >> 1) * 512 + (lane & 31) * 16 + (wm & 1) * 8);
-    const uint4 sb4 = *reinterpret_cast<const uint4*>(st + kOffSB + wn * 512 + (lane & 31) * 16);
-    const int sa0 = (int)(sa2.x >> sshift), sa1 = (int)(sa2.y >> sshift);
-    const int sb0 = (int)(sb4.x >> sshift), sb1 = (int)(sb4.y >> sshift);
-    const int sb2 = (int)(sb4.z >> sshift), sb3 = (int)(sb4.w >> sshift);
+  struct Frags {
+    v8i a0, a1, b0, b1, b2, b3;
+    uint2 sa;
+    uint4 sb;
+  };
+  auto read = [&](int slot, Frags& f) {
+    const uint8_t* st = lds + slot * kStageBytes;
+    f.sa = *reinterpret_cast<const uint2*>(st + kOffSA + (wm >> 1) * 512 + (lane & 31) * 16 + (wm & 1) * 8);
+    f.sb = *reinterpret_cast<const uint4*>(st + kOffSB + wn * 512 + (lane & 31) * 16);
     const uint8_t* la = st + kOffA;
     const uint8_t* lb = st + kOffB;
-    const v8i fa0 = frag(la, wm * 64 + (lane & 31), c0, sw);
-    const v8i fa1 = frag(la, wm * 64 + 32 + (lane & 31), c0, sw);
-    const v8i fb0 = frag(lb, wn * 128 + (lane & 31), c0, sw);
-    const v8i fb1 = frag(lb, wn * 128 + 32 + (lane & 31), c0, sw);
-    const v8i fb2 = frag(lb, wn * 128 + 64 + (lane & 31), c0, sw);
-    const v8i fb3 = frag(lb, wn * 128 + 96 + (lane & 31), c0, sw);
-    acc[0][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb0, fa0, acc[0][0], 0, 0, 2 * P, sb0, 2 * P, sa0);
-    acc[0][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb0, fa1, acc[0][1], 0, 0, 2 * P, sb0, 2 * P, sa1);
-    acc[1][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb1, fa0, acc[1][0], 0, 0, 2 * P, sb1, 2 * P, sa0);
-    acc[1][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb1, fa1, acc[1][1], 0, 0, 2 * P, sb1, 2 * P, sa1);
-    acc[2][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb2, fa0, acc[2][0], 0, 0, 2 * P, sb2, 2 * P, sa0);
-    acc[2][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb2, fa1, acc[2][1], 0, 0, 2 * P, sb2, 2 * P, sa1);
-    acc[3][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb3, fa0, acc[3][0], 0, 0, 2 * P, sb3, 2 * P, sa0);
-    acc[3][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb3, fa1, acc[3][1], 0, 0, 2 * P, sb3, 2 * P, sa1);
+    f.a0 = frag(la, wm * 64 + (lane & 31), c0, sw);
+    f.a1 = frag(la, wm * 64 + 32 + (lane & 31), c0, sw);
+    f.b0 = frag(lb, wn * 128 + (lane & 31), c0, sw);
+    f.b1 = frag(lb, wn * 128 + 32 + (lane & 31), c0, sw);
+    f.b2 = frag(lb, wn * 128 + 64 + (lane & 31), c0, sw);
+    f.b3 = frag(lb, wn * 128 + 96 + (lane & 31), c0, sw);
   };
-  // Steady state is branch-free so that each stage's MFMAs stay between its barrier and the next one (with
-  // conditional DMA blocks the compiler sinks the MFMAs of stage s below the barrier of stage s + 1).  Every
-  // step issues five DMA instructions per wave: stages past the end re-load the last stage into the ring slot
-  // just consumed (slot (s + 3) % 4 held stage s - 1, which every wave finished before this barrier; no later
-  // step reads it), so exactly two stages are always in flight behind the one waited for.
-  auto step = [&](int s, auto pc) {
-    wait_vmcnt<10>();  // this wave's stage-s DMA has landed
+  auto mma = [&](const Frags& f, auto pc) {
+    constexpr int P = decltype(pc)::value;  // half of the 128-wide K tile: blocks 2P, 2P + 1
+    const int sa0 = (int)(f.sa.x >> sshift), sa1 = (int)(f.sa.y >> sshift);
+    const int sb0 = (int)(f.sb.x >> sshift), sb1 = (int)(f.sb.y >> sshift);
+    const int sb2 = (int)(f.sb.z >> sshift), sb3 = (int)(f.sb.w >> sshift);
+    acc[0][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b0, f.a0, acc[0][0], 0, 0, 2 * P, sb0, 2 * P, sa0);
+    acc[0][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b0, f.a1, acc[0][1], 0, 0, 2 * P, sb0, 2 * P, sa1);
+    acc[1][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b1, f.a0, acc[1][0], 0, 0, 2 * P, sb1, 2 * P, sa0);
+    acc[1][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b1, f.a1, acc[1][1], 0, 0, 2 * P, sb1, 2 * P, sa1);
+    acc[2][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b2, f.a0, acc[2][0], 0, 0, 2 * P, sb2, 2 * P, sa0);
+    acc[2][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b2, f.a1, acc[2][1], 0, 0, 2 * P, sb2, 2 * P, sa1);
+    acc[3][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b3, f.a0, acc[3][0], 0, 0, 2 * P, sb3, 2 * P, sa0);
+    acc[3][1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b3, f.a1, acc[3][1], 0, 0, 2 * P, sb3, 2 * P, sa1);
+  };
+  // Steady state, branch-free (with conditional blocks the compiler sinks a stage's MFMAs below the next
+  // barrier).  Step s: wait until stage s + 1 has landed (this wave's DMA) and this wave's reads of stage s are
+  // in registers, barrier, refill the slot of stage s with stage s + 4, read stage s + 1's fragments, then
+  // run stage s's MFMAs from registers, so LDS latency and the DMA issue overlap the matrix work.  Every step
+  // issues five DMA instructions per wave; stages past the end re-load the last stage into the slot just
+  // consumed (no later step reads it), so exactly two stages are in flight behind the one waited for.
+  auto step = [&](int s, Frags& cur, Frags& nxt, auto pc) {
+    wait_vmcnt<10>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     // Bare s_barrier: __syncthreads() adds a workgroup fence that waits for every outstanding DMA
     // (vmcnt(0)), which would drain the ring.
-    __builtin_amdgcn_s_barrier();  // stage s visible to all waves; every wave is done with stage s-1's buffer
-    issue_to(min(s + 3, ns - 1), (s + 3) & (kStages - 1));
-    compute(s, pc);
+    __builtin_amdgcn_s_barrier();
+    issue_to(min(s + 4, ns - 1), s & (kStages - 1));
+    read((s + 1) & (kStages - 1), nxt);
+    mma(cur, pc);
     __builtin_amdgcn_sched_barrier(0);
   };
 
   issue_to(0, 0);
   issue_to(min(1, ns - 1), 1);
   issue_to(min(2, ns - 1), 2);
+  issue_to(min(3, ns - 1), 3);
+  wait_vmcnt<15>();  // stage 0 landed
+  __builtin_amdgcn_s_barrier();
+  Frags f0, f1;
+  read(0, f0);
   for (int s = 0; s < ns; s += 2) {
-    step(s, std::integral_constant<int, 0>{});
-    step(s + 1, std::integral_constant<int, 1>{});
+    step(s, f0, f1, std::integral_constant<int, 0>{});
+    step(s + 1, f1, f0, std::integral_constant<int, 1>{});
   }
   wait_vmcnt<0>();  // drain the redundant tail loads before the workgroup can exit
 
