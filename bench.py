@@ -1,20 +1,35 @@
 """Benchmark of the MXFP8 fused SwiGLU-MLP hot path on one MI355X.
 
-One step = forward + backward of one Qwen3.5-2B-shaped LoRA MLP layer (configuration 3: 10,752 tokens,
-d_model 2048, d_ffn 6144, LoRA r16 alpha 32) through the drop-in API the training script uses
-(mxfp8.enable_mxfp8 once, then fused_mlp.mlp + backward), on synthetic seeded inputs already resident in HBM.
+One step = forward + backward through the drop-in API the training script uses (mxfp8.enable_mxfp8 once, then
+fused_mlp.mlp per layer + backward), on synthetic seeded inputs already resident in HBM:
+  --config 3 (default, the headline): one Qwen3.5-2B-shaped LoRA MLP layer, 10,752 tokens, d_model 2048,
+             d_ffn 6144, LoRA r16 alpha 32;
+  --config 4: a stack of 24 such layers at 142,336 tokens (each layer takes the previous layer's output);
+  --config 5: configuration 3's shape on the outlier inputs (Student-t activations with edge blocks).
 
 Prints one JSON line:
-  value        MX GEMM work of the step (12·T·K·N flops; LoRA bf16 flops not counted) / step time, TFLOP/s
+  value        MX GEMM work of the step (12·T·K·N flops per layer; LoRA bf16 flops not counted) / step time
   roofline     the dominant kernel, the MX GEMM: its algorithmic flops / its launch time measured with HIP
-               events on the launch stream over the timed steps, against the 5.0 PFLOP/s dense MXFP8 peak
-  quantizer    mx_quant on the [T, K] activation and on a [T, 2N] buffer (back-to-back launches), GB/s of
-               algorithmic bytes (read bf16, write codes + blocked scales) against 8 TB/s
-  cpu_baseline the CPU oracle of the same path on a bounded token sample, on this host's cores
+               events on the launch stream over the timed steps, against the 5.0 PFLOP/s dense MXFP8 peak;
+               traffic = HBM bytes per GEMM launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+  quantizer    mx_quant on the [T, K] activation and on a [T, 2N] buffer, and the dual-axis preparation of the
+               frozen weights (quant_both on W_gate|up and W_down), back-to-back launches, GB/s of algorithmic
+               bytes (read bf16, write codes + blocked scales) against 8 TB/s
+  with_requant the step plus the dual-axis weight preparation of every layer
+  cpu_baseline the CPU oracle of the same layer on a bounded token sample, on this host's cores
+
+Profiling helpers (same file, so every profile names committed code only):
+  --copy-calib           also run a plain 1 GiB bf16 copy kernel (torch.neg, read 1 GiB + write 1 GiB) three
+                         times, so a rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run can scale its counters
+  --traffic-summary F W  read two rocprofv3 --pmc output directories (FETCH_SIZE run, WRITE_SIZE run) and write
+                         profiles/mx_gemm_c<cfg>_traffic.json + .md (no GPU needed)
 """
 import argparse
+import csv
+import glob
 import json
 import os
+import re
 import sys
 import time
 
@@ -25,20 +40,24 @@ for p in (ROOT, os.path.join(ROOT, "train-model-template_amd")):
 
 PEAK_MXFP8_TFLOPS = 5000.0  # MI355X dense MXFP8 (f8f6f4 MFMA) peak, public figure
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E peak
-CFG = 3
+COPY_CALIB_BYTES = 1 << 30  # bytes read (and written) by one --copy-calib launch
 
 
-def _traffic_from_profiles():
+def _traffic_path(cfg, ext):
+    return os.path.join(ROOT, "profiles", f"mx_gemm_c{cfg}_traffic.{ext}")
+
+
+def _traffic_from_profiles(cfg):
     """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary (profiles/), or None."""
-    p = os.path.join(ROOT, "profiles", "mx_gemm_c3_traffic.json")
+    p = _traffic_path(cfg, "json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         return json.load(f).get("bytes_per_launch")
 
 
-def _cpu_baseline(T_sample):
-    """Oracle fwd+bwd of the same layer on T_sample tokens (1 warmup, median of 3), TFLOP/s."""
+def _cpu_baseline(cfg, T_sample):
+    """Oracle fwd+bwd of one layer of the configuration on T_sample tokens (1 warmup, median of 3), TFLOP/s."""
     import torch
 
     import workloads
@@ -46,7 +65,7 @@ def _cpu_baseline(T_sample):
 
     cores = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
-    inp = workloads.make_inputs(CFG, T=T_sample)
+    inp = workloads.make_inputs(cfg, T=T_sample)
     W = omlp.prepare_weights(inp["Wg"], inp["Wu"], inp["Wd"])
     S, bg, bu, ad, bd = omlp.lora_cast(inp["Ag"], inp["Bg"], inp["Au"], inp["Bu"], inp["Ad"], inp["Bd"])
     s = inp["s"]
@@ -63,9 +82,155 @@ def _cpu_baseline(T_sample):
         ts.append(time.perf_counter() - t0)
     t = sorted(ts)[1]
     fl = workloads.flops(T_sample, inp["K"], inp["N"])
+    c = workloads.CONFIGS[cfg]
+    what = f"one layer of configuration {cfg} on {T_sample} of its {c['T']} tokens"
+    if c["layers"] > 1:
+        what += f" (the stack is {c['layers']} such layers; the per-token rate is the same)"
     return {"value": round(fl / t / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"oracle fwd+bwd of the config-3 layer on {T_sample} of its 10752 tokens (median of 3 after "
-                      f"1 warmup, {t:.2f} s per step; weight preparation excluded as on the GPU)"}
+            "sample": f"oracle fwd+bwd of {what}, median of 3 after 1 warmup, {t:.2f} s per step; weight "
+                      f"preparation excluded as on the GPU"}
+
+
+def _time_launches(fn, n):
+    import torch
+    for _ in range(3):
+        fn()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(n):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def _quantizer(T, K, N, dev):
+    import torch
+
+    import mxfp8
+    import workloads
+    out = {}
+    for name, shape in (("x[T,K]", (T, K)), ("dgu[T,2N]", (T, 2 * N))):
+        src = torch.randn(shape, device=dev).to(torch.bfloat16)
+        n = max(5, int(2e9 // (shape[0] * shape[1] * 3)))  # >= ~1 ms of launches
+        ms = _time_launches(lambda: mxfp8.mx_quant(src), n)
+        by = workloads.quant_bytes(*shape)
+        out[name] = {"GB/s": round(by / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 2), "bytes": by,
+                     "frac": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        del src
+    wq_ms = 0.0
+    for name, shape in (("W_gate|up dual[2N,K]", (2 * N, K)), ("W_down dual[K,N]", (K, N))):
+        w = (torch.randn(shape, device=dev) * 0.02).to(torch.bfloat16)
+        ms = _time_launches(lambda: mxfp8.quant_both(w), 50)
+        by = workloads.quant_bytes(*shape, dual=True)
+        out[name] = {"GB/s": round(by / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 2), "bytes": by,
+                     "frac": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        wq_ms += ms
+        del w
+    return out, wq_ms
+
+
+def _copy_calib(dev):
+    import torch
+    src = torch.ones(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _pmc_rows(d):
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows += list(csv.DictReader(fh))
+    return rows
+
+
+def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the MX GEMM launches, scaled by what the same counters read
+    for the 1 GiB copy kernel; writes profiles/mx_gemm_c<cfg>_traffic.{json,md}."""
+    import workloads
+    c = workloads.CONFIGS[cfg]
+    T, K, N, r = c["T"], c["K"], c["N"], c["r"]
+
+    def per_dispatch(d, counter):
+        vals = {}
+        for row in _pmc_rows(d):
+            if row["Counter_Name"] != counter:
+                continue
+            key = (row["Dispatch_Id"], row["Kernel_Name"], row.get("Grid_Size", ""))
+            vals[key] = vals.get(key, 0.0) + float(row["Counter_Value"])
+        return vals
+
+    fetch, write = per_dispatch(fetch_dir, "FETCH_SIZE"), per_dispatch(write_dir, "WRITE_SIZE")
+
+    def copy_kib(vals):
+        v = [x for (_, name, _), x in vals.items() if "neg" in name]
+        if not v:
+            raise SystemExit("no copy-calibration dispatch (run bench.py with --copy-calib)")
+        return sorted(v)[len(v) // 2]
+
+    f_scale = (COPY_CALIB_BYTES / 1024) / copy_kib(fetch)
+    w_scale = (COPY_CALIB_BYTES / 1024) / copy_kib(write)
+
+    # the four GEMM shapes of one layer, told apart by kernel template (epilogue rank) and grid size
+    shapes = {"gate|up": (T, 2 * N, K, 0), "down": (T, K, N, r), "dh": (T, N, K, 0), "dx": (T, K, 2 * N, 2 * r)}
+
+    def gemm_groups(vals):
+        g = {}
+        for (_, name, grid), v in vals.items():
+            if "gemm_kernel" not in name:
+                continue
+            m = re.search(r"(\w*gemm_kernel<[^>]*>)", name)
+            g.setdefault((m.group(1) if m else name[:60], grid), []).append(v)
+        return {k: sum(v) / len(v) for k, v in g.items()}
+
+    gf, gw = gemm_groups(fetch), gemm_groups(write)
+    rows = []
+    for (name, grid), kib in sorted(gf.items()):
+        fb = kib * 1024 * f_scale
+        wb = gw.get((name, grid), 0.0) * 1024 * w_scale
+        rows.append({"kernel": name, "grid": grid, "fetch_bytes": round(fb), "write_bytes": round(wb)})
+    if not rows:
+        raise SystemExit("no gemm_kernel dispatches in the PMC output")
+    # algorithmic bytes of each shape: read both MX operands and their scales once, write the bf16 output,
+    # read the rank-r LoRA operands of the epilogue
+    alg = {}
+    for nm, (M, Nn, Kk, rr) in shapes.items():
+        sc = lambda R, C: -(-R // 128) * (C // 128) * 512 // 4  # noqa: E731  (one scale per 32 along K)
+        alg[nm] = M * Kk + Nn * Kk + sc(M, Kk) + sc(Nn, Kk) + M * Nn * 2 + (M + Nn) * rr * 2
+    per_launch = sum(x["fetch_bytes"] + x["write_bytes"] for x in rows) / len(rows)
+    alg_mean = sum(alg.values()) / len(alg)
+    summary = {"config": cfg, "kernel": "mx_gemm (gate|up, down, dh, dx)",
+               "bytes_per_launch": round(per_launch),
+               "algorithmic_bytes_per_launch": round(alg_mean),
+               "copy_calibration": {"bytes": COPY_CALIB_BYTES, "fetch_scale": round(f_scale, 4),
+                                    "write_scale": round(w_scale, 4)},
+               "launches": rows, "algorithmic_bytes": alg,
+               "commands": [cmd_fetch, cmd_write]}
+    with open(_traffic_path(cfg, "json"), "w") as f:
+        json.dump(summary, f, indent=1)
+    with open(_traffic_path(cfg, "md"), "w") as f:
+        f.write(f"# HBM traffic of the MX GEMM launches, configuration {cfg} (rocprofv3 FETCH_SIZE / WRITE_SIZE)\n\n")
+        f.write("Commands (GPU box; one counter per run):\n\n```\ncd /tmp && export TMPDIR=/tmp\n"
+                f"{cmd_fetch}\n{cmd_write}\n```\n\n")
+        f.write(f"Scaled by the same counters on a plain copy kernel (torch.neg of 1 GiB bf16: reads 1 GiB, writes "
+                f"1 GiB): FETCH x{f_scale:.4f}, WRITE x{w_scale:.4f}.\n\n")
+        f.write("| kernel | grid | HBM read MB | HBM write MB |\n|---|---|---|---|\n")
+        for x in rows:
+            f.write(f"| {x['kernel']} | {x['grid']} | {x['fetch_bytes'] / 1e6:.1f} | {x['write_bytes'] / 1e6:.1f} |\n")
+        f.write("\n| shape | algorithmic MB (operands + scales once, bf16 output, LoRA operands) |\n|---|---|\n")
+        for nm, b in alg.items():
+            f.write(f"| {nm} | {b / 1e6:.1f} |\n")
+        f.write(f"\nMean per launch: measured {per_launch / 1e6:.1f} MB, algorithmic {alg_mean / 1e6:.1f} MB.\n")
+    print(json.dumps({"bytes_per_launch": summary["bytes_per_launch"],
+                      "algorithmic_bytes_per_launch": summary["algorithmic_bytes_per_launch"]}))
 
 
 def main():
@@ -73,9 +238,17 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-quant", action="store_true", help="skip the standalone quantizer timings")
     ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
+    ap.add_argument("--traffic-commands", nargs=2, default=("", ""), metavar=("CMD_FETCH", "CMD_WRITE"))
     args = ap.parse_args()
+    if args.traffic_summary:
+        _traffic_summary(args.config, *args.traffic_summary, *args.traffic_commands)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the MLP shards by tokens with "
               "one LoRA-gradient all-reduce per layer; see DESIGN.md).", file=sys.stderr)
@@ -90,25 +263,29 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    c = workloads.CONFIGS[CFG]
-    model, inps = workloads.build_model(CFG, device=dev)
+    cfg = args.config
+    c = workloads.CONFIGS[cfg]
+    model, inps = workloads.build_model(cfg, layers=c["layers"], device=dev)
     mxfp8.enable_mxfp8(model)
-    mod = model.layers[0].mlp
+    mods = [layer.mlp for layer in model.layers]
     inp = inps[0]
     T, K, N = inp["T"], inp["K"], inp["N"]
     x = inp["x"].to(dev).requires_grad_(True)
     dy = inp["dy"].to(dev)
-    params = [p for p in mod.parameters() if p.requires_grad]
+    del inps
+    params = [p for p in model.parameters() if p.requires_grad]
 
     def step():
         fused_linear.new_step()
         for p in params:
             p.grad = None
         x.grad = None
-        y = fused_mlp.mlp(mod, x)
+        y = x
+        for m in mods:
+            y = fused_mlp.mlp(m, y)
         y.backward(dy)
 
-    assert fused_mlp.mlp(mod, x) is not None, "fused path not taken"
+    assert fused_mlp.mlp(mods[0], x) is not None, "fused path not taken"
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -120,34 +297,13 @@ def main():
     wall = time.perf_counter() - t0
     ev = mxfp8.GEMM_EVENTS
     mxfp8.GEMM_EVENTS = None
-    # untimed instrumented-event overhead is inside the wall time; report it anyway as measured
+    # the instrumented events' own overhead is inside the wall time; reported as measured
     gemm_ms = sum(a.elapsed_time(b) for a, b, _ in ev)
     gemm_fl = sum(f for _, _, f in ev)
     ms = wall * 1e3 / args.steps
-    fl = workloads.flops(T, K, N)
+    fl = workloads.flops(T, K, N) * len(mods)
     value = fl / (ms * 1e-3) / 1e12
     gemm_tf = gemm_fl / (gemm_ms * 1e-3) / 1e12
-    traffic = _traffic_from_profiles()
-
-    # quantizer: back-to-back launches over >= 1 ms
-    quant = {}
-    for name, shape in (("x[T,K]", (T, K)), ("dgu[T,2N]", (T, 2 * N))):
-        src = torch.randn(shape, device=dev).to(torch.bfloat16)
-        n = 200 if shape[1] == K else 40
-        for _ in range(5):
-            mxfp8.mx_quant(src)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(n):
-            mxfp8.mx_quant(src)
-        e1.record()
-        torch.cuda.synchronize()
-        qms = e0.elapsed_time(e1) / n
-        by = workloads.quant_bytes(*shape)
-        quant[name] = {"GB/s": round(by / (qms * 1e-3) / 1e9, 1), "us": round(qms * 1e3, 2), "bytes": by,
-                       "frac": round(by / (qms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-        del src
 
     line = {
         "metric": "MXFP8 MLP fwd+bwd TFLOP/s (% MXFP8 peak); quantizer GB/s (% of HBM)",
@@ -161,17 +317,29 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "mxfp8",
-        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights and LoRA A/B, N(0,1e-2) upstream grad)",
-        "config": {"workload": workloads.DESCRIPTIONS[CFG], "tokens": T, "d_model": K, "d_ffn": N,
-                   "lora_r": c["r"], "lora_alpha": c["alpha"], "frac_of_mxfp8_peak": round(value / PEAK_MXFP8_TFLOPS, 4)},
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights and LoRA A/B, N(0,1e-2) upstream grad)"
+                if cfg != 5 else "synthetic (seeded Student-t(3) activations with x100 channels, all-zero, -0 and "
+                                 "448*2^k blocks; N(0,0.02) weights and LoRA A/B)",
+        "config": {"workload": workloads.DESCRIPTIONS[cfg], "layers": len(mods), "tokens": T, "d_model": K,
+                   "d_ffn": N, "lora_r": c["r"], "lora_alpha": c["alpha"],
+                   "frac_of_mxfp8_peak": round(value / PEAK_MXFP8_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tf / PEAK_MXFP8_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "mx_gemm (4 launches per step: gate|up, down, dh, dx)",
+                     "frac": round(gemm_tf / PEAK_MXFP8_TFLOPS, 4), "traffic": _traffic_from_profiles(cfg),
+                     "kernel": "mx_gemm (4 launches per layer: gate|up, down, dh, dx)",
                      "launches": len(ev), "kernel_ms_per_step": round(gemm_ms / args.steps, 4)},
-        "quantizer": quant,
     }
+    del model, mods, params, x, dy
+    torch.cuda.empty_cache()
+    if not args.no_quant:
+        quant, wq_ms = _quantizer(T, K, N, dev)
+        line["quantizer"] = quant
+        tot = ms + wq_ms * c["layers"]
+        line["with_requant"] = {"ms_per_step": round(tot, 4), "TFLOP/s": round(fl / (tot * 1e-3) / 1e12, 2),
+                                "weight_prep_ms_per_layer": round(wq_ms, 4)}
+    if args.copy_calib:
+        _copy_calib(dev)
     if not args.no_cpu:
-        line["cpu_baseline"] = _cpu_baseline(args.cpu_tokens)
+        line["cpu_baseline"] = _cpu_baseline(cfg, args.cpu_tokens)
     print(json.dumps(line), flush=True)
 
 

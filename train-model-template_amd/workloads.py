@@ -109,20 +109,22 @@ def _student_t(shape, seed, scale=1.0):
     return x, rng
 
 
-def make_inputs(cfg, T=None, layer=0, dy=True):
+def make_inputs(cfg, T=None, layer=0, dy=True, x=True):
     """CPU tensors for one layer of configuration ``cfg`` (1..5).  ``T`` overrides the token count (row
-    subsets of the same shape).  Returns dict(x, Wg, Wu, Wd, Ag, Bg, Au, Bu, Ad, Bd, dy, s, T, K, N, r)."""
+    subsets of the same shape).  Returns dict(x, Wg, Wu, Wd, Ag, Bg, Au, Bu, Ad, Bd, dy, s, T, K, N, r);
+    ``x=False`` / ``dy=False`` leave out the activation / upstream gradient (layers > 0 of a stack)."""
     c = CONFIGS[cfg]
     T = c["T"] if T is None else T
     K, N, r = c["K"], c["N"], c["r"]
     s = c["alpha"] / r
     out = dict(T=T, K=K, N=N, r=r, s=s)
-    if c.get("outliers"):
-        xf, rng = _student_t((T, K), seed_of(cfg, "x", layer))
-        xf = torch.from_numpy(_outlier_blocks(xf, rng))
-    else:
-        xf = _normal((T, K), 1.0, seed_of(cfg, "x", layer))
-    out["x"] = xf.to(torch.bfloat16)
+    if x:
+        if c.get("outliers"):
+            xf, rng = _student_t((T, K), seed_of(cfg, "x", layer))
+            xf = torch.from_numpy(_outlier_blocks(xf, rng))
+        else:
+            xf = _normal((T, K), 1.0, seed_of(cfg, "x", layer))
+        out["x"] = xf.to(torch.bfloat16)
     out["Wg"] = _normal((N, K), 0.02, seed_of(cfg, "Wg", layer)).to(torch.bfloat16)
     out["Wu"] = _normal((N, K), 0.02, seed_of(cfg, "Wu", layer)).to(torch.bfloat16)
     out["Wd"] = _normal((K, N), 0.02, seed_of(cfg, "Wd", layer)).to(torch.bfloat16)
@@ -218,11 +220,12 @@ class MLPStack(torch.nn.Module):
 
 def build_model(cfg, T=None, layers=1, device="cuda"):
     """(model, inputs) for `layers` independent seeded layers of configuration cfg, bf16 frozen weights and
-    fp32 LoRA parameters on `device`; inputs of layer 0 (x, dy) are returned on the CPU."""
+    fp32 LoRA parameters on `device`; inputs of layer 0 (x, dy) are returned on the CPU (the other layers'
+    dicts hold their weights only: a stack feeds each layer the previous layer's output)."""
     c = CONFIGS[cfg]
     mlps, inps = [], []
     for layer in range(layers):
-        inp = make_inputs(cfg, T=T, layer=layer, dy=(layer == 0))
+        inp = make_inputs(cfg, T=T, layer=layer, dy=(layer == 0), x=(layer == 0))
         m = SwiGLUMLP(inp, c["alpha"])
         for name in ("gate_proj", "up_proj", "down_proj"):
             getattr(m, name).base_layer.to(dtype=torch.bfloat16)
