@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 1
+#define MXFP8_MLP_ABI_VERSION 2
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 
@@ -58,6 +58,23 @@ int mxfp8_quant_dual(const void* x, int64_t rows, int64_t cols, int64_t ld_x, vo
                      void* st, void* stream);
 
 /*
+ * mxfp8_quant_rows for a whole [rows, cols] bf16 tensor with the codes in the MX-tiled layout: blocks of 16 rows
+ * x 64 codes stored as contiguous 1 KB, block (r/16, k/64) at ((r/16) * (cols/64) + k/64) * 1024; inside,
+ * row r%16 takes 64 bytes whose 16-byte chunk c sits at position c ^ ((r >> 2) & 3).  q holds
+ * ceil(rows/16)*16 rows (the padding rows are not written); scales as mxfp8_quant_rows (cols/128 tiles).
+ * Same codes and scales as the reference quantizer (/root/reference/scripts/mxfp8.py:46-86), another byte
+ * order: the operand layout of mxfp8_gemm_nt (layout bits), no reference counterpart as a layout.
+ */
+int mxfp8_quant_tiled(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, void* s, void* stream);
+
+/*
+ * Row-major codes [rows, cols] (row stride ld_q, cols % 64 == 0) -> the MX-tiled layout above into out
+ * (ceil(rows/16)*16 * cols bytes; padding rows zero).  Used for the frozen weights after enable_mxfp8's
+ * quantization (/root/reference/scripts/mxfp8.py:472-494); no reference counterpart as a layout.
+ */
+int mxfp8_tile_codes(const void* q, int64_t rows, int64_t cols, int64_t ld_q, void* out, void* stream);
+
+/*
  * out[rows, cols] (fp32, dense) = E4M3(q) * 2^(e - 127), NaN where the scale byte is 0xFF.
  * No reference counterpart as a function: the reference dequantizes only inside torch._scaled_mm
  * (/root/reference/scripts/fused_mlp.py:279); this exposes the same arithmetic for checks.
@@ -74,10 +91,27 @@ int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
  *   C = bf16( bf16(A·Bᵀ) + alpha * P[M, r] · Q[N, r]ᵀ ),  P, Q bf16 with row strides ld_p, ld_q,
  *   r in {16, 32, 64}.
  * Requires K % 128 == 0, N % 128 == 0, lda/ldb % 16 == 0, ldc % 4 == 0.
+ * layout: bit 0 set = A codes in the MX-tiled layout (mxfp8_quant_tiled / mxfp8_tile_codes, lda ignored),
+ * bit 1 = the same for B.  Results are bit-identical to the row-major operands; the tiled layout lets every
+ * DMA of the GEMM move a contiguous 1 KB instead of sixteen 64-byte row pieces.
+ * workspace (optional, 256-byte aligned, workspace_bytes long): when it holds at least
+ * mxfp8_gemm_workspace_size(M, N, K) bytes, the tiles of a last wave that would leave more than half of the
+ * CUs idle are split along K; their fp32 pieces go through the workspace and are added in a fixed order
+ * (the result does not depend on scheduling).  Its first 4 KB are arrival counters that must be zero before
+ * the first call (allocate it zeroed); every call leaves them zero.  Calls that share a workspace must not run
+ * concurrently.  NULL / too small: every tile runs whole (same result bits as with the split only where no
+ * tile was split).
  */
 int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
                   int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
-                  const void* lora_q, int64_t ld_q, int64_t r, float alpha, void* stream);
+                  const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of workspace mxfp8_gemm_nt uses for this shape on the current device (0: no split).  No reference
+ * counterpart: torch._scaled_mm (fused_mlp.py:279) manages the cuBLAS workspace itself.
+ */
+int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
 
 /*
  * Fused SwiGLU forward of the MLP after the gate|up MX GEMM (replaces _fwd_kernel / mlp_fwd,
@@ -87,11 +121,12 @@ int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, con
  *   q_h [T, N] + s_h (blocked, N/128 tiles per row, padded rows 0)   = MX(h)       (skipped if q_h == NULL)
  *   part [n_groups, T, r] fp32: xS_down partial sums h·adᵀ over the columns of each of n_groups groups
  *   h_out [T, N] bf16 (optional, may be NULL): h itself, for checks
+ *   q_layout: 0 = q_h row-major, 1 = MX-tiled (see mxfp8_quant_tiled; ceil(T/16)*16 rows)
  * Requires N % 128 == 0, (N / 32) % n_groups == 0, r in {16, 32}, T * 2N < 2^31.
  */
 int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu, const void* ad, int64_t T,
                   int64_t N, int64_t r, float s_g, float s_u, void* q_h, void* s_h, float* part, int64_t n_groups,
-                  void* h_out, void* stream);
+                  void* h_out, int64_t q_layout, void* stream);
 
 /*
  * Fused SwiGLU backward (replaces _bwd_kernel / mlp_bwd, /root/reference/scripts/fused_mlp.py:112-175,
@@ -104,12 +139,13 @@ int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu
  *   dbg_part, dbu_part [ceil(Tpad/SB), N, r] fp32 and dad_part [ceil(Tpad/SB), r, N]: per super-block sums of
  *     dgᵀ·xs_g, duᵀ·xs_u and (hᵀ·dxd)ᵀ (unscaled)
  *   dgu_out [T, 2N] bf16 (optional, may be NULL): dg | du themselves, for checks
+ *   q_layout: 0 = q row-major, 1 = MX-tiled with 2N codes per row (see mxfp8_quant_tiled)
  */
 int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, const void* dhm, const void* dxd,
                   const void* dxdT, const void* bg, const void* bu, const void* bgT, const void* buT, const void* ad,
                   const void* adT, int64_t T, int64_t N, int64_t r, float s_g, float s_u, int64_t SB, int64_t CG,
                   void* q, void* s, float* dxa_part, float* dbg_part, float* dbu_part, float* dad_part,
-                  void* dgu_out, void* stream);
+                  void* dgu_out, int64_t q_layout, void* stream);
 
 /*
  * out[i] = scale * Σ_{p=0..n_parts-1} part[p * count + i], summed in ascending p (deterministic), stored as

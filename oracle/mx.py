@@ -148,3 +148,35 @@ def dequant(q, s, rows, cols, n_col_tiles=None, ld=None):
     out = torch.ldexp(vals, (e - 127).unsqueeze(-1).to(torch.float32))
     out = torch.where((e == 255).unsqueeze(-1), torch.full_like(out, float("nan")), out)
     return out.view(rows, cols)
+
+
+def to_tiled(q):
+    """Row-major codes [R, K] (uint8, K % 64 == 0) -> the MX-tiled GEMM operand layout as a flat uint8 array of
+    ceil(R/16)*16*K bytes (padding rows zero): block (r//16, k//64) at ((r//16)*(K//64) + k//64)*1024, row r%16
+    at +64*(r%16) of it, and the block's 16-code chunk c of that row at position c ^ ((r >> 2) & 3).  Written as
+    a reshape/permute of the padded array.  No reference counterpart: the operand layout of this build's GEMM
+    (include/mxfp8_mlp.h, mxfp8_quant_tiled); the reference's codes are row-major (mxfp8.py:46-86)."""
+    q = np.asarray(q, dtype=np.uint8)
+    R, K = q.shape
+    Rp = -(-R // 16) * 16
+    a = np.zeros((Rp, K), np.uint8)
+    a[:R] = q
+    a = a.reshape(Rp // 16, 16, K // 64, 4, 16)  # [rg, r16, kb, chunk, byte]
+    out = np.empty_like(a)
+    for r in range(16):
+        sw = (r >> 2) & 3
+        for c in range(4):
+            out[:, r, :, c ^ sw, :] = a[:, r, :, c, :]
+    return np.ascontiguousarray(out.transpose(0, 2, 1, 3, 4)).reshape(-1)  # [rg, kb, r16, position, byte]
+
+
+def from_tiled(t, R, K):
+    """Inverse of to_tiled: the first R rows of row-major codes [R, K]."""
+    Rp = -(-R // 16) * 16
+    a = np.asarray(t, dtype=np.uint8).reshape(Rp // 16, K // 64, 16, 4, 16).transpose(0, 2, 1, 3, 4)
+    out = np.empty_like(a)
+    for r in range(16):
+        sw = (r >> 2) & 3
+        for c in range(4):
+            out[:, r, :, c, :] = a[:, r, :, c ^ sw, :]
+    return out.reshape(Rp, K)[:R]

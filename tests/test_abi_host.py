@@ -20,7 +20,7 @@ HEADER = os.path.join(ROOT, "include", "mxfp8_mlp.h")
 def _declared():
     txt = open(HEADER).read()
     txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(mxfp8_\w+)\s*\(", txt, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(mxfp8_\w+)\s*\(", txt, flags=re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 9, names
+    assert len(names) == 12, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -56,13 +56,37 @@ def test_argument_checks_reject_before_launch(lib):
     # null pointer
     assert lib.mxfp8_quant_rows(None, 4, 128, 128, p, 128, p, 1, 0, None) == -1
     # GEMM K not a multiple of 128
-    assert lib.mxfp8_gemm_nt(p, p, 96, p, p, 96, 4, 128, 96, p, 128, None, 0, None, 0, 0, 1.0, None) == -1
+    assert lib.mxfp8_gemm_nt(p, p, 96, p, p, 96, 4, 128, 96, p, 128, None, 0, None, 0, 0, 1.0, 0, None, 0, None) == -1
     # GEMM epilogue rank not supported
-    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, p, 8, p, 8, 8, 1.0, None) == -1
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, p, 8, p, 8, 8, 1.0, 0, None, 0, None) == -1
+    # unknown operand layout
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 4, None, 0, None) == -1
+    assert b"layout" in lib.mxfp8_last_error()
+    # workspace given but misaligned
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 0,
+                             ctypes.c_void_p(16), 1 << 20, None) == -1
+    assert b"workspace" in lib.mxfp8_last_error()
     # backward column group must divide N and be a multiple of 256
-    args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, None]
+    args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, 0, None]
     assert lib.mxfp8_mlp_bwd(*args) == -1
+    # tiled quantizer / tile_codes shape checks
+    assert lib.mxfp8_quant_tiled(p, 4, 100, 100, p, p, None) == -1
+    assert lib.mxfp8_tile_codes(p, 4, 96, 96, p, None) == -1
     assert lib.mxfp8_sum_parts(None, 1, 4, 1.0, p, 0, None) == -1
+
+
+def test_gemm_workspace_plan(lib):
+    # without a GPU the library plans for 256 CUs (MI355X): tail waves that fill at most half of the CUs are
+    # split along K into up to 4 pieces of an even number of 64-wide K steps; 4 KB of counters come first
+    ws = lib.mxfp8_gemm_workspace_size
+    part = 256 * 256 * 4
+    assert ws(10752, 12288, 2048) == 0  # 2016 tiles: last wave 224 of 256 CUs
+    assert ws(10752, 6144, 2048) == 0   # 1008 tiles: last wave 240
+    assert ws(10752, 2048, 12288) == 4096 + 80 * 3 * part  # 336 tiles: 80 split in 3 (64 steps each)
+    assert ws(10752, 2048, 6144) == 4096 + 80 * 3 * part
+    assert ws(256, 7168, 1024) == 4096 + 28 * 4 * part  # 28 tiles: 4 pieces of 4 steps
+    assert ws(256, 1024, 128) == 0  # 2 K steps cannot be split into pieces of at least 4
+    assert ws(0, 128, 128) == 0 and ws(4, 100, 128) == 0
 
 
 def test_native_refuses_cpu_tensors(lib):

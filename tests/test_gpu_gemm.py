@@ -97,3 +97,63 @@ def test_gemm_lora_epilogue(r, gpu):
     ref = (c0.float().cpu() + 2.0 * (P.float() @ Q.float().t())).to(torch.bfloat16).float()
     err = (c.float().cpu() - ref).abs()
     assert (err <= ref.abs() * 2.0 ** -7 + 1e-4).all(), err.max()
+
+
+def _operands(M, N, K, seed, gpu):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    return mxfp8.mx_quant(a) + mxfp8.mx_quant(b)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 7168, 1024), (1000, 1024, 3584), (10752, 2048, 6144)])
+def test_gemm_split_tail(M, N, K, gpu):
+    # tail tiles split along K (the workspace plan) against every tile run whole: the same exact products
+    # summed in another fp32 order, so at most one bf16 step apart; repeated split runs are bit-identical
+    # (pieces are added in part order, whatever order they finish in) and leave the counters at zero
+    import _native
+    assert _native.load().mxfp8_gemm_workspace_size(M, N, K) > 0
+    qa, sa, qb, sb = _operands(M, N, K, M + N + K, gpu)
+    whole = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+    _native.gemm_nt(qa, sa, K, qb, sb, K, M, N, K, whole, split=False)
+    c1, c2 = mxfp8.mx_mm(qa, sa, qb, sb), mxfp8.mx_mm(qa, sa, qb, sb)
+    assert torch.equal(c1, c2)
+    ws, _ = _native.gemm_workspace(M, N, K, c1.device)
+    assert int(torch.count_nonzero(ws[:4096])) == 0
+    w, s = whole.float(), c1.float()
+    assert bool(((w - s).abs() <= w.abs() * 2.0 ** -7 + 1e-6 * w.abs().max()).all())
+    if M * N <= 1 << 21:
+        _assert_close(c1, _ref_gemm_f64(qa, sa, qb, sb, M, N, K))
+
+
+def test_gemm_split_lora_epilogue(gpu):
+    # the rank-r epilogue runs once, in the piece that finishes a split tile
+    M, N, K, r = 512, 1024, 2048, 32
+    qa, sa, qb, sb = _operands(M, N, K, 77, gpu)
+    g = torch.Generator().manual_seed(78)
+    P = torch.randn(M, r, generator=g).to(torch.bfloat16)
+    Q = (torch.randn(N, r, generator=g) * 0.5).to(torch.bfloat16)
+    import _native
+    assert _native.load().mxfp8_gemm_workspace_size(M, N, K) > 0
+    c0 = mxfp8.mx_mm(qa, sa, qb, sb)
+    c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P.to(gpu), Q.to(gpu)), alpha=2.0)
+    ref = (c0.float().cpu() + 2.0 * (P.float() @ Q.float().t())).to(torch.bfloat16).float()
+    err = (c.float().cpu() - ref).abs()
+    assert (err <= ref.abs() * 2.0 ** -7 + 1e-4).all(), err.max()
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 384, 512), (1000, 1024, 3584), (4096, 2048, 1024)])
+def test_gemm_tiled_operands_bit_identical(M, N, K, gpu):
+    # MX-tiled A and/or B leave the same bytes in LDS as row-major operands: identical results, bit for bit
+    qa, sa, qb, sb = _operands(M, N, K, 3 * M + N, gpu)
+    ref = mxfp8.mx_mm(qa, sa, qb, sb)
+    ta, tb = mxfp8.tile_codes(qa), mxfp8.tile_codes(qb)
+    for layout, a, b in ((1, ta, qb), (2, qa, tb), (3, ta, tb)):
+        c = mxfp8.mx_mm(a, sa, b, sb, layout=layout, m=M)
+        assert torch.equal(c, ref), layout
+    # and with the rank-r epilogue
+    g = torch.Generator().manual_seed(M)
+    P = torch.randn(M, 16, generator=g).to(torch.bfloat16).to(gpu)
+    Q = torch.randn(N, 16, generator=g).to(torch.bfloat16).to(gpu)
+    assert torch.equal(mxfp8.mx_mm(ta, sa, tb, sb, lora=(P, Q), alpha=2.0, layout=3, m=M),
+                       mxfp8.mx_mm(qa, sa, qb, sb, lora=(P, Q), alpha=2.0))

@@ -7,6 +7,7 @@ Bars (north star):
     summation order of the rank-r products and exp/division ulps);
   - GEMM/MLP outputs and LoRA gradients: max|Δ| / max|ref| <= 2e-2 against the oracle's dequantize-then-
     matmul path (TOL below)."""
+import numpy as np
 import pytest
 import torch
 
@@ -117,6 +118,10 @@ def test_fwd_kernel_elementwise_and_codes(cfg, T, gpu):
     # xS_down = bf16(h · adᵀ) from the GPU's own h
     ref = (h.cpu().double() @ ad.double().t())
     assert _rel(xsd, ref) <= 1e-2
+    # the MX-tiled output (the GEMM operand layout of the fused path) holds the same codes
+    qt, st, xsd_t = fused_mlp.mlp_fwd(g(f["gu"]), g(f["xs"]), g(bg), g(bu), g(ad), s, s, True, tiled=True)
+    assert torch.equal(st, sh) and torch.equal(xsd_t, xsd)
+    assert np.array_equal(mx.from_tiled(qt.view(torch.uint8).cpu().numpy().reshape(-1), T, N), qr.numpy())
 
 
 @pytest.mark.parametrize("cfg,T", [(2, 512), (3, 300), (5, 1024)])
@@ -132,6 +137,10 @@ def test_bwd_kernel_elementwise_and_codes(cfg, T, gpu):
     assert fg < 1e-2 and fu < 1e-2
     qr, sr = mx.quant(dgu.cpu())
     assert torch.equal(q.view(torch.uint8).cpu(), qr) and torch.equal(sc.view(torch.uint8).cpu(), sr)
+    qt, sct = fused_mlp.mlp_bwd(g(f["gu"]), g(f["xs"]), g(b["dhm"]), g(b["dxd"]), g(bg), g(bu), g(ad), s, s, True,
+                                tiled=True)[:2]
+    assert torch.equal(sct, sc)
+    assert np.array_equal(mx.from_tiled(qt.view(torch.uint8).cpu().numpy().reshape(-1), T, 2 * N), qr.numpy())
     # partial-sum products from the GPU's own dg / du and the oracle's h, in float64
     dg64, du64 = dgu[:, :N].cpu().double(), dgu[:, N:].cpu().double()
     h64 = b["h"].double()

@@ -1,6 +1,7 @@
 """GPU parity of the MX quantizer kernels (libmxfp8_mlp.so via mxfp8.py) against the CPU oracle: codes and
 scales must be bit-exact (north star), on the benchmark configurations' activations, the outlier config, the
 frozen-weight dual-axis path, column-slice destinations and edge shapes."""
+import numpy as np
 import pytest
 import torch
 
@@ -110,3 +111,28 @@ def test_dequant_matches_oracle(gpu):
     ref = mx.dequant(qr, sr, 512, inp["K"])
     assert torch.equal(torch.isnan(d), torch.isnan(ref))
     assert torch.equal(d.nan_to_num(), ref.nan_to_num())
+
+
+@pytest.mark.parametrize("T,K", [(1, 128), (45, 384), (300, 1024), (8896, 2048)])
+def test_quant_tiled_layout(T, K, gpu):
+    # the GEMM operand layout: the same codes and scales as the oracle, bytes in the MX-tiled order
+    g = torch.Generator().manual_seed(T + K)
+    x = (torch.randn(T, K, generator=g) * torch.exp2(torch.randint(-10, 10, (T, 1), generator=g).float()))
+    x = x.to(torch.bfloat16)
+    q, s = mxfp8.mx_quant_tiled(x.to(gpu))
+    qr, sr = mx.quant(x)
+    assert torch.equal(_bytes(s), sr)
+    assert q.shape == (mxfp8.tiled_rows(T), K)
+    qt = _bytes(q).numpy().reshape(-1)
+    ref = mx.to_tiled(qr.numpy())
+    live = mx.from_tiled(qt, T, K)  # padding rows are not written by the quantizer
+    assert np.array_equal(live, qr.numpy())
+    assert np.array_equal(qt.reshape(-1, K)[:T // 16 * 16], ref.reshape(-1, K)[:T // 16 * 16])
+
+
+@pytest.mark.parametrize("R,K", [(128, 128), (6144, 2048), (37, 640)])
+def test_tile_codes(R, K, gpu):
+    g = torch.Generator().manual_seed(R * K)
+    q = torch.randint(0, 256, (R, K), generator=g, dtype=torch.uint8)
+    out = mxfp8.tile_codes(q.to(gpu).view(torch.float8_e4m3fn))
+    assert np.array_equal(_bytes(out).numpy().reshape(-1), mx.to_tiled(q.numpy()))

@@ -235,3 +235,27 @@ def test_column_slice_store_matches_separate_quant():
     mx.quant_into(du, q, s, N, 2 * N // 128)
     q2, s2 = mx.quant(torch.cat([dg, du], 1))
     assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+def test_tiled_layout_is_the_gemm_lds_image():
+    # The MX-tiled layout must hold, for each 16-row x 64-code slice, exactly the 1 KB the GEMM's row-major DMA
+    # leaves in LDS: lane i of that DMA reads row i // 4 of the slice, logical 16-byte chunk
+    # (i % 4) ^ ((i // 16) % 4), and lands at byte 16 i.  Checked slice by slice on a ragged shape, plus the
+    # inverse and padding.
+    rng = np.random.default_rng(7)
+    R, K = 45, 192
+    q = rng.integers(0, 256, size=(R, K), dtype=np.uint8)
+    t = mx.to_tiled(q)
+    Rp = 48
+    assert t.size == Rp * K
+    qp = np.zeros((Rp, K), np.uint8)
+    qp[:R] = q
+    for rg in range(Rp // 16):
+        for kb in range(K // 64):
+            blk = t[(rg * (K // 64) + kb) * 1024:(rg * (K // 64) + kb + 1) * 1024]
+            for i in range(64):
+                row = rg * 16 + i // 4
+                c = (i % 4) ^ ((i // 16) % 4)
+                assert np.array_equal(blk[16 * i:16 * i + 16], qp[row, kb * 64 + 16 * c:kb * 64 + 16 * c + 16])
+    assert np.array_equal(mx.from_tiled(t, R, K), q)
+    assert not t.reshape(Rp // 16, K // 64, 16, 64)[-1, :, R - 32:].any()  # rows 45..47 are zero padding

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
 
@@ -21,16 +21,23 @@ SIGNATURES = {
     "mxfp8_last_error": [],
     "mxfp8_quant_rows": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr],
     "mxfp8_quant_dual": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr],
+    "mxfp8_quant_tiled": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr],
+    "mxfp8_tile_codes": [_ptr, _i64, _i64, _i64, _ptr, _ptr],
     "mxfp8_dequant": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _ptr],
     "mxfp8_gemm_nt": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
-                      _i64, _f32, _ptr],
-    "mxfp8_mlp_fwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _i64, _ptr, _ptr],
+                      _i64, _f32, _i64, _ptr, _i64, _ptr],
+    "mxfp8_gemm_workspace_size": [_i64, _i64, _i64],
+    "mxfp8_mlp_fwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _i64, _ptr, _i64,
+                      _ptr],
     "mxfp8_mlp_bwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32,
-                      _f32, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr],
+                      _f32, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr],
     "mxfp8_sum_parts": [_ptr, _i64, _i64, _f32, _ptr, _int, _ptr],
 }
 
+_RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64}
+
 _lib = None
+_WORKSPACE = {}  # (device index, stream) -> zero-initialised uint8 workspace of the MX GEMM
 
 
 class NativeError(RuntimeError):
@@ -49,7 +56,7 @@ def load(path=LIB_PATH):
     for name, args in SIGNATURES.items():
         fn = getattr(L, name)
         fn.argtypes = args
-        fn.restype = ctypes.c_char_p if name == "mxfp8_last_error" else _int
+        fn.restype = _RESTYPES.get(name, _int)
     v = L.mxfp8_abi_version()
     if v != ABI_VERSION:
         raise NativeError(f"{path}: ABI version {v}, expected {ABI_VERSION}; rebuild the library")
@@ -97,12 +104,39 @@ def quant_dual(x, q, s, qt, st):
     call("mxfp8_quant_dual", _p(x), R, C, x.stride(0), _p(q), _p(s), _p(qt), _p(st), like=x)
 
 
+def quant_tiled(x, q, s):
+    """x [R, C] bf16 -> codes in the MX-tiled layout into q (ceil(R/16)*16 * C bytes) and blocked scales."""
+    R, C = x.shape
+    call("mxfp8_quant_tiled", _p(x), R, C, x.stride(0), _p(q), _p(s), like=x)
+
+
+def tile_codes(q, rows, cols, out):
+    """Row-major codes (row stride q.stride(0)) -> the MX-tiled layout into out."""
+    call("mxfp8_tile_codes", _p(q), rows, cols, q.stride(0), _p(out), like=out)
+
+
 def dequant(q, s, rows, cols, ld_q, s_col_tiles, out):
     call("mxfp8_dequant", _p(q), rows, cols, ld_q, _p(s), s_col_tiles, _p(out), like=out)
 
 
-def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0):
-    """c[M, N] = bf16(A·Bᵀ) [+ alpha · P·Qᵀ with lora = (P [M, r], Q [N, r])]."""
+def gemm_workspace(M, N, K, device):
+    """The GEMM workspace for this shape on the current stream of `device`: one buffer per (device, stream),
+    grown on demand and allocated zeroed (its arrival counters must start at zero; every call leaves them
+    zero), so calls on one stream, which are ordered, share it safely."""
+    need = load().mxfp8_gemm_workspace_size(M, N, K)
+    if need <= 0:
+        return None, 0
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = ws
+    return ws, ws.numel()
+
+
+def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0, split=True, layout=0):
+    """c[M, N] = bf16(A·Bᵀ) [+ alpha · P·Qᵀ with lora = (P [M, r], Q [N, r])].  layout bit 0 / 1: A / B codes
+    MX-tiled.  split=False runs every tile whole (no workspace)."""
     if lora is None:
         p = q = None
         ldp = ldq = r = 0
@@ -110,20 +144,22 @@ def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0):
         p, q = lora
         r = p.shape[1]
         ldp, ldq = p.stride(0), q.stride(0)
+    _gpu(c, "mxfp8_gemm_nt")
+    ws, ws_bytes = gemm_workspace(M, N, K, c.device) if split else (None, 0)
     call("mxfp8_gemm_nt", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(p), ldp,
-         _p(q), ldq, r, float(alpha), like=c)
+         _p(q), ldq, r, float(alpha), layout, _p(ws), ws_bytes, like=c)
 
 
-def mlp_fwd(gu, xs, bg, bu, ad, T, N, r, s_g, s_u, q, s, part, n_groups, h_out=None):
+def mlp_fwd(gu, xs, bg, bu, ad, T, N, r, s_g, s_u, q, s, part, n_groups, h_out=None, q_layout=0):
     call("mxfp8_mlp_fwd", _p(gu), _p(xs), _p(bg), _p(bu), _p(ad), T, N, r, float(s_g), float(s_u), _p(q), _p(s),
-         _p(part), n_groups, _p(h_out), like=gu)
+         _p(part), n_groups, _p(h_out), q_layout, like=gu)
 
 
 def mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, r, s_g, s_u, SB, CG, q, s, dxa_part,
-            dbg_part, dbu_part, dad_part, dgu_out=None):
+            dbg_part, dbu_part, dad_part, dgu_out=None, q_layout=0):
     call("mxfp8_mlp_bwd", _p(gu), _p(xs), _p(xsT), _p(dhm), _p(dxd), _p(dxdT), _p(bg), _p(bu), _p(bgT), _p(buT),
          _p(ad), _p(adT), T, N, r, float(s_g), float(s_u), SB, CG, _p(q), _p(s), _p(dxa_part), _p(dbg_part),
-         _p(dbu_part), _p(dad_part), _p(dgu_out), like=gu)
+         _p(dbu_part), _p(dad_part), _p(dgu_out), q_layout, like=gu)
 
 
 def sum_parts(part, n_parts, count, out, scale=1.0):

@@ -100,10 +100,11 @@ __device__ __forceinline__ v16f lora_tile(const uint16_t* wrow, const v8bf* xf) 
 }
 
 // Quantize one 32-column block of the lane's row held as 8 packed bf16 pairs w[0..7] (columns
-// tile_col(2k), tile_col(2k+1)) plus the other 16 values in lane ^ 32: codes into q[m, jb..jb+31] (4-byte
-// pieces), scale byte into the blocked layout (lanes < 32), or scale 0 for padded rows.
-__device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, bool live, uint8_t* qrow, int jb,
-                                           uint8_t* s, int64_t s_col_tiles) {
+// tile_col(2k), tile_col(2k+1)) plus the other 16 values in lane ^ 32: codes of row mc, columns jb..jb+31
+// (4-byte pieces) into q, row-major with Kq codes per row or MX-tiled (tiled_offset) with Kq codes per row;
+// scale byte into the blocked layout (lanes < 32), or scale 0 for padded rows.
+__device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
+                                           int64_t Kq, bool tiled, int jb, uint8_t* s, int64_t s_col_tiles) {
   u16x2 mm = {0, 0};
 #pragma unroll
   for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
@@ -115,7 +116,10 @@ __device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, b
   for (int g = 0; g < 4; ++g) c[g] = encode4_bf16(w[2 * g], w[2 * g + 1], e);
   if (live) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) *reinterpret_cast<uint32_t*>(qrow + jb + g * 8 + (lane >> 5) * 4) = c[g];
+    for (int g = 0; g < 4; ++g) {
+      const int64_t k = jb + g * 8 + (lane >> 5) * 4;
+      *reinterpret_cast<uint32_t*>(q + (tiled ? tiled_offset(mc, k, Kq) : mc * Kq + k)) = c[g];
+    }
   }
   if (lane < 32) s[blocked_offset(m, jb >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
 }
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const uint16_t* __restrict__ g
                                                   const uint16_t* __restrict__ ad, int T, int N, int tiles_per_group,
                                                   float s_g, float s_u, uint8_t* __restrict__ q,
                                                   uint8_t* __restrict__ s, float* __restrict__ part,
-                                                  uint16_t* __restrict__ h_out) {
+                                                  uint16_t* __restrict__ h_out, bool q_tiled) {
   __shared__ float red[4][32][R];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lg = lane >> 5;
   const int m = blockIdx.x * 32 + (lane & 31);
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(const uint16_t* __restrict__ g
       hv[i + 1] = (g1 * fast_sigmoid(g1)) * u1;
       hw[i / 2] = rnd2(hv[i], hv[i + 1]);
     }
-    if (kWriteQ) quant_tile(hw, lane, m, live, q + (int64_t)mc * N, jb, s, N / 128);
+    if (kWriteQ) quant_tile(hw, lane, m, live, q, mc, N, q_tiled, jb, s, N / 128);
     if (h_out && live) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(512) void bwd_kernel(
     const uint16_t* __restrict__ buT, const uint16_t* __restrict__ ad, const uint16_t* __restrict__ adT, int T,
     int Tpad, int N, int SB, int CG, float s_g, float s_u, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
     float* __restrict__ dxa_part, float* __restrict__ dbg_part, float* __restrict__ dbu_part,
-    float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out) {
+    float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out, bool q_tiled) {
   __shared__ float red[8][32][3 * R];                               // per-wave dxa | dxa_u | xS products
   __shared__ __attribute__((aligned(16))) uint16_t tr[8][3][32][40];  // per-wave transposed dg, du, h [j][m]
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lg = lane >> 5;
@@ -282,9 +286,8 @@ __global__ __launch_bounds__(512) void bwd_kernel(
         }
       }
       if (kQuant) {
-        uint8_t* qrow = q + (int64_t)mc * 2 * N;
-        quant_tile(dgw, lane, m, live, qrow, jb, s, 2 * N / 128);
-        quant_tile(duw, lane, m, live, qrow, N + jb, s, 2 * N / 128);
+        quant_tile(dgw, lane, m, live, q, mc, 2 * N, q_tiled, jb, s, 2 * N / 128);
+        quant_tile(duw, lane, m, live, q, mc, 2 * N, q_tiled, N + jb, s, 2 * N / 128);
       }
       // dxa_g | dxa_u | xS_down products over this tile's 32 columns: D[ρ][m]
       v16f pg = v16f{}, pu = v16f{}, px = v16f{};
@@ -384,8 +387,9 @@ __global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict_
 
 extern "C" int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu, const void* ad, int64_t T,
                              int64_t N, int64_t r, float s_g, float s_u, void* q_h, void* s_h, float* part,
-                             int64_t n_groups, void* h_out, void* stream) {
+                             int64_t n_groups, void* h_out, int64_t q_layout, void* stream) {
   MX_CHECK_ARG(gu && xs && bg && bu && ad && part, "mxfp8_mlp_fwd: null pointer");
+  MX_CHECK_ARG(q_layout == 0 || q_layout == 1, "mxfp8_mlp_fwd: q_layout must be 0 (row-major) or 1 (MX-tiled)");
   MX_CHECK_ARG((q_h == nullptr) == (s_h == nullptr), "mxfp8_mlp_fwd: q_h and s_h go together");
   MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && (r == 16 || r == 32), "mxfp8_mlp_fwd: bad shape");
   MX_CHECK_ARG(T * 2 * N < (1LL << 31), "mxfp8_mlp_fwd: T * 2N must stay below 2^31");
@@ -399,7 +403,7 @@ extern "C" int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, con
   const int tpg = (int)(N / 32 / n_groups);
   hipStream_t stm = (hipStream_t)stream;
 #define FWD_ARGS (const uint16_t*)gu, (const uint16_t*)xs, (const uint16_t*)bg, (const uint16_t*)bu, (const uint16_t*)ad, \
-                 (int)T, (int)N, tpg, s_g, s_u, (uint8_t*)q_h, (uint8_t*)s_h, part, (uint16_t*)h_out
+                 (int)T, (int)N, tpg, s_g, s_u, (uint8_t*)q_h, (uint8_t*)s_h, part, (uint16_t*)h_out, q_layout == 1
   if (r == 16) {
     if (q_h) fwd_kernel<16, true><<<grid, 256, 0, stm>>>(FWD_ARGS);
     else fwd_kernel<16, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
@@ -416,7 +420,8 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                              const void* dxdT, const void* bg, const void* bu, const void* bgT, const void* buT,
                              const void* ad, const void* adT, int64_t T, int64_t N, int64_t r, float s_g, float s_u,
                              int64_t SB, int64_t CG, void* q, void* s, float* dxa_part, float* dbg_part,
-                             float* dbu_part, float* dad_part, void* dgu_out, void* stream) {
+                             float* dbu_part, float* dad_part, void* dgu_out, int64_t q_layout, void* stream) {
+  MX_CHECK_ARG(q_layout == 0 || q_layout == 1, "mxfp8_mlp_bwd: q_layout must be 0 (row-major) or 1 (MX-tiled)");
   MX_CHECK_ARG(gu && xs && xsT && dhm && dxd && dxdT && bg && bu && bgT && buT && ad && adT && dxa_part &&
                    dbg_part && dbu_part && dad_part,
                "mxfp8_mlp_bwd: null pointer");
@@ -436,7 +441,8 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
 #define BWD_ARGS (const uint16_t*)gu, (const uint16_t*)xs, (const uint16_t*)xsT, (const uint16_t*)dhm, (const uint16_t*)dxd, \
                  (const uint16_t*)dxdT, (const uint16_t*)bg, (const uint16_t*)bu, (const uint16_t*)bgT,                    \
                  (const uint16_t*)buT, (const uint16_t*)ad, (const uint16_t*)adT, (int)T, (int)Tpad, (int)N, (int)SB,     \
-                 (int)CG, s_g, s_u, (uint8_t*)q, (uint8_t*)s, dxa_part, dbg_part, dbu_part, dad_part, (uint16_t*)dgu_out
+                 (int)CG, s_g, s_u, (uint8_t*)q, (uint8_t*)s, dxa_part, dbg_part, dbu_part, dad_part, (uint16_t*)dgu_out, \
+                 q_layout == 1
   if (r == 16) {
     if (q) bwd_kernel<16, true><<<grid, 512, 0, stm>>>(BWD_ARGS);
     else bwd_kernel<16, false><<<grid, 512, 0, stm>>>(BWD_ARGS);

@@ -80,6 +80,16 @@ __device__ __forceinline__ int64_t blocked_offset(int64_t i, int64_t b, int64_t 
   return ((i >> 7) * n_col_tiles + (b >> 2)) * 512 + (i & 31) * 16 + ((i & 127) >> 5) * 4 + (b & 3);
 }
 
+// Byte offset of code (row r, column k) in the MX-tiled layout of an operand with K codes per row: blocks of
+// 16 rows x 64 codes stored as contiguous 1 KB, block (r/16, k/64) at ((r/16) * (K/64) + k/64) * 1024; inside
+// a block row r%16 takes 64 bytes whose 16-byte chunk c (codes 16c..16c+15 of the block) sits at position
+// c ^ ((r >> 2) & 3).  This is byte for byte the image the GEMM keeps in LDS for one 16-row slice of a K step
+// (the swizzle spreads a ds_read_b128 over the 64 banks), so one global_load_lds_dwordx4 moves a whole block.
+__device__ __forceinline__ int64_t tiled_offset(int64_t r, int64_t k, int64_t K) {
+  return ((r >> 4) * (K >> 6) + (k >> 6)) * 1024 + (r & 15) * 64 + ((((k >> 4) & 3) ^ ((r >> 2) & 3)) << 4) +
+         (k & 15);
+}
+
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

@@ -6,9 +6,18 @@
 //
 // Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile in K steps of 64 (two scale blocks).
 // The eight waves form a 2 (N) x 4 (M) grid of 128 x 64 sub-tiles, each a 4 x 2 grid of 32 x 32 MFMA tiles
-// (128 accumulators per lane); two waves share each SIMD so one's LDS reads overlap the other's MFMAs.
+// (128 accumulators per lane); two waves share each SIMD, so while one waits at a step's barrier or for its
+// LDS reads the other keeps the matrix pipe busy (measured: with one wave per SIMD and 128 x 128
+// sub-tiles the per-step barrier drains the pipe and the kernel is slower, although it reads LDS less).
 // The matrix instruction takes the weight (B) fragment as its first operand, so each lane's accumulators
 // cover one output row m and 16 columns n in runs of 4.
+//
+// Operand layouts: row-major codes (row stride lda / ldb), or the MX-tiled layout (tiled_offset in
+// mx_device.h) in which each 16-row x 64-code slice is one contiguous 1 KB block in LDS order.  The GEMM is
+// bound by how fast the DMA brings operands from L2: measured with the MFMAs removed, the tiled layout moves
+// the same bytes in ~0.7x the time of the row-major one (64-byte row pieces use half of each 128-byte line
+// per request), and the full GEMM gains 10-25%.  Both layouts leave the same bytes in LDS, so results are
+// bit-identical.
 //
 // Operand staging: global memory goes straight into LDS with global_load_lds_dwordx4 (no VGPR round trip)
 // through a ring of 4 stages of 34 KB: A codes 256 x 64 B, B codes 256 x 64 B, and the two 128-row blocked
@@ -21,6 +30,13 @@
 // Scale words: for a 32-row group the 16 bytes at (row % 32) * 16 of a blocked tile hold the four 32-row
 // groups' scales for one 128-wide K tile; a lane shifts its word by 8 * (lane / 32) so that op_sel 0 / 2
 // selects block 2P + lane/32 of the current half-tile P.
+// Work order: a 1-D grid in which workgroup i runs on XCD i % 8 (the dispatcher's round robin).  Tiles are
+// numbered in groups of kGroupM M-tiles (M fastest inside a group) and each XCD takes a contiguous range of
+// that order, so the ~32 tiles resident on one XCD share A and B panels in its L2.  When the last wave of
+// tiles would fill at most half of the CUs, those tail tiles are split along K into `parts` pieces run as
+// separate workgroups after the full tiles; each piece writes its fp32 accumulators to the caller's
+// workspace, and the piece that arrives last (agent-scope counter) adds the pieces in part order, which
+// makes the result independent of arrival order, runs the epilogue and resets its counter to zero.
 #include <type_traits>
 
 #include "abi_common.h"
@@ -34,6 +50,13 @@ constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4, kThreads = 512;
 constexpr int kCodeBytes = kBM * kBK;                 // 16 KB per operand per stage
 constexpr int kOffA = 0, kOffB = kCodeBytes, kOffSA = 2 * kCodeBytes, kOffSB = 2 * kCodeBytes + 1024;
 constexpr int kStageBytes = 2 * kCodeBytes + 2048;    // 34 KB
+constexpr int kGroupM = 4;
+constexpr int kMaxParts = 4;
+constexpr int64_t kPartBytes = (int64_t)kBM * kBN * 4;  // fp32 partial tile
+// Workspace layout: arrival counters at a fixed place (so every shape finds its own counters at zero, each
+// launch resets those it used), fp32 partial tiles after them.
+constexpr int64_t kCounterBytes = 4096;
+constexpr int kMaxSplitTiles = (int)(kCounterBytes / 4);
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -64,6 +87,26 @@ struct Lora {
   float alpha;
 };
 
+// Launch plan (computed on the host, see make_plan).
+struct Plan {
+  int tm, tn;        // tiles along M and N
+  int full;          // logical tiles [0, full) run whole
+  int per_full;      // full tiles per XCD (ceil(full / 8)); grid part one = 8 * per_full workgroups
+  int nsplit;        // logical tiles [full, full + nsplit) split along K
+  int parts;         // pieces per split tile
+  int chunk;         // K steps per piece (even)
+  int per_split;     // pieces per XCD (ceil(nsplit * parts / 8))
+  float4* ws;        // [nsplit][parts][8 waves][32][64 lanes] float4 partial accumulators
+  int* cnt;          // [nsplit] arrival counters (zero between launches)
+};
+
+__device__ __forceinline__ void tile_coords(int t, int tm, int tn, int& mt, int& nt) {
+  const int g = t / (kGroupM * tn), r = t - g * (kGroupM * tn);
+  const int rows = min(kGroupM, tm - g * kGroupM);
+  mt = g * kGroupM + r % rows;
+  nt = r / rows;
+}
+
 // 32 bytes of one operand row for the stage's 64-wide K step: chunk c0 (k 16*(l/32)..) and c0 + 2 (k 32 + ..)
 __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw) {
   uint4 lo = *reinterpret_cast<const uint4*>(base + row * kBK + ((c0 ^ sw) << 4));
@@ -79,13 +122,35 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
                                                         const uint8_t* __restrict__ SA, int64_t lda,
                                                         const uint8_t* __restrict__ B,
                                                         const uint8_t* __restrict__ SB, int64_t ldb, int M, int N,
-                                                        int K, uint16_t* __restrict__ C, int64_t ldc, Lora lora) {
+                                                        int K, uint16_t* __restrict__ C, int64_t ldc, Lora lora,
+                                                        Plan plan, int tiled) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageBytes];
+  __shared__ int arrived;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wn = wave >> 2, wm = wave & 3;  // compute sub-tile: n rows wn*128 + [0,128), m rows wm*64 + [0,64)
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
-  const int ns = K / kBK;  // even: K % 128 == 0
+
+  // ---- which tile (and which K piece) this workgroup computes
+  const int ns_all = K / kBK;  // even: K % 128 == 0
+  int tile, part = -1, s_begin = 0, s_end = ns_all;
+  {
+    const int i = blockIdx.x, x = i & 7, j = i >> 3;
+    if (i < 8 * plan.per_full) {
+      tile = x * plan.per_full + j;
+      if (tile >= plan.full) return;
+    } else {
+      const int jj = (i - 8 * plan.per_full) >> 3;
+      const int u = x * plan.per_split + jj;
+      if (jj >= plan.per_split || u >= plan.nsplit * plan.parts) return;
+      tile = plan.full + u / plan.parts;
+      part = u % plan.parts;
+      s_begin = part * plan.chunk;
+      s_end = min(ns_all, s_begin + plan.chunk);
+    }
+  }
+  int mt_, nt_;
+  tile_coords(tile, plan.tm, plan.tn, mt_, nt_);
+  const int m0 = mt_ * kBM, n0 = nt_ * kBN;
   const int nkt = K / 128;
 
   // DMA roles: waves 0-3 stage A, waves 4-7 stage B; wave slot w4 = wave & 3 covers rows w4*64 + [0, 64)
@@ -94,13 +159,25 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   const int w4 = wave & 3;
   const int R0 = dB ? n0 : m0, Rn = dB ? N : M;
   const int64_t ldd = dB ? ldb : lda;
-  const uint8_t* gb = (dB ? B : A) + (int64_t)R0 * ldd;
+  // Row-major operand: lane -> row slice*16 + lane/4 of the wave's rows, logical chunk chosen so that the
+  // lane's 16 bytes land at their swizzled LDS position.  MX-tiled operand (tiled_offset in mx_device.h):
+  // the slice is one contiguous 1 KB block already in LDS order, lane i copies bytes 16i..16i+15, and a K
+  // step advances 1 KB instead of 64 B.
+  const bool op_tiled = (tiled >> (dB ? 1 : 0)) & 1;
+  const int kst = K / kBK;
+  const uint8_t* gb = (dB ? B : A) + (op_tiled ? (int64_t)(R0 >> 4) * kst * 1024 : (int64_t)R0 * ldd);
+  const int sstride = op_tiled ? 1024 : kBK;
   const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3 for these rows
   uint32_t goff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int row = w4 * 64 + j * 16 + (lane >> 2);
-    goff[j] = (uint32_t)((min(R0 + row, Rn - 1) - R0) * ldd) + lchunk * 16;  // clamp rows past the end
+    if (op_tiled) {
+      const int rg = min((R0 >> 4) + w4 * 4 + j, ((Rn + 15) >> 4) - 1) - (R0 >> 4);  // clamp past the end
+      goff[j] = (uint32_t)(rg * kst * 1024) + lane * 16;
+    } else {
+      const int row = w4 * 64 + j * 16 + (lane >> 2);
+      goff[j] = (uint32_t)((min(R0 + row, Rn - 1) - R0) * ldd) + lchunk * 16;  // clamp rows past the end
+    }
   }
   // Fifth DMA of the stage, without divergence: waves 0 and 4 copy the two 128-row scale tiles of their
   // operand (1 KB, lane -> tile lane / 32, bytes (lane % 32) * 16 of it); the other waves repeat their fourth
@@ -114,7 +191,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   const uint32_t lds0 = lds_addr(lds);
   auto issue_to = [&](int s, int slot) {  // DMA stage s into ring slot `slot`
     const uint32_t st = lds0 + slot * kStageBytes;
-    const uint8_t* g = gb + s * kBK;
+    const uint8_t* g = gb + s * sstride;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(g + goff[j], st + dma_code_off + j * 1024);
     dma16(scl ? sgp + (s >> 1) * 512 : g + goff[3], st + dma5_off);
@@ -168,31 +245,74 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   // run stage s's MFMAs from registers, so LDS latency and the DMA issue overlap the matrix work.  Every step
   // issues five DMA instructions per wave; stages past the end re-load the last stage into the slot just
   // consumed (no later step reads it), so exactly two stages are in flight behind the one waited for.
+  const int last = s_end - 1;
   auto step = [&](int s, Frags& cur, Frags& nxt, auto pc) {
     wait_vmcnt<10>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     // Bare s_barrier: __syncthreads() adds a workgroup fence that waits for every outstanding DMA
     // (vmcnt(0)), which would drain the ring.
     __builtin_amdgcn_s_barrier();
-    issue_to(min(s + 4, ns - 1), s & (kStages - 1));
-    read((s + 1) & (kStages - 1), nxt);
+    issue_to(min(s + 4, last), (s - s_begin) & (kStages - 1));
+    read((s + 1 - s_begin) & (kStages - 1), nxt);
     mma(cur, pc);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  issue_to(0, 0);
-  issue_to(min(1, ns - 1), 1);
-  issue_to(min(2, ns - 1), 2);
-  issue_to(min(3, ns - 1), 3);
-  wait_vmcnt<15>();  // stage 0 landed
+  issue_to(s_begin, 0);
+  issue_to(min(s_begin + 1, last), 1);
+  issue_to(min(s_begin + 2, last), 2);
+  issue_to(min(s_begin + 3, last), 3);
+  wait_vmcnt<15>();  // stage s_begin landed
   __builtin_amdgcn_s_barrier();
   Frags f0, f1;
   read(0, f0);
-  for (int s = 0; s < ns; s += 2) {
+  for (int s = s_begin; s < s_end; s += 2) {
     step(s, f0, f1, std::integral_constant<int, 0>{});
     step(s + 1, f1, f0, std::integral_constant<int, 1>{});
   }
   wait_vmcnt<0>();  // drain the redundant tail loads before the workgroup can exit
+
+  if (part >= 0) {
+    // split tile: publish this piece, and let the last piece to arrive finish the tile
+    const int st_ = tile - plan.full;
+    float4* wsp = plan.ws + (((int64_t)st_ * plan.parts + part) * 8 + wave) * (32 * 64) + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          wsp[((i * 2 + j) * 4 + q) * 64] =
+              make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    __syncthreads();  // every wave's stores have completed (workgroup release)
+    if (tid == 0)
+      arrived = __hip_atomic_fetch_add(plan.cnt + st_, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != plan.parts - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // see the other pieces' stores
+    const float4* wsb = plan.ws + ((int64_t)st_ * plan.parts * 8 + wave) * (32 * 64) + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int p = 0; p < plan.parts; ++p) {
+            const float4 v = p == part ? make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                                     acc[i][j][4 * q + 3])
+                                       : wsb[(int64_t)p * 8 * 32 * 64 + ((i * 2 + j) * 4 + q) * 64];
+            if (p == 0) {
+              t = v;
+            } else {
+              t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+            }
+          }
+          acc[i][j][4 * q] = t.x; acc[i][j][4 * q + 1] = t.y; acc[i][j][4 * q + 2] = t.z;
+          acc[i][j][4 * q + 3] = t.w;
+        }
+    if (tid == 0) __hip_atomic_store(plan.cnt + st_, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
   // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]
@@ -235,22 +355,74 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   }
 }
 
+int cached_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// Split the tail wave along K when it would leave more than half of the CUs idle (one workgroup per CU:
+// the LDS ring takes 136 KB).  Returns the workspace bytes the plan needs (0 without a split).
+int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
+  p.tm = (int)((M + kBM - 1) / kBM);
+  p.tn = (int)((N + kBN - 1) / kBN);
+  const int total = p.tm * p.tn, ns = (int)(K / kBK);
+  const int rem = total % cus;
+  p.full = total;
+  p.nsplit = 0;
+  p.parts = 1;
+  p.chunk = ns;
+  if (rem > 0 && 2 * rem <= cus && rem <= kMaxSplitTiles) {
+    int parts = min(kMaxParts, cus / rem);
+    int chunk = 2 * ((ns + 2 * parts - 1) / (2 * parts));
+    parts = (ns + chunk - 1) / chunk;
+    if (parts >= 2 && chunk >= 4) {
+      p.full = total - rem;
+      p.nsplit = rem;
+      p.parts = parts;
+      p.chunk = chunk;
+    }
+  }
+  p.per_full = (p.full + 7) / 8;
+  p.per_split = (p.nsplit * p.parts + 7) / 8;
+  if (!p.nsplit) return 0;
+  return kCounterBytes + (int64_t)p.nsplit * p.parts * kPartBytes;
+}
+
 }  // namespace
+
+extern "C" int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 128 || N % 128) return 0;
+  Plan p;
+  return make_plan(M, N, K, cached_cus(), p);
+}
 
 extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
                              int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
-                             const void* lora_q, int64_t ld_q, int64_t r, float alpha, void* stream) {
+                             const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
   MX_CHECK_ARG(a && sa && b && sb && c, "mxfp8_gemm_nt: null pointer");
   MX_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 128 == 0 && N % 128 == 0,
                "mxfp8_gemm_nt: need K %% 128 == 0 and N %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                (long long)N, (long long)K);
   MX_CHECK_ARG(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "mxfp8_gemm_nt: dimension too large");
+  MX_CHECK_ARG(layout >= 0 && layout <= 3, "mxfp8_gemm_nt: layout must be 0..3 (bit 0: A MX-tiled, bit 1: B)");
+  if (layout & 1) lda = K;  // the tiled layout has no row stride
+  if (layout & 2) ldb = K;
   MX_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0 && ldc >= N && ldc % 4 == 0,
                "mxfp8_gemm_nt: bad strides");
   MX_CHECK_ARG(256LL * lda < (1LL << 32) && 256LL * ldb < (1LL << 32), "mxfp8_gemm_nt: stride too large");
   MX_CHECK_ARG(mx_aligned(a, 16) && mx_aligned(b, 16) && mx_aligned(sa, 16) && mx_aligned(sb, 16) &&
                    mx_aligned(c, 8),
                "mxfp8_gemm_nt: misaligned buffer");
+  MX_CHECK_ARG(workspace_bytes >= 0 && (workspace_bytes == 0 || (workspace && mx_aligned(workspace, 256))),
+               "mxfp8_gemm_nt: workspace must be 256-byte aligned");
   if (lora_p) {
     MX_CHECK_ARG(lora_q && (r == 16 || r == 32 || r == 64), "mxfp8_gemm_nt: epilogue needs P, Q and r in {16, 32, 64}");
     MX_CHECK_ARG(ld_p >= r && ld_q >= r && ld_p % 8 == 0 && ld_q % 8 == 0 && mx_aligned(lora_p, 16) &&
@@ -258,18 +430,35 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
                  "mxfp8_gemm_nt: bad epilogue strides/alignment");
   }
   if (M == 0) return MXFP8_OK;
-  dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
+  Plan plan;
+  const int64_t need = make_plan(M, N, K, cached_cus(), plan);
+  if (need > workspace_bytes) {  // no (or too small a) workspace: run every tile whole
+    plan.full = plan.tm * plan.tn;
+    plan.per_full = (plan.full + 7) / 8;
+    plan.nsplit = 0;
+    plan.per_split = 0;
+    plan.parts = 1;
+  }
+  plan.cnt = plan.nsplit ? (int*)workspace : nullptr;
+  plan.ws = plan.nsplit ? (float4*)((char*)workspace + kCounterBytes) : nullptr;
+  dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
   Lora lo{(const uint16_t*)lora_p, ld_p, (const uint16_t*)lora_q, ld_q, alpha};
   hipStream_t stm = (hipStream_t)stream;
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+  uint16_t* Cp = (uint16_t*)c;
   if (!lora_p)
-    gemm_kernel<0><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+    gemm_kernel<0><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
+                                                (int)layout);
   else if (r == 16)
-    gemm_kernel<16><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+    gemm_kernel<16><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
+                                                (int)layout);
   else if (r == 32)
-    gemm_kernel<32><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+    gemm_kernel<32><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
+                                                (int)layout);
   else
-    gemm_kernel<64><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo);
+    gemm_kernel<64><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
+                                                (int)layout);
   MX_CHECK_LAUNCH("mxfp8_gemm_nt");
   return MXFP8_OK;
 }

@@ -5,6 +5,8 @@
 // /root/reference/scripts/fused_mlp.py:40-62 (_mx_store column slices).  Bytes are identical to the
 // reference arithmetic described in mx_device.h.
 //
+// Codes go out row-major or in the MX-tiled layout the GEMM streams (tiled_offset in mx_device.h).
+//
 // Work decomposition: one 256-thread workgroup per 128 x 128 tile, which is exactly one 512-byte scale tile.
 // Each thread owns 8 consecutive columns (one 16-byte load) of 8 rows; the 4 threads of a 32-column block
 // reduce their amax with two lane swaps.  The tile's scale bytes are assembled in LDS and leave as one
@@ -39,7 +41,7 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
                                                          int64_t ld_x, uint8_t* __restrict__ q, int64_t ld_q,
                                                          uint8_t* __restrict__ s, int64_t s_col_tiles,
                                                          int64_t s_tile0, uint8_t* __restrict__ qt,
-                                                         uint8_t* __restrict__ st) {
+                                                         uint8_t* __restrict__ st, int64_t tk) {
   __shared__ uint32_t stile[kTile];                          // row-axis scale tile (512 B)
   __shared__ uint32_t sttile[kTile];                         // transposed-axis scale tile
   __shared__ __attribute__((aligned(16))) uint16_t xt[kCols ? kTile * kLdT : 1];
@@ -69,7 +71,8 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
       uint32_t e;
       uint2 codes = quant8(v[it], e);
       if (r < rows) {
-        *reinterpret_cast<uint2*>(q + r * ld_q + col) = codes;
+        // row-major (row stride ld_q), or the MX-tiled layout with tk codes per row
+        *reinterpret_cast<uint2*>(q + (tk ? tiled_offset(r, col, tk) : r * ld_q + col)) = codes;
         if ((tid & 3) == 0) sb[(rl & 31) * 16 + (rl >> 5) * 4 + (c8 >> 5)] = (uint8_t)e;
       }
     }
@@ -151,6 +154,21 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t* __rest
   *reinterpret_cast<float4*>(out + idx) = o;
 }
 
+// Row-major codes [rows, cols] (row stride ld_q) -> the MX-tiled layout (ceil(rows/16)*16 rows; the rows
+// past `rows` in the last 16-row block are zero).  One thread per 16-byte chunk of the output.
+__global__ __launch_bounds__(kThreads) void tile_codes_kernel(const uint8_t* __restrict__ q, int64_t rows,
+                                                              int64_t cols, int64_t ld_q, uint8_t* __restrict__ out,
+                                                              int64_t n_chunks) {
+  const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (o >= n_chunks) return;
+  const int64_t blk = o >> 6, kbs = cols >> 6;
+  const int64_t r = (blk / kbs) * 16 + ((o >> 2) & 15), kb = blk % kbs;
+  const int c = (int)(o & 3) ^ (int)((r >> 2) & 3);
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (r < rows) v = *reinterpret_cast<const uint4*>(q + r * ld_q + kb * 64 + c * 16);
+  reinterpret_cast<uint4*>(out)[o] = v;
+}
+
 }  // namespace
 
 extern "C" int mxfp8_quant_rows(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, int64_t ld_q,
@@ -166,7 +184,7 @@ extern "C" int mxfp8_quant_rows(const void* x, int64_t rows, int64_t cols, int64
   MX_CHECK_ARG((rows + 127) / 128 <= 0x7fffffff, "mxfp8_quant_rows: too many rows");
   dim3 grid((unsigned)(cols / 128), (unsigned)((rows + 127) / 128));
   quant_kernel<true, false><<<grid, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)x, rows, ld_x, (uint8_t*)q, ld_q, (uint8_t*)s, s_col_tiles, s_tile0, nullptr, nullptr);
+      (const uint16_t*)x, rows, ld_x, (uint8_t*)q, ld_q, (uint8_t*)s, s_col_tiles, s_tile0, nullptr, nullptr, 0);
   MX_CHECK_LAUNCH("mxfp8_quant_rows");
   return MXFP8_OK;
 }
@@ -187,14 +205,46 @@ extern "C" int mxfp8_quant_dual(const void* x, int64_t rows, int64_t cols, int64
   hipStream_t stm = (hipStream_t)stream;
   if (q && qt)
     quant_kernel<true, true><<<grid, kThreads, 0, stm>>>((const uint16_t*)x, rows, ld_x, (uint8_t*)q, cols,
-                                                         (uint8_t*)s, cols / 128, 0, (uint8_t*)qt, (uint8_t*)st);
+                                                         (uint8_t*)s, cols / 128, 0, (uint8_t*)qt, (uint8_t*)st, 0);
   else if (q)
     quant_kernel<true, false><<<grid, kThreads, 0, stm>>>((const uint16_t*)x, rows, ld_x, (uint8_t*)q, cols,
-                                                          (uint8_t*)s, cols / 128, 0, nullptr, nullptr);
+                                                          (uint8_t*)s, cols / 128, 0, nullptr, nullptr, 0);
   else
     quant_kernel<false, true><<<grid, kThreads, 0, stm>>>((const uint16_t*)x, rows, ld_x, nullptr, 0, nullptr, 0,
-                                                          0, (uint8_t*)qt, (uint8_t*)st);
+                                                          0, (uint8_t*)qt, (uint8_t*)st, 0);
   MX_CHECK_LAUNCH("mxfp8_quant_dual");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_quant_tiled(const void* x, int64_t rows, int64_t cols, int64_t ld_x, void* q, void* s,
+                                 void* stream) {
+  MX_CHECK_ARG(x && q && s, "mxfp8_quant_tiled: null pointer");
+  MX_CHECK_ARG(rows >= 0 && cols > 0 && cols % 128 == 0, "mxfp8_quant_tiled: need cols %% 128 == 0 (cols=%lld)",
+               (long long)cols);
+  MX_CHECK_ARG(ld_x >= cols && ld_x % 8 == 0, "mxfp8_quant_tiled: bad ld_x=%lld", (long long)ld_x);
+  MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(q, 16) && mx_aligned(s, 16), "mxfp8_quant_tiled: misaligned buffer");
+  if (rows == 0) return MXFP8_OK;
+  MX_CHECK_ARG((rows + 127) / 128 <= 0x7fffffff, "mxfp8_quant_tiled: too many rows");
+  dim3 grid((unsigned)(cols / 128), (unsigned)((rows + 127) / 128));
+  quant_kernel<true, false><<<grid, kThreads, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x, rows, ld_x, (uint8_t*)q, 0, (uint8_t*)s, cols / 128, 0, nullptr, nullptr, cols);
+  MX_CHECK_LAUNCH("mxfp8_quant_tiled");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_tile_codes(const void* q, int64_t rows, int64_t cols, int64_t ld_q, void* out, void* stream) {
+  MX_CHECK_ARG(q && out, "mxfp8_tile_codes: null pointer");
+  MX_CHECK_ARG(rows >= 0 && cols > 0 && cols % 64 == 0 && ld_q >= cols && ld_q % 16 == 0,
+               "mxfp8_tile_codes: bad shape (rows=%lld cols=%lld ld_q=%lld)", (long long)rows, (long long)cols,
+               (long long)ld_q);
+  MX_CHECK_ARG(mx_aligned(q, 16) && mx_aligned(out, 16), "mxfp8_tile_codes: misaligned buffer");
+  if (rows == 0) return MXFP8_OK;
+  const int64_t n_chunks = (rows + 15) / 16 * 16 * cols / 16;
+  const int64_t blocks = (n_chunks + kThreads - 1) / kThreads;
+  MX_CHECK_ARG(blocks <= 0x7fffffff, "mxfp8_tile_codes: too large");
+  tile_codes_kernel<<<(unsigned)blocks, kThreads, 0, (hipStream_t)stream>>>((const uint8_t*)q, rows, cols, ld_q,
+                                                                            (uint8_t*)out, n_chunks);
+  MX_CHECK_LAUNCH("mxfp8_tile_codes");
   return MXFP8_OK;
 }
 

@@ -3,6 +3,8 @@
 Drop-in for /root/reference/scripts/fused_mlp.py: same module names (ENABLED, ACTIVE, SAVED_LESS, mlp, _MLP,
 mlp_fwd, mlp_bwd), same saved-tensor set, same return dtypes and the same None fallback contract of mlp().
 
+  Every MX GEMM operand of the path is in the MX-tiled layout (mxfp8.mx_quant_tiled, tile_codes): the same codes
+  and scales as mx_quant in 1 KB blocks the GEMM streams without strided row pieces.
   forward : xs = x·[A_g; A_u]ᵀ (bf16) -> MX(x) -> MX GEMM gate|up (W_gu [2N, K]) -> fused kernel reading gu
             once: LoRA-B of gate and up, bf16 rounding, h = silu(g)·u, MX(h) and the xS_down partials ->
             MX GEMM down with the LoRA epilogue y = bf16(y + s_d · xS_down · B_dᵀ) inside the GEMM.
@@ -69,29 +71,31 @@ def _bwd_grid(T, N, R):
     return best[1], best[2]
 
 
-def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None):
+def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False):
     """gu [T, 2N] bf16, xs [T, 2R] bf16 (xa_gate | xa_up), bg/bu [N, R], ad [R, N] bf16 -> (q_h, s_h, xS_down
-    bf16) (fused_mlp.py:198-215).  h_out (optional [T, N] bf16) receives h for checks."""
+    bf16) (fused_mlp.py:198-215).  h_out (optional [T, N] bf16) receives h for checks; tiled=True writes q_h
+    in the MX-tiled GEMM operand layout ([ceil(T/16)*16, N] bytes, see mxfp8.mx_quant_tiled)."""
     T, N2 = gu.shape
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
     ng = _fwd_groups(T, N)
     if write_q:
-        q = torch.empty((T, N), dtype=_F8, device=dev)
+        q = torch.empty((mxfp8.tiled_rows(T) if tiled else T, N), dtype=_F8, device=dev)
         s = torch.empty(_cdiv(T, 128) * (N // 128) * 512, dtype=torch.uint8, device=dev)
     else:
         q = s = None
     part = torch.empty((ng, T, R), dtype=torch.float32, device=dev)
     LAST["fwd"] = dict(n_groups=ng)
-    _native.mlp_fwd(gu, xs, bg, bu, ad, T, N, R, s_g, s_u, q, s, part, ng, h_out)
+    _native.mlp_fwd(gu, xs, bg, bu, ad, T, N, R, s_g, s_u, q, s, part, ng, h_out, q_layout=int(tiled))
     xsd = torch.empty((T, R), dtype=torch.bfloat16, device=dev)
     _native.sum_parts(part, ng, T * R, xsd)
     return (q, s.view(_E8), xsd) if write_q else (None, None, xsd)
 
 
-def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None):
+def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=False):
     """-> (q_dgu [T, 2N] fp8, s_dgu, [dxa_gate | dxa_up | xS_down] [T, 3R] fp32 (dxa not yet scaled by s),
-    dBg, dBu [N, R] fp32 (not scaled), dAd [R, N] fp32) (fused_mlp.py:235-259)."""
+    dBg, dBu [N, R] fp32 (not scaled), dAd [R, N] fp32) (fused_mlp.py:235-259).  tiled=True writes q_dgu in
+    the MX-tiled GEMM operand layout ([ceil(T/16)*16, 2N] bytes)."""
     T, N2 = gu.shape
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
@@ -106,7 +110,7 @@ def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None):
     dxdT[:, :T] = dxd.t()
     bgT, buT, adT = bg.t().contiguous(), bu.t().contiguous(), ad.t().contiguous()
     if need_q:
-        q = torch.empty((T, N2), dtype=_F8, device=dev)
+        q = torch.empty((mxfp8.tiled_rows(T) if tiled else T, N2), dtype=_F8, device=dev)
         s = torch.empty(_cdiv(T, 128) * (N2 // 128) * 512, dtype=torch.uint8, device=dev)
     else:
         q = s = None
@@ -115,7 +119,7 @@ def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None):
     dbu_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
     dad_p = torch.empty((nsb, R, N), dtype=torch.float32, device=dev)
     _native.mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, R, s_g, s_u, SB, CG, q, s,
-                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out)
+                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out, q_layout=int(tiled))
     dxa = torch.empty((T, 3 * R), dtype=torch.float32, device=dev)
     dbg = torch.empty((N, R), dtype=torch.float32, device=dev)
     dbu = torch.empty((N, R), dtype=torch.float32, device=dev)
@@ -145,13 +149,15 @@ class _MLP(torch.autograd.Function):
         ad = _cast(((id(Ad),), dt), lambda: torch.cat([Ad.detach().to(dt)]))
         bd = _cast((id(Bd), dt), lambda: Bd.detach().to(dt))
         xs = x2 @ S.t()  # [T, 2R] = xa_gate | xa_up
-        q, sc = mxfp8.mx_quant(x2)
-        gu = mxfp8.mx_mm(q, sc, hold.w, hold.ws)  # [T, 2N] gate | up
+        T = x2.shape[0]
+        # GEMM operands in the MX-tiled layout (same codes and scales as mx_quant; the GEMM streams 1 KB blocks)
+        q, sc = mxfp8.mx_quant_tiled(x2)
+        gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=3, m=T)  # [T, 2N] gate | up
         del q, sc
         if need_out:
-            qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True)
+            qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True)
             # y = bf16(bf16(MX(h)·W_downᵀ) + s_d · xS_down · B_dᵀ): the addmm_ of fused_mlp.py:284 in the epilogue
-            y = mxfp8.mx_mm(qh, sh, down._mx_w, down._mx_ws, lora=(xsd, bd), alpha=s_d)
+            y = mxfp8.mx_mm(qh, sh, down._mx_w_tl, down._mx_ws, lora=(xsd, bd), alpha=s_d, layout=3, m=T)
             del qh, sh, xsd
         else:  # graph only (checkpoint recompute / prefix backward): nobody reads y
             STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
@@ -172,14 +178,14 @@ class _MLP(torch.autograd.Function):
         dy2 = dy.reshape(-1, dy.shape[-1]).to(dt)
         if not dy2.is_contiguous():
             dy2 = dy2.contiguous()
-        qd, sd = mxfp8.mx_quant(dy2)
-        wt, wts = mxfp8.mx_wt(down)
-        dhm = mxfp8.mx_mm(qd, sd, wt, wts)  # [T, N] = MX(dy) · W_down
+        T = dy2.shape[0]
+        qd, sd = mxfp8.mx_quant_tiled(dy2)
+        dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=3, m=T)  # [T, N] = MX(dy) · W_down
         del qd, sd
         dxd = dy2 @ bd
         if s_d != 1:
             dxd.mul_(s_d)
-        qg, sg, dxa, dB_g, dB_u, dA_d = mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_x)
+        qg, sg, dxa, dB_g, dB_u, dA_d = mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_x, tiled=True)
         del dhm
         dB_d = dy2.t() @ dxa[:, 2 * R:].to(dt)  # xS_down in bf16, as the unfused path saved it
         if s_d != 1:
@@ -196,7 +202,7 @@ class _MLP(torch.autograd.Function):
         if need_x:
             # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
             # fused_mlp.py:331 in its epilogue
-            dx = mxfp8.mx_mm(qg, sg, hold.wt, hold.wts, lora=(dxa, S.t().contiguous()), alpha=1.0)
+            dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, S.t().contiguous()), alpha=1.0, layout=3, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
         dA = dxa.t() @ x2
@@ -226,6 +232,8 @@ def mlp(mlp_mod, x, need_out=True):
     if pg is None or pu is None or pg[0] is not pu[0] or (pg[1], pu[1]) != (0, 1) or not mxfp8.is_mx(db):
         return None
     hold = pg[0]
+    if getattr(hold, "w_tl", None) is None or getattr(db, "_mx_wt_tl", None) is None:
+        return None  # weights not prepared by this module's enable_mxfp8 (no MX-tiled copies)
     r = Ag.shape[0]
     T = x.numel() // x.shape[-1]
     if not (_r_ok(r) and Au.shape[0] == r and Ad.shape[0] == r and x.shape[-1] == hold.w.shape[1]

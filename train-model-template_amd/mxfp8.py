@@ -5,7 +5,8 @@ quantization and MX GEMM runs in the hand-written gfx950 kernels of libmxfp8_mlp
 no CPU or Triton path, and a CPU tensor is an error.
 
 Layouts (identical to the reference's cuBLAS-compatible ones):
-  codes   float8_e4m3fn, row-major, quantized along the last dimension in blocks of 32;
+  codes   float8_e4m3fn, row-major, quantized along the last dimension in blocks of 32 (the fused MLP path
+          also keeps an MX-tiled copy, the GEMM's operand layout: mx_quant_tiled, tile_codes);
   scales  float8_e8m0fnu, flat, 128x4 blocked: byte of (row i, block b) at
           ((i // 128) * (C // 128) + b // 4) * 512 + (i % 32) * 16 + ((i % 128) // 32) * 4 + b % 4,
           padded rows (up to a multiple of 128) hold 0.
@@ -48,6 +49,33 @@ def mx_quant(x2d):
     return q, s.view(E8)
 
 
+def tiled_rows(R):
+    """Rows held by an MX-tiled code buffer of R rows (16-row blocks)."""
+    return _cdiv(R, 16) * 16
+
+
+def mx_quant_tiled(x2d):
+    """mx_quant with the codes in the MX-tiled operand layout of the GEMM (16-row x 64-code blocks of 1 KB, see
+    include/mxfp8_mlp.h): same codes and scales in another byte order.  The code tensor is [ceil(R/16)*16, K]
+    bytes; pass layout bits to mx_mm.  No reference counterpart (an internal layout of the fused path)."""
+    R, K = x2d.shape
+    assert x2d.dtype == torch.bfloat16 and x2d.stride(1) == 1 and K % 128 == 0, (x2d.dtype, x2d.shape)
+    q = torch.empty((tiled_rows(R), K), dtype=F8, device=x2d.device)
+    s = torch.empty(scale_numel(R, K), dtype=torch.uint8, device=x2d.device)
+    if R:
+        _native.quant_tiled(x2d, q, s)
+    return q, s.view(E8)
+
+
+def tile_codes(q):
+    """Row-major codes [R, K] (any row stride) -> the MX-tiled layout ([ceil(R/16)*16, K] bytes)."""
+    R, K = q.shape
+    out = torch.empty((tiled_rows(R), K), dtype=F8, device=q.device)
+    if R:
+        _native.tile_codes(q, R, K, out)
+    return out
+
+
 def quant_ref(x2d):
     """Quantization of a frozen weight (mxfp8.py:40-43: torchao to_mx RCEIL + to_blocked).  Same arithmetic
     and layout as mx_quant, which is what runs here."""
@@ -84,13 +112,18 @@ def dequant(q, s, shape):
 GEMM_EVENTS = None  # set to a list to record (start event, end event, flops) around every MX GEMM launch
 
 
-def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0):
+def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     """bf16 [M, N] = MX(q [M, K]) · MX(wq [N, K])ᵀ, i.e. torch._scaled_mm(q, wq.t(), s, ws, out_dtype=bf16).
     wq may be a row slice/stride view (row stride wq.stride(0)); optional rank-r epilogue
-    out = bf16(out + alpha · P · Qᵀ) with lora = (P [M, r], Q [N, r]) (the addmm_ after the GEMM)."""
+    out = bf16(out + alpha · P · Qᵀ) with lora = (P [M, r], Q [N, r]) (the addmm_ after the GEMM).
+    layout bit 0 / 1: q / wq hold MX-tiled codes (mx_quant_tiled, tile_codes); then M = m (q has the rows
+    padded to 16)."""
     M, K = q.shape
+    if m is not None:
+        M = m
     N = wq.shape[0]
     assert wq.shape[1] == K and q.stride(1) == 1 and wq.stride(1) == 1, (q.shape, wq.shape)
+    assert not (layout & 1) or q.shape[0] == tiled_rows(M), (q.shape, M)
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=q.device)
     if M:
@@ -98,7 +131,8 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0):
         if ev is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-        _native.gemm_nt(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, out, lora=lora, alpha=alpha)
+        _native.gemm_nt(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, out, lora=lora, alpha=alpha,
+                        layout=layout)
         if ev is not None:
             e1.record()
             ev.append((e0, e1, 2 * M * N * K))
@@ -225,6 +259,7 @@ def enable_mxfp8(model):
             n = gb.weight.shape[0]
             hold = types.SimpleNamespace(n=n, half_t=[None, None])
             hold.w, hold.ws, hold.wt, hold.wts = quant_both(w)
+            hold.w_tl, hold.wt_tl = tile_codes(hold.w), tile_codes(hold.wt)  # GEMM operand layout of the fused path
             del w
             ns = hold.ws.numel() // 2  # forward scales are ordered by tile row: first half = gate
             for i, lin in enumerate((gb, ub)):
@@ -235,6 +270,7 @@ def enable_mxfp8(model):
         w = lin.weight.data
         if id(lin) not in paired:
             lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(w.to(torch.bfloat16))
+            lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
         lin._mx_fbwd = False  # the grouped LoRA backward of the non-MLP linears is not part of this library
         lin._bf16_cpu = w.to("cpu", copy=True)
         lin.weight.data = torch.empty((0,), dtype=w.dtype, device=w.device)
@@ -250,7 +286,8 @@ def disable_mxfp8(model):
     for _, lin in _base_linears(model):
         if hasattr(lin, "_bf16_cpu"):
             lin.weight.data = lin._bf16_cpu.to(lin.weight.device)
-            for a in ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_cat", "_mx_gu", "_mx_fbwd", "_bf16_cpu", "forward"):
+            for a in ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_cat", "_mx_gu", "_mx_fbwd",
+                      "_bf16_cpu", "forward"):
                 if a in lin.__dict__:
                     delattr(lin, a)
     _last[:] = [None, 0, None, None]
