@@ -120,10 +120,16 @@ int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
  *   g = bf16(gu[:, j] + s_g xs_g·bgᵀ), u = bf16(gu[:, N+j] + s_u xs_u·buᵀ), h = bf16(g / (exp(-g) + 1) * u)
  *   q_h [T, N] + s_h (blocked, N/128 tiles per row, padded rows 0)   = MX(h)       (skipped if q_h == NULL)
  *   part [n_groups, T, r] fp32: xS_down partial sums h·adᵀ over the columns of each of n_groups groups
- *   h_out [T, N] bf16 (optional, may be NULL): h itself, for checks
+ *   h_out [T, N] bf16 (optional, may be NULL; needs q_h): h itself, for checks
  *   q_layout: 0 = q_h row-major, 1 = MX-tiled (see mxfp8_quant_tiled; ceil(T/16)*16 rows)
  * Requires N % 128 == 0, (N / 32) % n_groups == 0, r in {16, 32}, T * 2N < 2^31.
  */
+/*
+ * The n_groups mxfp8_mlp_fwd runs best with on the current device (from the kernel's occupancy and the CU
+ * count), 0 for an unsupported shape.  The reference sizes its grid with a fixed rule (fused_mlp.py:198-210).
+ */
+int64_t mxfp8_mlp_fwd_groups(int64_t T, int64_t N, int64_t r);
+
 int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu, const void* ad, int64_t T,
                   int64_t N, int64_t r, float s_g, float s_u, void* q_h, void* s_h, float* part, int64_t n_groups,
                   void* h_out, int64_t q_layout, void* stream);

@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 12, names
+    assert len(names) == 13, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -102,16 +102,28 @@ def test_bwd_grid_choice():
     for T, N in [(10752, 6144), (4096, 3584), (256, 3584), (142336, 6144), (8896, 6144)]:
         sb, cg = fused_mlp._bwd_grid(T, N, 16)
         tpad = -(-T // 128) * 128
-        assert sb % 128 == 0 and cg % 256 == 0 and N % cg == 0 and sb <= tpad
+        assert sb % 128 == 0 and cg % 128 == 0 and N % cg == 0 and sb <= tpad
         nsb, ncg = -(-tpad // sb), N // cg
-        assert nsb * ncg >= 2 * 256 or (sb == 128 and cg == 256)
+        # work per CU slot (rounds of 512 workgroups x row blocks x column quads) within 15% of the balanced
+        # lower bound (SB is at least 4 row blocks)
+        work = -(-(nsb * ncg) // 512) * (sb // 32) * (cg // 128)
+        lower = max(4, -(-(tpad // 32) * (N // 128) // 512))
+        assert work <= 1.15 * lower, (T, N, sb, cg, work, lower)
 
 
-def test_fwd_groups_choice():
-    fused_mlp._CUS[0] = 256
-    for T, N in [(10752, 6144), (256, 3584), (4096, 3584)]:
+def test_fwd_groups_choice(lib):
+    # one wave per (32-row block, column group); without a GPU the library assumes 256 CUs, and the kernel is
+    # built for 3 waves per SIMD: 3072 waves per round
+    cap = 256 * 4 * 3
+    for T, N in [(10752, 6144), (256, 3584), (4096, 3584), (8896, 6144)]:
         ng = fused_mlp._fwd_groups(T, N)
-        assert (N // 32) % ng == 0 and (N // 32) // ng >= 4
+        nt = N // 32
+        assert ng > 0 and nt % ng == 0
+        nrb = -(-T // 128) * 4
+        cost = -(-nrb * ng // cap) * (nt // ng + 1)
+        for g in [d for d in range(1, nt + 1) if nt % d == 0]:
+            assert cost <= -(-nrb * g // cap) * (nt // g + 1), (T, N, ng, g)
+    assert lib.mxfp8_mlp_fwd_groups(10752, 100, 16) == 0 and lib.mxfp8_mlp_fwd_groups(10752, 6144, 8) == 0
 
 
 def test_mlp_gating_on_cpu_returns_none():

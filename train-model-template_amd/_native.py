@@ -27,6 +27,7 @@ SIGNATURES = {
     "mxfp8_gemm_nt": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
                       _i64, _f32, _i64, _ptr, _i64, _ptr],
     "mxfp8_gemm_workspace_size": [_i64, _i64, _i64],
+    "mxfp8_mlp_fwd_groups": [_i64, _i64, _i64],
     "mxfp8_mlp_fwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _i64, _ptr, _i64,
                       _ptr],
     "mxfp8_mlp_bwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32,
@@ -34,7 +35,7 @@ SIGNATURES = {
     "mxfp8_sum_parts": [_ptr, _i64, _i64, _f32, _ptr, _int, _ptr],
 }
 
-_RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64}
+_RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64, "mxfp8_mlp_fwd_groups": _i64}
 
 _lib = None
 _WORKSPACE = {}  # (device index, stream) -> zero-initialised uint8 workspace of the MX GEMM

@@ -128,86 +128,211 @@ __device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, b
 __device__ __forceinline__ v8bf words_bf8(const uint32_t* w) { return as_bf8(make_uint4(w[0], w[1], w[2], w[3])); }
 
 // ---------------------------------------------------------------------------------------------- forward
-// grid (row blocks of 32 up to Tpad, column groups); 4 waves share the row block, wave w takes the group's
-// column tiles w, w+4, ...; xS_down partial summed over the 4 waves in LDS (fixed order).
-template <int R, bool kWriteQ>
-__global__ __launch_bounds__(256) void fwd_kernel(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ xs,
-                                                  const uint16_t* __restrict__ bg, const uint16_t* __restrict__ bu,
-                                                  const uint16_t* __restrict__ ad, int T, int N, int tiles_per_group,
-                                                  float s_g, float s_u, uint8_t* __restrict__ q,
-                                                  uint8_t* __restrict__ s, float* __restrict__ part,
-                                                  uint16_t* __restrict__ h_out, bool q_tiled) {
-  __shared__ float red[4][32][R];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lg = lane >> 5;
-  const int m = blockIdx.x * 32 + (lane & 31);
+// Column order of the forward tiles.  The LoRA-B product D[a][m] = Σ_ρ W[j(a), ρ] X[m, ρ] may take any weight
+// row for MFMA row a; choosing j(a) = pi_col(a) puts, in lane l, the 16 CONTIGUOUS columns lg*16 + i
+// (i = register, lg = l / 32) of row m = l % 32.  A lane then loads its gate / up values as two 16-byte
+// pieces, quantizes 16 adjacent codes of one 32-block with its partner lane l ^ 32, and stores them as one
+// 16-byte word (the accumulator order of the previous tile layout needed four 8-byte loads and four 4-byte
+// stores per 16 values).
+__device__ __forceinline__ int pi_col(int a) { return ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3); }
+
+// 16 contiguous bf16 at p (32 bytes) as 8 packed words
+__device__ __forceinline__ void load16(const uint16_t* p, uint32_t* w) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+// D[a][m] = Σ_ρ W[jb + pi_col(a), ρ] · X[m, ρ] from the lane's weight-row fragments wf (lane l holds weight row
+// jb + pi_col(l % 32), k = h*16 + (l/32)*8 .. +7 in wf[h])
+template <int R>
+__device__ __forceinline__ v16f lora_pi(const v8bf* wf, const v8bf* xf) {
+  v16f d = v16f{};
+#pragma unroll
+  for (int h = 0; h < R / 16; ++h) d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[h], xf[h], d, 0, 0, 0);
+  return d;
+}
+
+// MX-quantize the 16 contiguous values w (8 packed pairs) of row mc, columns k0..k0+15, which with the partner
+// lane's 16 form one 32-block: one 16-byte code store (row-major with Kq codes per row, or MX-tiled), scale
+// byte of row m (0 for padded rows).
+__device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
+                                        int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
+  u16x2 mm = {0, 0};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
+  uint32_t am = amax_bits(mm);
+  am = max(am, (uint32_t)__shfl_xor((int)am, 32));
+  const uint32_t e = e8m0_from_amax_bits(am);
+  const uint4 c = make_uint4(encode4_bf16(w[0], w[1], e), encode4_bf16(w[2], w[3], e), encode4_bf16(w[4], w[5], e),
+                             encode4_bf16(w[6], w[7], e));
+  *reinterpret_cast<uint4*>(q + (tiled ? tiled_offset(mc, k0, Kq) : mc * Kq + k0)) = c;
+  // both lanes of the pair store the same byte (no divergent branch in the loop)
+  s[blocked_offset(m, k0 >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
+}
+
+// Grid (ceil(Tpad / 128), column groups): wave w of workgroup b owns the 32-row block 4b + w and walks every
+// 32-column tile of the group, loading tile t + 1 while it computes tile t; the four waves of a workgroup
+// walk the same tiles, so they share the LoRA weight rows in L1.  A wave sums its own xS_down partial over the
+// group's columns in registers and stores it, so no wave ever waits for another.  Rows past T compute row
+// T - 1 again and store the same bytes there (every store is unconditional, so the compiler's memory-counter
+// waits stay exact); only their scale bytes differ (0 in the padded rows of the last scale tile).
+#ifndef MX_FWD_WAVES_PER_SIMD
+#define MX_FWD_WAVES_PER_SIMD 3
+#endif
+constexpr int kFwdWavesPerSimd = MX_FWD_WAVES_PER_SIMD;  // register budget 512 / n VGPRs (n = 4 spills: measured slower)
+template <int R, bool kWriteQ, bool kH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPerSimd, 8))) void fwd_kernel(
+    const uint16_t* __restrict__ gu, const uint16_t* __restrict__ xs, const uint16_t* __restrict__ bg,
+    const uint16_t* __restrict__ bu, const uint16_t* __restrict__ ad, int T, int Tpad, int N, int tiles_per_group,
+    float s_g, float s_u, uint8_t* __restrict__ q, uint8_t* __restrict__ s, float* __restrict__ part,
+    uint16_t* __restrict__ h_out, bool q_tiled) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
+  const int rb = blockIdx.x * 4 + w;
+  if (rb * 32 >= Tpad) return;  // wave-uniform
+  const int m = rb * 32 + (lane & 31);
   const bool live = m < T;
   const int mc = live ? m : T - 1;
-  const uint16_t* gurow = gu + (int64_t)mc * 2 * N;
+  const uint16_t* grow = gu + (int64_t)mc * 2 * N + lg * 16;  // this lane's 16 columns of a tile: grow + jb
   v8bf xg[R / 16], xu[R / 16];
 #pragma unroll
   for (int h = 0; h < R / 16; ++h) {
     xg[h] = load_bf8(xs + (int64_t)mc * 2 * R + h * 16 + lg * 8);
     xu[h] = load_bf8(xs + (int64_t)mc * 2 * R + R + h * 16 + lg * 8);
   }
+  const int rho = lane & 31;
+  const uint16_t* adrow = ad + (int64_t)(rho < R ? rho : 0) * N + lg * 16;
   v16f acc = v16f{};  // xS_down partial D[ρ][m]
-  const int t0 = blockIdx.y * tiles_per_group;
-  for (int t = t0 + w; t < t0 + tiles_per_group; t += 4) {
+  const int t0 = blockIdx.y * tiles_per_group, t_end = t0 + tiles_per_group;
+  // Every operand of a tile is loaded one tile ahead, together: the memory counter completes in order, so a
+  // load issued after the prefetch and used in the same tile would wait for the prefetch as well.
+  struct TileIn {
+    uint32_t g[8], u[8];          // gate / up values of the lane's 16 columns
+    v8bf bg[R / 16], bu[R / 16];  // LoRA-B weight rows jb + pi_col(lane % 32)
+    v8bf ad[2];                   // ad[ρ, jb + lg*16 + 8 ks + 0..7], ρ = lane % 32 (zero past r)
+  };
+  auto fetch = [&](int t, TileIn& in) {
     const int jb = t * 32;
-    float gv[16], uv[16];
-    load_tile(gurow, jb, lane, live, gv);
-    load_tile(gurow + N, jb, lane, live, uv);
-    const v16f lgd = lora_tile<R>(bg + (int64_t)(jb + (lane & 31)) * R + lg * 8, xg);
-    const v16f lud = lora_tile<R>(bu + (int64_t)(jb + (lane & 31)) * R + lg * 8, xu);
-    float hv[16];
-    uint32_t hw[8];  // h as packed bf16 pairs (columns i, i+1)
+    load16(grow + jb, in.g);
+    load16(grow + N + jb, in.u);
+    const int64_t wr = (int64_t)(jb + pi_col(lane & 31)) * R + lg * 8;
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      float g0 = gv[i] + s_g * lgd[i], g1 = gv[i + 1] + s_g * lgd[i + 1];
-      float u0 = uv[i] + s_u * lud[i], u1 = uv[i + 1] + s_u * lud[i + 1];
-      rnd2(g0, g1);
-      rnd2(u0, u1);
-      hv[i] = (g0 * fast_sigmoid(g0)) * u0;
-      hv[i + 1] = (g1 * fast_sigmoid(g1)) * u1;
-      hw[i / 2] = rnd2(hv[i], hv[i + 1]);
+    for (int h = 0; h < R / 16; ++h) {
+      in.bg[h] = load_bf8(bg + wr + h * 16);
+      in.bu[h] = load_bf8(bu + wr + h * 16);
     }
-    if (kWriteQ) quant_tile(hw, lane, m, live, q, mc, N, q_tiled, jb, s, N / 128);
-    if (h_out && live) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<uint2*>(h_out + (int64_t)m * N + jb + g * 8 + lg * 4) = make_uint2(hw[2 * g], hw[2 * g + 1]);
+    for (int ks = 0; ks < 2; ++ks) {  // load, then select: a branch here would blur the counter waits
+      const v8bf v = load_bf8(adrow + jb + 8 * ks);
+      in.ad[ks] = rho < R ? v : v8bf{};
     }
-    // xS_down: D[ρ][m] += Σ_j ad[ρ, j] h[m, j]; A operand rows ρ = lane % 32 (zero past r)
-    const int rho = lane & 31;
+  };
+  // one tile: compute from `cur` while `nxt` (tile t + 1) is in flight
+  auto tile = [&](int t, const TileIn& cur, TileIn& nxt) {
+    const int jb = t * 32;
+    fetch(min(t + 1, t_end - 1), nxt);  // past the group's end this reloads a tile, unused
+    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch here, a whole tile before its use
+    // g and u as packed bf16 pairs, one at a time (each rank-r product is live only while it is added)
+    uint32_t gp[8], hw[8];  // hw: first u, then h, as packed bf16 pairs (columns lg*16 + i, i + 1)
+    {
+      const v16f d = lora_pi<R>(cur.bg, xg);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v8bf af = rho < R ? load_bf8_perm(ad + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, words_bf8(hw + 4 * ks), acc, 0, 0, 0);
+      for (int i = 0; i < 16; i += 2) {
+        float g0 = bf16_lo(cur.g[i / 2]) + s_g * d[i], g1 = bf16_hi(cur.g[i / 2]) + s_g * d[i + 1];
+        gp[i / 2] = rnd2(g0, g1);
+      }
     }
+    {
+      const v16f d = lora_pi<R>(cur.bu, xu);
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        float u0 = bf16_lo(cur.u[i / 2]) + s_u * d[i], u1 = bf16_hi(cur.u[i / 2]) + s_u * d[i + 1];
+        hw[i / 2] = rnd2(u0, u1);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float g0 = bf16_lo(gp[i]), g1 = bf16_hi(gp[i]);
+      float h0 = (g0 * fast_sigmoid(g0)) * bf16_lo(hw[i]), h1 = (g1 * fast_sigmoid(g1)) * bf16_hi(hw[i]);
+      hw[i] = rnd2(h0, h1);
+    }
+    if (kWriteQ) quant16(hw, lane, m, live, q, mc, N, q_tiled, jb + lg * 16, s, N / 128);
+    if (kH) {
+      uint4* o = reinterpret_cast<uint4*>(h_out + (int64_t)mc * N + jb + lg * 16);
+      o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      o[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    }
+    // xS_down: D[ρ][m] += Σ_j ad[ρ, j] h[m, j]; MFMA k step ks covers, in lane l, columns lg*16 + 8 ks + 0..7
+    // (registers 4ks..4ks+3 of hw), and the A operand row ρ = lane % 32 holds ad at the same columns
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.ad[ks], words_bf8(hw + 4 * ks), acc, 0, 0, 0);
+  };
+  TileIn b0, b1;  // alternating buffers: no register copies between tiles
+  fetch(t0, b0);
+  int t = t0;
+  for (; t + 1 < t_end; t += 2) {
+    tile(t, b0, b1);
+    tile(t + 1, b1, b0);
   }
+  if (t < t_end) tile(t, b0, b1);
   // acc lane l: m = l % 32, ρ = (i/4)*8 + (l/32)*4 + i%4
+  if (live) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int rho = tile_col(i, lane);
-    if (rho < R) red[w][lane & 31][rho] = acc[i];
-  }
-  __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
-    const int mm = idx / R, rr = idx % R;
-    const int row = blockIdx.x * 32 + mm;
-    if (row < T)
-      part[((int64_t)blockIdx.y * T + row) * R + rr] = ((red[0][mm][rr] + red[1][mm][rr]) + red[2][mm][rr]) + red[3][mm][rr];
+    for (int i = 0; i < 16; ++i) {
+      const int rr = tile_col(i, lane);
+      if (rr < R) part[((int64_t)blockIdx.y * T + m) * R + rr] = acc[i];
+    }
   }
 }
 
 // --------------------------------------------------------------------------------------------- backward
-// Program (blockIdx.x = super-block of SB rows, blockIdx.y = column group of CG columns); 8 waves, each owning
-// one 32-column tile of the current 256-column octet.  Outer loop over octets, inner over 32-row blocks.
-//   dB_g, dB_u, dA_d: per-wave accumulators over the inner loop (tile transposed through LDS), written to
-//     the super-block's partial after it;
-//   dxa_g, dxa_u, xS_down: per (row block, octet), the 8 waves' products are summed in LDS (fixed order)
-//     and read-modify-written into the column group's [T, 3r] partial (first octet stores).
-template <int R, bool kQuant>
-__global__ __launch_bounds__(512) void bwd_kernel(
+// Grid (super-blocks of SB rows, column groups of CG columns), 256 threads = 4 waves.  The workgroup walks its
+// column group in quads of 128 columns (wave w on tile 4q + w) and, inside a quad, its super-block in 32-row
+// blocks, in the forward kernel's column order (lane l: row m = l % 32, columns lg*16 + 0..15 of the tile).
+//   per tile: recompute g, u, h; dh = bf16(dhm + dxd·ad); du, dg; MX(dg), MX(du) (codes + scales);
+//     dxa_g | dxa_u | xS_down products D[ρ][m] over the tile's columns (MFMA, k = columns), summed over the
+//     quad's 4 waves in LDS (fixed order) and stored (first quad) or added (later quads) into the column
+//     group's [T, 3r] partial;
+//     dB_g, dB_u, dA_dᵀ contributions D[j][ρ] (16x16x32 MFMA, k = rows): the wave writes its dg, du, h rows
+//     to LDS and reads them back column-wise with ds_read_b64_tr_b16; accumulated over the super-block in
+//     registers and stored after it.
+// The large operands of the next row block (gu, dhm) are loaded one row block ahead; the small per-row
+// operands (xs, dxd and their transposed copies, L2-resident) are issued first in each row block, so waiting
+// for them leaves the prefetch in flight.  Rows past T quantize row T - 1 again (the same bytes) and then
+// zero their values, so they add nothing to dB / dA_d.
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s16 __attribute__((ext_vector_type(8)));
+constexpr int kTrLd = 36;  // bf16 row stride of the per-wave transpose tiles (72 bytes: conflict-free reads)
+
+// 4 bf16 of rows r0 + k (k = 0..3) of column c0 + lane % 16 of a [32][kTrLd] tile.  ds_read_b64_tr_b16 gives
+// lane i of each 16-lane group E[i/4 + 4k][i % 4], E[s] being the four bf16 at lane s's address (measured on
+// gfx950); lane s therefore points at row r0 + s/4, columns c0 + 4 (s % 4) .. + 3.
+__device__ __forceinline__ v4s tr4(const uint16_t* tile, int r0, int c0, int lane) {
+  const int sl = lane & 15;
+  const uint16_t* p = tile + (r0 + (sl >> 2)) * kTrLd + c0 + 4 * (sl & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+}
+
+// 16x16x32 A operand of the transposed tile: lane l holds column c0 + l % 16, rows 8 (l / 16) + 0..7
+__device__ __forceinline__ v8bf tr_operand(const uint16_t* tile, int c0, int lane) {
+  const int g8 = (lane >> 4) * 8;
+  const v4s lo = tr4(tile, g8, c0, lane), hi = tr4(tile, g8 + 4, c0, lane);
+  const v8s16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(v8bf, v);
+}
+
+// the lane's 16 packed values as row l % 32, columns lg*16 .. + 15 of a [32][kTrLd] tile
+__device__ __forceinline__ void tr_store(uint16_t* tile, int lane, const uint32_t* w) {
+  uint32_t* p = reinterpret_cast<uint32_t*>(tile + (lane & 31) * kTrLd + (lane >> 5) * 16);
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) *reinterpret_cast<uint2*>(p + k) = make_uint2(w[k], w[k + 1]);
+}
+
+// Register budget: two waves per SIMD (<= 256 VGPRs; with three the kernel spills), i.e. two workgroups per
+// CU (the LDS, 52 KB at r = 16, would allow three).
+template <int R, bool kQuant, bool kDgu>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void bwd_kernel(
     const uint16_t* __restrict__ gu, const uint16_t* __restrict__ xs, const uint16_t* __restrict__ xsT,
     const uint16_t* __restrict__ dhm, const uint16_t* __restrict__ dxd, const uint16_t* __restrict__ dxdT,
     const uint16_t* __restrict__ bg, const uint16_t* __restrict__ bu, const uint16_t* __restrict__ bgT,
@@ -215,145 +340,192 @@ __global__ __launch_bounds__(512) void bwd_kernel(
     int Tpad, int N, int SB, int CG, float s_g, float s_u, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
     float* __restrict__ dxa_part, float* __restrict__ dbg_part, float* __restrict__ dbu_part,
     float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out, bool q_tiled) {
-  __shared__ float red[8][32][3 * R];                               // per-wave dxa | dxa_u | xS products
-  __shared__ __attribute__((aligned(16))) uint16_t tr[8][3][32][40];  // per-wave transposed dg, du, h [j][m]
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, lg = lane >> 5;
+  __shared__ float red[4][32][3 * R + 1];                              // per-wave dxa | dxa_u | xS products
+  __shared__ __attribute__((aligned(16))) uint16_t trt[4][3][32 * kTrLd];  // per-wave dg, du, h rows
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int r0 = blockIdx.x * SB, r1 = min(r0 + SB, Tpad);
   const int c0 = blockIdx.y * CG;
   const int rho = lane & 31;
-  for (int oc = 0; oc < CG / 256; ++oc) {
-    const int jb = c0 + oc * 256 + w * 32;  // this wave's tile
-    const uint16_t* bgrow = bg + (int64_t)(jb + (lane & 31)) * R + lg * 8;
-    const uint16_t* burow = bu + (int64_t)(jb + (lane & 31)) * R + lg * 8;
-    const uint16_t* adtrow = adT + (int64_t)(jb + (lane & 31)) * R + lg * 8;
-    // dB_g, dB_u, dA_d of this tile as D[j][ρ] on the 16x16x32 bf16 MFMA (A = transposed tile rows j, k = m;
-    // B = xsᵀ / dxdᵀ rows ρ): lane l holds ρ = l % 16 (+16 h) and j = jb + 16 jh + (l / 16) * 4 + i
+  const int rho_c = rho < R ? rho : 0;
+  struct RowIn {
+    uint32_t g[8], u[8], d[8];  // gate, up, dhm of the lane's row and 16 columns
+  };
+  for (int oc = 0; oc < CG / 128; ++oc) {
+    const int jb = c0 + oc * 128 + w * 32;  // this wave's tile
+    // weights of this tile: LoRA-B rows jb + pi_col(lane % 32) (bg, bu, adᵀ) and, for the products that
+    // reduce over the columns, rows ρ of bgᵀ, buᵀ, ad at the lane's columns
+    v8bf wbg[R / 16], wbu[R / 16], wad[R / 16], fbg[2], fbu[2], fad[2];
+    {
+      const int64_t wr = (int64_t)(jb + pi_col(lane & 31)) * R + lg * 8;
+#pragma unroll
+      for (int h = 0; h < R / 16; ++h) {
+        wbg[h] = load_bf8(bg + wr + h * 16);
+        wbu[h] = load_bf8(bu + wr + h * 16);
+        wad[h] = load_bf8(adT + wr + h * 16);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {  // load, then select (no branch)
+        const int64_t off = (int64_t)rho_c * N + jb + lg * 16 + 8 * ks;
+        const v8bf a = load_bf8(bgT + off), b = load_bf8(buT + off), c = load_bf8(ad + off);
+        fbg[ks] = rho < R ? a : v8bf{};
+        fbu[ks] = rho < R ? b : v8bf{};
+        fad[ks] = rho < R ? c : v8bf{};
+      }
+    }
+    // dB_g, dB_u, dA_d of this tile as D[j][ρ]: lane l holds ρ = 16 h + l % 16, j = jb + 16 jh + (l/16)*4 + i
     v4f dbg[2][R / 16], dbu[2][R / 16], dad[2][R / 16];
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
       for (int h = 0; h < R / 16; ++h) dbg[jh][h] = dbu[jh][h] = dad[jh][h] = v4f{};
-    for (int rb = r0; rb < r1; rb += 32) {
+    auto fetch = [&](int rb, RowIn& in) {
+      const int mc = min(rb + (lane & 31), T - 1);
+      const uint16_t* row = gu + (int64_t)mc * 2 * N + jb + lg * 16;
+      load16(row, in.g);
+      load16(row + N, in.u);
+      load16(dhm + (int64_t)mc * N + jb + lg * 16, in.d);
+    };
+    auto block = [&](int rb, const RowIn& cur, RowIn& nxt) {
       const int m = rb + (lane & 31);
       const bool live = m < T;
       const int mc = live ? m : T - 1;
-      v8bf xg[R / 16], xu[R / 16], xd[R / 16];
+      // small operands of this row block first (see above), then the next row block's large ones
+      v8bf xg[R / 16], xu[R / 16], xd[R / 16], tg[R / 16], tu[R / 16], td[R / 16];
 #pragma unroll
       for (int h = 0; h < R / 16; ++h) {
         xg[h] = load_bf8(xs + (int64_t)mc * 2 * R + h * 16 + lg * 8);
         xu[h] = load_bf8(xs + (int64_t)mc * 2 * R + R + h * 16 + lg * 8);
         xd[h] = load_bf8(dxd + (int64_t)mc * R + h * 16 + lg * 8);
+        const int rr = h * 16 + (lane & 15), mo = rb + (lane >> 4) * 8;
+        tg[h] = load_bf8(xsT + (int64_t)rr * Tpad + mo);
+        tu[h] = load_bf8(xsT + (int64_t)(R + rr) * Tpad + mo);
+        td[h] = load_bf8(dxdT + (int64_t)rr * Tpad + mo);
       }
-      float gv[16], uv[16], dv[16];
-      load_tile(gu + (int64_t)mc * 2 * N, jb, lane, live, gv);
-      load_tile(gu + (int64_t)mc * 2 * N + N, jb, lane, live, uv);
-      load_tile(dhm + (int64_t)mc * N, jb, lane, live, dv);
-      const v16f lgd = lora_tile<R>(bgrow, xg);
-      const v16f lud = lora_tile<R>(burow, xu);
-      const v16f ldd = lora_tile<R>(adtrow, xd);
-      float dgv[16], duv[16], hv[16];
-      uint32_t dgw[8], duw[8], hw[8];  // the same as packed bf16 pairs
+      fetch(min(rb + 32, r1 - 32), nxt);  // past the super-block's end this reloads a row block, unused
+      __builtin_amdgcn_sched_barrier(0);
+      // g, u, dh as packed bf16 pairs, one rank-r product at a time
+      uint32_t gp[8], upk[8], dp[8];
+      {
+        const v16f d = lora_pi<R>(wbg, xg);
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        float g0 = gv[i] + s_g * lgd[i], g1 = gv[i + 1] + s_g * lgd[i + 1];
-        float u0 = uv[i] + s_u * lud[i], u1 = uv[i + 1] + s_u * lud[i + 1];
-        float d0 = dv[i] + ldd[i], d1 = dv[i + 1] + ldd[i + 1];
-        rnd2(g0, g1);
-        rnd2(u0, u1);
-        rnd2(d0, d1);  // dh
+        for (int i = 0; i < 16; i += 2) {
+          float a = bf16_lo(cur.g[i / 2]) + s_g * d[i], b = bf16_hi(cur.g[i / 2]) + s_g * d[i + 1];
+          gp[i / 2] = rnd2(a, b);
+        }
+      }
+      {
+        const v16f d = lora_pi<R>(wbu, xu);
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          float a = bf16_lo(cur.u[i / 2]) + s_u * d[i], b = bf16_hi(cur.u[i / 2]) + s_u * d[i + 1];
+          upk[i / 2] = rnd2(a, b);
+        }
+      }
+      {
+        const v16f d = lora_pi<R>(wad, xd);
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          float a = bf16_lo(cur.d[i / 2]) + d[i], b = bf16_hi(cur.d[i / 2]) + d[i + 1];
+          dp[i / 2] = rnd2(a, b);  // dh
+        }
+      }
+      uint32_t dgw[8], duw[8], hw[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float g0 = bf16_lo(gp[i]), g1 = bf16_hi(gp[i]);
+        const float u0 = bf16_lo(upk[i]), u1 = bf16_hi(upk[i]);
+        const float d0 = bf16_lo(dp[i]), d1 = bf16_hi(dp[i]);
         const float sg0 = fast_sigmoid(g0), sg1 = fast_sigmoid(g1);
         const float sl0 = g0 * sg0, sl1 = g1 * sg1;
-        hv[i] = sl0 * u0;
-        hv[i + 1] = sl1 * u1;
-        hw[i / 2] = rnd2(hv[i], hv[i + 1]);
-        duv[i] = d0 * sl0;
-        duv[i + 1] = d1 * sl1;
-        duw[i / 2] = rnd2(duv[i], duv[i + 1]);
-        dgv[i] = ((d0 * u0) * sg0) * (g0 * (1.0f - sg0) + 1.0f);
-        dgv[i + 1] = ((d1 * u1) * sg1) * (g1 * (1.0f - sg1) + 1.0f);
-        dgw[i / 2] = rnd2(dgv[i], dgv[i + 1]);
+        float h0 = sl0 * u0, h1 = sl1 * u1;
+        hw[i] = rnd2(h0, h1);
+        float du0 = d0 * sl0, du1 = d1 * sl1;
+        duw[i] = rnd2(du0, du1);
+        float dg0 = ((d0 * u0) * sg0) * (g0 * (1.0f - sg0) + 1.0f);
+        float dg1 = ((d1 * u1) * sg1) * (g1 * (1.0f - sg1) + 1.0f);
+        dgw[i] = rnd2(dg0, dg1);
       }
-      if (!live) {
+      if (kDgu) {
+        uint4* o = reinterpret_cast<uint4*>(dgu_out + (int64_t)mc * 2 * N + jb + lg * 16);
+        o[0] = make_uint4(dgw[0], dgw[1], dgw[2], dgw[3]);
+        o[1] = make_uint4(dgw[4], dgw[5], dgw[6], dgw[7]);
+        uint4* o2 = reinterpret_cast<uint4*>(dgu_out + (int64_t)mc * 2 * N + N + jb + lg * 16);
+        o2[0] = make_uint4(duw[0], duw[1], duw[2], duw[3]);
+        o2[1] = make_uint4(duw[4], duw[5], duw[6], duw[7]);
+      }
+      if (kQuant) {
+        quant16(dgw, lane, m, live, q, mc, 2 * N, q_tiled, jb + lg * 16, s, 2 * N / 128);
+        quant16(duw, lane, m, live, q, mc, 2 * N, q_tiled, N + jb + lg * 16, s, 2 * N / 128);
+      }
+      if (!live) {  // padded rows add nothing to the sums below
 #pragma unroll
         for (int i = 0; i < 8; ++i) dgw[i] = duw[i] = hw[i] = 0u;
       }
-      if (dgu_out && live) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          uint16_t* o = dgu_out + (int64_t)m * 2 * N + jb + g * 8 + lg * 4;
-          *reinterpret_cast<uint2*>(o) = make_uint2(dgw[2 * g], dgw[2 * g + 1]);
-          *reinterpret_cast<uint2*>(o + N) = make_uint2(duw[2 * g], duw[2 * g + 1]);
-        }
-      }
-      if (kQuant) {
-        quant_tile(dgw, lane, m, live, q, mc, 2 * N, q_tiled, jb, s, 2 * N / 128);
-        quant_tile(duw, lane, m, live, q, mc, 2 * N, q_tiled, N + jb, s, 2 * N / 128);
-      }
-      // dxa_g | dxa_u | xS_down products over this tile's 32 columns: D[ρ][m]
-      v16f pg = v16f{}, pu = v16f{}, px = v16f{};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bool ok = rho < R;
-        const v8bf fg = ok ? load_bf8_perm(bgT + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
-        const v8bf fu = ok ? load_bf8_perm(buT + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
-        const v8bf fa = ok ? load_bf8_perm(ad + (int64_t)rho * N, jb + 16 * ks, lg) : v8bf{};
-        pg = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fg, words_bf8(dgw + 4 * ks), pg, 0, 0, 0);
-        pu = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fu, words_bf8(duw + 4 * ks), pu, 0, 0, 0);
-        px = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, words_bf8(hw + 4 * ks), px, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int rr = tile_col(i, lane);
-        if (rr < R) {
-          red[w][lane & 31][rr] = pg[i];
-          red[w][lane & 31][R + rr] = pu[i];
-          red[w][lane & 31][2 * R + rr] = px[i];
-        }
-      }
-      // transpose dg, du, h to [j][m] for the products that reduce over m
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const int j = tile_col(i, lane);
-        tr[w][0][j][lane & 31] = (uint16_t)dgw[i / 2];
-        tr[w][0][j + 1][lane & 31] = (uint16_t)(dgw[i / 2] >> 16);
-        tr[w][1][j][lane & 31] = (uint16_t)duw[i / 2];
-        tr[w][1][j + 1][lane & 31] = (uint16_t)(duw[i / 2] >> 16);
-        tr[w][2][j][lane & 31] = (uint16_t)hw[i / 2];
-        tr[w][2][j + 1][lane & 31] = (uint16_t)(hw[i / 2] >> 16);
-      }
-      __syncthreads();
-      // D[j][ρ] += Σ_m dg[m, j] xs_g[m, ρ] etc. over the 32 rows of this block (one K = 32 step)
+      // dxa_g | dxa_u | xS_down products over this tile's columns, D[ρ][m] -> LDS (lane l: m = l % 32,
+      // ρ = tile_col(i, l))
       {
-        const int mo = (lane >> 4) * 8;  // this lane's 8 rows of the block
+        v16f p = v16f{};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fbg[ks], words_bf8(dgw + 4 * ks), p, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int rr = tile_col(i, lane);
+          if (rr < R) red[w][lane & 31][rr] = p[i];
+        }
+        p = v16f{};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fbu[ks], words_bf8(duw + 4 * ks), p, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int rr = tile_col(i, lane);
+          if (rr < R) red[w][lane & 31][R + rr] = p[i];
+        }
+        p = v16f{};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fad[ks], words_bf8(hw + 4 * ks), p, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int rr = tile_col(i, lane);
+          if (rr < R) red[w][lane & 31][2 * R + rr] = p[i];
+        }
+      }
+      // dB_g, dB_u, dA_dᵀ: D[j][ρ] += Σ_m dg[m, j] xs_g[m, ρ] etc. over the 32 rows (one k = 32 step)
+      tr_store(trt[w][0], lane, dgw);
+      tr_store(trt[w][1], lane, duw);
+      tr_store(trt[w][2], lane, hw);
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh) {
+        const v8bf ag = tr_operand(trt[w][0], jh * 16, lane);
+        const v8bf au = tr_operand(trt[w][1], jh * 16, lane);
+        const v8bf ah = tr_operand(trt[w][2], jh * 16, lane);
 #pragma unroll
         for (int h = 0; h < R / 16; ++h) {
-          const int rr = h * 16 + (lane & 15);
-          const v8bf bgx = load_bf8(xsT + (int64_t)rr * Tpad + rb + mo);
-          const v8bf bux = load_bf8(xsT + (int64_t)(R + rr) * Tpad + rb + mo);
-          const v8bf bdx = load_bf8(dxdT + (int64_t)rr * Tpad + rb + mo);
-#pragma unroll
-          for (int jh = 0; jh < 2; ++jh) {
-            const int jl = jh * 16 + (lane & 15);
-            dbg[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(load_bf8(&tr[w][0][jl][mo]), bgx, dbg[jh][h], 0, 0, 0);
-            dbu[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(load_bf8(&tr[w][1][jl][mo]), bux, dbu[jh][h], 0, 0, 0);
-            dad[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(load_bf8(&tr[w][2][jl][mo]), bdx, dad[jh][h], 0, 0, 0);
-          }
+          dbg[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ag, tg[h], dbg[jh][h], 0, 0, 0);
+          dbu[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(au, tu[h], dbu[jh][h], 0, 0, 0);
+          dad[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, td[h], dad[jh][h], 0, 0, 0);
         }
       }
-      // sum the 8 waves' dxa | xS products and accumulate into the column group's partial
-      for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 512) {
+      // sum the 4 waves' products (fixed order) into the column group's partial
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 256) {
         const int mm = idx / (3 * R), cc = idx % (3 * R);
         const int row = rb + mm;
         if (row < T) {
-          float v = red[0][mm][cc];
-#pragma unroll
-          for (int k = 1; k < 8; ++k) v += red[k][mm][cc];
+          const float v = ((red[0][mm][cc] + red[1][mm][cc]) + red[2][mm][cc]) + red[3][mm][cc];
           float* dst = dxa_part + ((int64_t)blockIdx.y * T + row) * 3 * R + cc;
           *dst = oc == 0 ? v : *dst + v;
         }
       }
       __syncthreads();
+    };
+    RowIn b0, b1;  // alternating buffers: no register copies between row blocks
+    fetch(r0, b0);
+    int rb = r0;
+    for (; rb + 32 < r1; rb += 64) {
+      block(rb, b0, b1);
+      block(rb + 32, b1, b0);
     }
+    if (rb < r1) block(rb, b0, b1);
     // dB partials of this super-block: D[j][ρ], lane l: ρ = 16 h + l % 16, j = jb + 16 jh + (l / 16) * 4 + i
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
@@ -385,12 +557,45 @@ __global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict_
 
 }  // namespace
 
+namespace {
+
+int device_cus() {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+    return 256;
+  return v;
+}
+
+}  // namespace
+
+extern "C" int64_t mxfp8_mlp_fwd_groups(int64_t T, int64_t N, int64_t r) {
+  if (T <= 0 || N <= 0 || N % 128 || (r != 16 && r != 32)) return 0;
+  // One wave per (32-row block, column group); a CU holds kFwdWavesPerSimd waves per SIMD.  Every wave of a
+  // round runs at the same pace, so the time goes as rounds x (tiles per group + ~1 tile of set-up).  Pick
+  // the group count (a divisor of N/32) with the least of that; among ties, the fewest groups (smallest
+  // partial-sum buffer).
+  const int64_t cap = (int64_t)device_cus() * 4 * kFwdWavesPerSimd, nt = N / 32, nrb = (T + 127) / 128 * 4;
+  int64_t best = 1, best_cost = -1;
+  for (int64_t g = 1; g <= nt; ++g) {
+    if (nt % g) continue;
+    const int64_t rounds = (nrb * g + cap - 1) / cap;
+    const int64_t cost = rounds * (nt / g + 1);
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = g;
+    }
+  }
+  return best;
+}
+
 extern "C" int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu, const void* ad, int64_t T,
                              int64_t N, int64_t r, float s_g, float s_u, void* q_h, void* s_h, float* part,
                              int64_t n_groups, void* h_out, int64_t q_layout, void* stream) {
   MX_CHECK_ARG(gu && xs && bg && bu && ad && part, "mxfp8_mlp_fwd: null pointer");
   MX_CHECK_ARG(q_layout == 0 || q_layout == 1, "mxfp8_mlp_fwd: q_layout must be 0 (row-major) or 1 (MX-tiled)");
   MX_CHECK_ARG((q_h == nullptr) == (s_h == nullptr), "mxfp8_mlp_fwd: q_h and s_h go together");
+  MX_CHECK_ARG(!h_out || q_h, "mxfp8_mlp_fwd: h_out needs q_h");
   MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && (r == 16 || r == 32), "mxfp8_mlp_fwd: bad shape");
   MX_CHECK_ARG(T * 2 * N < (1LL << 31), "mxfp8_mlp_fwd: T * 2N must stay below 2^31");
   MX_CHECK_ARG(n_groups > 0 && (N / 32) % n_groups == 0, "mxfp8_mlp_fwd: n_groups must divide N / 32");
@@ -399,17 +604,20 @@ extern "C" int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, con
                    (!h_out || mx_aligned(h_out, 16)),
                "mxfp8_mlp_fwd: misaligned buffer");
   const int64_t Tpad = (T + 127) / 128 * 128;
-  dim3 grid((unsigned)(Tpad / 32), (unsigned)n_groups);
+  dim3 grid((unsigned)(Tpad / 128), (unsigned)n_groups);
   const int tpg = (int)(N / 32 / n_groups);
   hipStream_t stm = (hipStream_t)stream;
 #define FWD_ARGS (const uint16_t*)gu, (const uint16_t*)xs, (const uint16_t*)bg, (const uint16_t*)bu, (const uint16_t*)ad, \
-                 (int)T, (int)N, tpg, s_g, s_u, (uint8_t*)q_h, (uint8_t*)s_h, part, (uint16_t*)h_out, q_layout == 1
+                 (int)T, (int)Tpad, (int)N, tpg, s_g, s_u, (uint8_t*)q_h, (uint8_t*)s_h, part, (uint16_t*)h_out, \
+                 q_layout == 1
   if (r == 16) {
-    if (q_h) fwd_kernel<16, true><<<grid, 256, 0, stm>>>(FWD_ARGS);
-    else fwd_kernel<16, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
+    if (h_out) fwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(FWD_ARGS);
+    else if (q_h) fwd_kernel<16, true, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
+    else fwd_kernel<16, false, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
   } else {
-    if (q_h) fwd_kernel<32, true><<<grid, 256, 0, stm>>>(FWD_ARGS);
-    else fwd_kernel<32, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
+    if (h_out) fwd_kernel<32, true, true><<<grid, 256, 0, stm>>>(FWD_ARGS);
+    else if (q_h) fwd_kernel<32, true, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
+    else fwd_kernel<32, false, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
   }
 #undef FWD_ARGS
   MX_CHECK_LAUNCH("mxfp8_mlp_fwd");
@@ -426,10 +634,10 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                    dbg_part && dbu_part && dad_part,
                "mxfp8_mlp_bwd: null pointer");
   MX_CHECK_ARG((q == nullptr) == (s == nullptr), "mxfp8_mlp_bwd: q and s go together");
-  MX_CHECK_ARG(T > 0 && N > 0 && N % 256 == 0 && (r == 16 || r == 32), "mxfp8_mlp_bwd: bad shape (N %% 256)");
+  MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && (r == 16 || r == 32), "mxfp8_mlp_bwd: bad shape (N %% 128)");
   MX_CHECK_ARG(T * 2 * N < (1LL << 31), "mxfp8_mlp_bwd: T * 2N must stay below 2^31");
-  MX_CHECK_ARG(SB > 0 && SB % 128 == 0 && CG > 0 && CG % 256 == 0 && N % CG == 0,
-               "mxfp8_mlp_bwd: SB must be a multiple of 128, CG a multiple of 256 dividing N");
+  MX_CHECK_ARG(SB > 0 && SB % 128 == 0 && CG > 0 && CG % 128 == 0 && N % CG == 0,
+               "mxfp8_mlp_bwd: SB must be a multiple of 128, CG a multiple of 128 dividing N");
   MX_CHECK_ARG(mx_aligned(gu, 16) && mx_aligned(dhm, 16) && mx_aligned(xs, 16) && mx_aligned(xsT, 16) &&
                    mx_aligned(dxd, 16) && mx_aligned(dxdT, 16) && mx_aligned(bg, 16) && mx_aligned(bu, 16) &&
                    mx_aligned(bgT, 16) && mx_aligned(buT, 16) && mx_aligned(ad, 16) && mx_aligned(adT, 16) &&
@@ -443,12 +651,15 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                  (const uint16_t*)buT, (const uint16_t*)ad, (const uint16_t*)adT, (int)T, (int)Tpad, (int)N, (int)SB,     \
                  (int)CG, s_g, s_u, (uint8_t*)q, (uint8_t*)s, dxa_part, dbg_part, dbu_part, dad_part, (uint16_t*)dgu_out, \
                  q_layout == 1
+  MX_CHECK_ARG(!dgu_out || q, "mxfp8_mlp_bwd: dgu_out needs q");
   if (r == 16) {
-    if (q) bwd_kernel<16, true><<<grid, 512, 0, stm>>>(BWD_ARGS);
-    else bwd_kernel<16, false><<<grid, 512, 0, stm>>>(BWD_ARGS);
+    if (dgu_out) bwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(BWD_ARGS);
+    else if (q) bwd_kernel<16, true, false><<<grid, 256, 0, stm>>>(BWD_ARGS);
+    else bwd_kernel<16, false, false><<<grid, 256, 0, stm>>>(BWD_ARGS);
   } else {
-    if (q) bwd_kernel<32, true><<<grid, 512, 0, stm>>>(BWD_ARGS);
-    else bwd_kernel<32, false><<<grid, 512, 0, stm>>>(BWD_ARGS);
+    if (dgu_out) bwd_kernel<32, true, true><<<grid, 256, 0, stm>>>(BWD_ARGS);
+    else if (q) bwd_kernel<32, true, false><<<grid, 256, 0, stm>>>(BWD_ARGS);
+    else bwd_kernel<32, false, false><<<grid, 256, 0, stm>>>(BWD_ARGS);
   }
 #undef BWD_ARGS
   MX_CHECK_LAUNCH("mxfp8_mlp_bwd");

@@ -45,29 +45,29 @@ def _divisors(n):
     return [d for d in range(1, n + 1) if n % d == 0]
 
 
-def _fwd_groups(T, N):
-    """Column groups of the forward kernel: the fewest (smallest partial buffer) that still give >= 4
-    workgroups per CU, each group keeping at least 4 column tiles (one per wave)."""
-    nt = N // 32
-    nrb = _cdiv(T, 128) * 4
-    ok = [d for d in _divisors(nt) if nt // d >= 4] or [1]
-    return next((d for d in ok if nrb * d >= 4 * _n_cu()), ok[-1])
+def _fwd_groups(T, N, R=16):
+    """Column groups of the forward kernel, chosen by the library from the kernel's occupancy on this device
+    (mxfp8_mlp_fwd_groups: fewest rounds x tiles per group, at least 4 tiles per group)."""
+    return int(_native.load().mxfp8_mlp_fwd_groups(T, N, R))
 
 
 def _bwd_grid(T, N, R):
-    """(SB, CG) of the backward kernel: the fewest partial-sum bytes (per super-block dB/dA partials plus per
-    column-group dxa partials, as in fused_mlp.py:218-232) with at least 2 workgroups per CU."""
+    """(SB, CG) of the backward kernel (SB, CG multiples of 128; two 4-wave workgroups per CU).  Every
+    workgroup of a round runs at the same pace, so the time goes as rounds x (SB/32 row blocks x CG/128 column
+    quads); pick the least of that, then the fewest partial-sum bytes (per super-block dB / dA_d partials plus
+    per column-group dxa partials, as in fused_mlp.py:218-232)."""
     tpad = _cdiv(T, 128) * 128
+    cap = 2 * _n_cu()
     best = None
-    for cg in [256 * d for d in _divisors(N // 256)]:
+    for cg in [128 * d for d in _divisors(N // 128)]:
         ncg = N // cg
         for sb in range(128, tpad + 128, 128):
             nsb = _cdiv(tpad, sb)
-            if nsb * ncg < 2 * _n_cu() and not (sb == 128 and cg == 256):
-                continue
-            cost = nsb * N * R * 3 * 4 + ncg * T * 3 * R * 4
-            if best is None or cost < best[0]:
-                best = (cost, sb, cg)
+            work = _cdiv(nsb * ncg, cap) * (sb // 32) * (cg // 128)
+            partial = nsb * N * R * 3 * 4 + ncg * T * 3 * R * 4
+            key = (work, partial)
+            if best is None or key < best[0]:
+                best = (key, sb, cg)
     return best[1], best[2]
 
 
@@ -78,7 +78,7 @@ def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False):
     T, N2 = gu.shape
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
-    ng = _fwd_groups(T, N)
+    ng = _fwd_groups(T, N, R)
     if write_q:
         q = torch.empty((mxfp8.tiled_rows(T) if tiled else T, N), dtype=_F8, device=dev)
         s = torch.empty(_cdiv(T, 128) * (N // 128) * 512, dtype=torch.uint8, device=dev)
