@@ -161,6 +161,48 @@ int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, const void* d
 int mxfp8_sum_parts(const float* part, int64_t n_parts, int64_t count, float scale, void* out, int out_bf16,
                     void* stream);
 
+/*
+ * Per-step bf16 forms of the fp32 LoRA weights (replaces the _cast copies of /root/reference/scripts/
+ * fused_mlp.py:272-276 and the transposed copies its kernels index): A_g, A_u [r, K], B_g, B_u [N, r],
+ * A_d [r, N], B_d [K, r] -> S = [A_g; A_u] [2r, K], Sᵀ [K, 2r], b_g, b_u [N, r], b_gᵀ, b_uᵀ [r, N], a_d [r, N],
+ * a_dᵀ [N, r], b_d [K, r], b_dᵀ [r, K]; round to nearest even.  r <= 64.
+ */
+int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg, const float* Bu, const float* Ad, const float* Bd,
+                    int64_t r, int64_t K, int64_t N, void* S, void* ST, void* bg, void* bu, void* bgT, void* buT,
+                    void* ad, void* adT, void* bd, void* bdT, void* stream);
+
+/*
+ * out[t, ρ] = bf16(x[t, :] · w[ρ, :]), then bf16(out · scale) when scale != 1; x [T, K] bf16 (row stride ld_x),
+ * w [rp, K] bf16, out [T, rp] bf16; outT (optional) [rp, Tpad] bf16, the same values transposed and zero for
+ * t >= T.  Replaces xs = x2 @ S.t() and dxd = (dy2 @ bd).mul_(s_d) (/root/reference/scripts/fused_mlp.py:277,
+ * :311-313).  K % 256 == 0, rp in {16, 32, 64}.
+ */
+int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* w, int64_t rp, float scale, void* out,
+                  void* outT, int64_t Tpad, void* stream);
+
+/* Token chunks mxfp8_lora_tn uses for [T, K] (its partial buffer holds chunks * rp * K floats). */
+int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);
+
+/*
+ * out = bf16(Σ_t p[t, ρ] x[t, k]) (then bf16(· scale) when scale != 1) over the T tokens, as [rp, K]
+ * (transpose = 0) or [K, rp] (transpose = 1), fp32 holding the bf16 value (out_f32 = 1) or bf16; x [T, K],
+ * p [T, rp] bf16; part: scratch of mxfp8_lora_tn_chunks(T, K) * rp * K floats, the per-chunk sums (added in
+ * chunk order).  Replaces dB_d = (dy2.t() @ xS_down).mul_(s_d) and dA = dxa.t() @ x2
+ * (/root/reference/scripts/fused_mlp.py:316-318, :333).  K % 128 == 0, rp in {16, 32, 64}.
+ */
+int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp, int64_t chunks,
+                  float* part, float scale, int64_t transpose, int64_t out_f32, void* out, void* stream);
+
+/*
+ * The backward kernel's partial sums, added in order, scaled and cast as the reference's backward does
+ * (/root/reference/scripts/fused_mlp.py:258, :319-326): dxa [T, 2r] bf16 = bf16(s_g · Σ dxa_g | s_u · Σ dxa_u),
+ * xsd [T, r] bf16 = bf16(Σ xS_down), dB_g, dB_u [N, r] fp32 = s · Σ, dA_d [r, N] fp32 = Σ.  Partials as written by
+ * mxfp8_mlp_bwd (ncg column groups, nsb super-blocks).
+ */
+int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part, const float* dbu_part, const float* dad_part,
+                         int64_t ncg, int64_t nsb, int64_t T, int64_t N, int64_t r, float s_g, float s_u, void* dxa,
+                         void* xsd, float* dbg, float* dbu, float* dad, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

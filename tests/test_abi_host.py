@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 13, names
+    assert len(names) == 18, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -69,6 +69,12 @@ def test_argument_checks_reject_before_launch(lib):
     # backward column group must divide N and be a multiple of 256
     args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, 0, None]
     assert lib.mxfp8_mlp_bwd(*args) == -1
+    # LoRA products: K must be a multiple of 256 (x · Wᵀ) / 128 (token reduction), rp in {16, 32, 64}
+    assert lib.mxfp8_lora_nt(p, 4, 200, 200, p, 16, 1.0, p, None, 0, None) == -1
+    assert lib.mxfp8_lora_nt(p, 4, 256, 256, p, 8, 1.0, p, None, 0, None) == -1
+    assert lib.mxfp8_lora_tn(p, 4, 96, 96, p, 16, 1, ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), 1.0, 0, 0, p,
+                             None) == -1
+    assert lib.mxfp8_lora_tn_chunks(10752, 2048) > 0 and lib.mxfp8_lora_tn_chunks(10752, 100) == 0
     # tiled quantizer / tile_codes shape checks
     assert lib.mxfp8_quant_tiled(p, 4, 100, 100, p, p, None) == -1
     assert lib.mxfp8_tile_codes(p, 4, 96, 96, p, None) == -1

@@ -33,9 +33,16 @@ SIGNATURES = {
     "mxfp8_mlp_bwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32,
                       _f32, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _ptr, _i64, _ptr],
     "mxfp8_sum_parts": [_ptr, _i64, _i64, _f32, _ptr, _int, _ptr],
+    "mxfp8_lora_prep": [_ptr] * 6 + [_i64, _i64, _i64] + [_ptr] * 10 + [_ptr],
+    "mxfp8_lora_nt": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
+    "mxfp8_lora_tn_chunks": [_i64, _i64],
+    "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
+    "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
+                             _ptr, _ptr],
 }
 
-_RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64, "mxfp8_mlp_fwd_groups": _i64}
+_RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64, "mxfp8_mlp_fwd_groups": _i64,
+             "mxfp8_lora_tn_chunks": _i64}
 
 _lib = None
 _WORKSPACE = {}  # (device index, stream) -> zero-initialised uint8 workspace of the MX GEMM
@@ -168,3 +175,36 @@ def sum_parts(part, n_parts, count, out, scale=1.0):
     assert out.dtype in (torch.float32, torch.bfloat16) and part.dtype == torch.float32
     call("mxfp8_sum_parts", _p(part), n_parts, count, float(scale), _p(out), int(out.dtype == torch.bfloat16),
          like=part)
+
+
+def lora_prep(Ag, Au, Bg, Bu, Ad, Bd, out):
+    """out: dict of bf16 tensors S, ST, bg, bu, bgT, buT, ad, adT, bd, bdT (see include/mxfp8_mlp.h)."""
+    R, K = Ag.shape
+    N = Bg.shape[0]
+    call("mxfp8_lora_prep", *[_p(t) for t in (Ag, Au, Bg, Bu, Ad, Bd)], R, K, N,
+         *[_p(out[k]) for k in ("S", "ST", "bg", "bu", "bgT", "buT", "ad", "adT", "bd", "bdT")], like=Ag)
+
+
+def lora_nt(x, w, out, scale=1.0, outT=None):
+    """out[t, ρ] = bf16(x[t] · w[ρ]) (then · scale); outT [rp, Tpad] optional (zero-padded transposed copy)."""
+    T, K = x.shape
+    call("mxfp8_lora_nt", _p(x), T, K, x.stride(0), _p(w), w.shape[0], float(scale), _p(out), _p(outT),
+         outT.shape[1] if outT is not None else 0, like=x)
+
+
+def lora_tn(x, p, out, part, scale=1.0, transpose=False):
+    """out = bf16(pᵀ · x) (then · scale), [rp, K] or transposed; part: float scratch (lora_tn_chunks)."""
+    T, K = x.shape
+    rp = p.shape[1]
+    chunks = part.numel() // (rp * K)
+    call("mxfp8_lora_tn", _p(x), T, K, x.stride(0), _p(p), rp, chunks, _p(part), float(scale), int(transpose),
+         int(out.dtype == torch.float32), _p(out), like=x)
+
+
+def lora_tn_chunks(T, K):
+    return int(load().mxfp8_lora_tn_chunks(T, K))
+
+
+def mlp_bwd_finish(dxa_p, dbg_p, dbu_p, dad_p, T, N, r, s_g, s_u, dxa, xsd, dbg, dbu, dad):
+    call("mxfp8_mlp_bwd_finish", _p(dxa_p), _p(dbg_p), _p(dbu_p), _p(dad_p), dxa_p.shape[0], dbg_p.shape[0], T, N, r,
+         float(s_g), float(s_u), _p(dxa), _p(xsd), _p(dbg), _p(dbu), _p(dad), like=dxa)

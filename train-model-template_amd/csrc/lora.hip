@@ -1,0 +1,358 @@
+// The rank-r LoRA products around the fused MLP, for gfx950: the per-step bf16 forms of the adapter
+// parameters, the activation x adapter products (reduction over the model dimension), the adapter-gradient
+// products (reduction over the tokens) and the final reduction of the backward kernel's partial sums.
+//
+// Reference (all in /root/reference/scripts/fused_mlp.py, _MLP, with bf16 torch GEMMs at fp32 accumulation):
+//   :272-276  S = [A_g; A_u], b_g, b_u, a_d, b_d: bf16 copies of the fp32 adapter weights (fused_linear._cast)
+//   :277      xs  = bf16(x · Sᵀ)                               [T, 2r]
+//   :311-313  dxd = bf16(bf16(dy · B_d) · s_d)                 [T, r]
+//   :316-318  dB_d = bf16(bf16(dyᵀ · bf16(xS_down)) · s_d)     [K, r]
+//   :319-326  dxa = bf16(s · Σ partials) (gate and up scales), dB_g, dB_u = s · Σ partials (fp32), dA_d (fp32)
+//   :333      dA  = bf16(dxaᵀ · x)                             [2r, K]
+// Products that reduce over the model dimension read the activation once, row by row (MFMA with k along
+// the row).  Products that reduce over the tokens split the tokens into chunks whose fp32 partials are added
+// in chunk order by a second kernel (deterministic); inside a chunk both operands are transposed through LDS
+// with ds_read_b64_tr_b16 so that k runs along the tokens.
+#include "abi_common.h"
+#include "mx_device.h"
+
+using namespace mxk;
+
+namespace {
+
+__device__ __forceinline__ uint16_t bf(float x) { return (uint16_t)f32_to_bf16_bits(x); }
+
+// ------------------------------------------------------------------------------------------------- prep
+struct PrepArgs {
+  const float *Ag, *Au, *Bg, *Bu, *Ad, *Bd;  // [r, K], [r, K], [N, r], [N, r], [r, N], [K, r] fp32
+  uint16_t *S, *ST, *bg, *bu, *bgT, *buT, *ad, *adT, *bd, *bdT;
+  int R, K, N;
+};
+
+// One thread per output element of: S [2r, K], Sᵀ [K, 2r], b_g, b_u [N, r], b_gᵀ, b_uᵀ [r, N], a_d [r, N],
+// a_dᵀ [N, r], b_d [K, r], b_dᵀ [r, K] (round to nearest even, as Tensor.to(bfloat16)).
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t R = a.R, K = a.K, N = a.N;
+  int64_t n = 2 * R * K;
+  if (i < n) {
+    const int64_t r = i / K, k = i % K;
+    a.S[i] = bf(r < R ? a.Ag[r * K + k] : a.Au[(r - R) * K + k]);
+    return;
+  }
+  i -= n;
+  if (i < n) {
+    const int64_t k = i / (2 * R), r = i % (2 * R);
+    a.ST[i] = bf(r < R ? a.Ag[r * K + k] : a.Au[(r - R) * K + k]);
+    return;
+  }
+  i -= n;
+  n = N * R;
+  if (i < n) { a.bg[i] = bf(a.Bg[i]); return; }
+  i -= n;
+  if (i < n) { a.bu[i] = bf(a.Bu[i]); return; }
+  i -= n;
+  if (i < n) {
+    const int64_t r = i / N, j = i % N;
+    a.bgT[i] = bf(a.Bg[j * R + r]);
+    return;
+  }
+  i -= n;
+  if (i < n) {
+    const int64_t r = i / N, j = i % N;
+    a.buT[i] = bf(a.Bu[j * R + r]);
+    return;
+  }
+  i -= n;
+  if (i < n) { a.ad[i] = bf(a.Ad[i]); return; }
+  i -= n;
+  if (i < n) {
+    const int64_t j = i / R, r = i % R;
+    a.adT[i] = bf(a.Ad[r * N + j]);
+    return;
+  }
+  i -= n;
+  n = K * R;
+  if (i < n) { a.bd[i] = bf(a.Bd[i]); return; }
+  i -= n;
+  if (i < n) {
+    const int64_t r = i / K, k = i % K;
+    a.bdT[i] = bf(a.Bd[k * R + r]);
+  }
+}
+
+// ----------------------------------------------------------------------------------------- x · Wᵀ (nt)
+// out[t, ρ] = bf16(X[t, :] · W[ρ, :]) (then bf16(· scale) when scale != 1), X [T, K] bf16 (row stride ldx),
+// W [RP, K] bf16; optionally outT [RP, Tpad] (zero for t >= T).  Grid: Tpad / 32 row blocks, 4 waves, wave w
+// summing a quarter of K for the block's 32 rows with the 32x32x16 MFMA (A = W rows ρ, B = X rows t, k along
+// the row); the 4 quarters are added in LDS in a fixed order.
+template <int RP>
+__global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W,
+                                                 int T, int Tpad, int K, float scale, uint16_t* __restrict__ out,
+                                                 uint16_t* __restrict__ outT) {
+  constexpr int NA = (RP + 31) / 32;  // 32-row groups of W
+  __shared__ float red[4][32][RP + 1];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
+  const int t = blockIdx.x * 32 + (lane & 31);
+  const int tc = min(t, T - 1);
+  const int kq = K / 4, k0 = w * kq;
+  const uint16_t* xrow = X + (int64_t)tc * ldx + lg * 8;
+  v16f acc[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) acc[a] = v16f{};
+  for (int k = k0; k < k0 + kq; k += 64) {
+    v8bf xb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xb[u] = load_bf8(xrow + k + 16 * u);
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      const int rho = a * 32 + (lane & 31);
+      const uint16_t* wrow = W + (int64_t)(rho < RP ? rho : 0) * K + lg * 8 + k;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const v8bf wv = load_bf8(wrow + 16 * u);
+        acc[a] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rho < RP ? wv : v8bf{}, xb[u], acc[a], 0, 0, 0);
+      }
+    }
+  }
+  // acc[a] lane l: t = l % 32, ρ = a*32 + (i/4)*8 + (l/32)*4 + i%4
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rho = a * 32 + (i >> 2) * 8 + lg * 4 + (i & 3);
+      if (rho < RP) red[w][lane & 31][rho] = acc[a][i];
+    }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 32 * RP; idx += 256) {
+    const int tt = idx / RP, rho = idx % RP;
+    const int row = blockIdx.x * 32 + tt;
+    float v = round_bf16(((red[0][tt][rho] + red[1][tt][rho]) + red[2][tt][rho]) + red[3][tt][rho]);
+    if (scale != 1.0f) v = round_bf16(v * scale);
+    if (row < T) out[(int64_t)row * RP + rho] = bf(v);
+    if (outT) outT[(int64_t)rho * Tpad + row] = row < T ? bf(v) : (uint16_t)0;
+  }
+}
+
+// ------------------------------------------------------------------------------------- Pᵀ · X (tn)
+// part[c, ρ, k] = Σ_{t in chunk c} P[t, ρ] X[t, k], P [T, RP] bf16, X [T, K] bf16 (row stride ldx).  Grid
+// (K / 128, chunks), 4 waves, wave w on columns blockIdx.x * 128 + 32 w .. + 31.  Per 32-token step the wave
+// writes its X tile and the P tile to LDS and reads both back with k along the tokens (16x16x32 MFMA: A = Xᵀ
+// rows k, B = Pᵀ... as columns ρ); tokens past T are zero.  The next step's tiles are loaded one step ahead.
+template <int RP>
+__global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+                                                 const uint16_t* __restrict__ P, int T, int K, int chunk,
+                                                 float* __restrict__ part) {
+  constexpr int NH = RP / 16;
+  __shared__ __attribute__((aligned(16))) uint16_t xt[4][32 * kTrLd];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[4][(RP > 32 ? 2 : 1)][32 * kTrLd];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
+  const int kb = blockIdx.x * 128 + w * 32;
+  const int t0 = blockIdx.y * chunk, t1 = min(t0 + chunk, T);
+  v4f acc[2][NH];
+#pragma unroll
+  for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+    for (int h = 0; h < NH; ++h) acc[jh][h] = v4f{};
+  constexpr int PW = RP / 4;  // packed words of P per lane: half of the row (RP / 2 values)
+  struct Step {
+    uint32_t x[8];   // X row t + l % 32, columns kb + lg*16 .. + 15
+    uint32_t p[PW];  // P row t + l % 32, columns lg * RP/2 .. + RP/2 - 1
+  };
+  auto fetch = [&](int t, Step& st) {
+    const int row = t + (lane & 31);
+    const bool ok = row < t1;
+    const int rc = min(row, T - 1);
+    load16(X + (int64_t)rc * ldx + kb + lg * 16, st.x);
+    uint32_t pv[PW];
+    const uint16_t* prow = P + (int64_t)rc * RP + lg * (RP / 2);
+    if constexpr (RP == 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(prow);
+      pv[0] = v.x; pv[1] = v.y; pv[2] = v.z; pv[3] = v.w;
+    } else {
+#pragma unroll
+      for (int q = 0; q < PW; q += 8) load16(prow + 2 * q, pv + q);
+    }
+    // tokens past the chunk are zero (not 0 * whatever row T - 1 holds)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) st.x[k] = ok ? st.x[k] : 0u;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) st.p[k] = ok ? pv[k] : 0u;
+  };
+  Step cur, nxt;
+  fetch(t0, cur);
+  for (int t = t0; t < t1; t += 32) {
+    fetch(min(t + 32, t1 - 1 - ((t1 - 1 - t0) % 32)), nxt);  // the last step reloads itself, unused
+    __builtin_amdgcn_sched_barrier(0);
+    tr_store(xt[w], lane, cur.x);
+    // P tile row l % 32: the lane's RP/2 columns (RP = 64: lane half lg fills tile lg, columns 0..31)
+    {
+      uint32_t* prow = reinterpret_cast<uint32_t*>(pt[w][RP > 32 ? lg : 0] + (lane & 31) * kTrLd) +
+                       (RP > 32 ? 0 : lg * (PW));
+#pragma unroll
+      for (int k = 0; k < PW; k += 2) *reinterpret_cast<uint2*>(prow + k) = make_uint2(cur.p[k], cur.p[k + 1]);
+    }
+    const v8bf a0 = tr_operand(xt[w], 0, lane), a1 = tr_operand(xt[w], 16, lane);
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const v8bf b = RP > 32 ? tr_operand(pt[w][h >> 1], (h & 1) * 16, lane) : tr_operand(pt[w][0], h * 16, lane);
+      acc[0][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc[0][h], 0, 0, 0);
+      acc[1][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc[1][h], 0, 0, 0);
+    }
+    cur = nxt;
+  }
+  // acc[jh][h] lane l: ρ = 16 h + l % 16, k = kb + 16 jh + (l / 16) * 4 + i
+#pragma unroll
+  for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rho = h * 16 + (lane & 15);
+        const int k = kb + jh * 16 + (lane >> 4) * 4 + i;
+        part[((int64_t)blockIdx.y * RP + rho) * K + k] = acc[jh][h][i];
+      }
+}
+
+// out = bf16(Σ_c part[c, ρ, k]) (then bf16(· scale) when scale != 1), written as [RP, K] or transposed
+// [K, RP]; as fp32 holding the bf16 value (out_f32) or as bf16.  The chunks are added in order.
+__global__ __launch_bounds__(256) void tn_sum_kernel(const float* __restrict__ part, int chunks, int RP, int K,
+                                                     float scale, int transpose, int out_f32, void* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = (int64_t)RP * K;
+  if (i >= n) return;
+  float v = part[i];
+  for (int c = 1; c < chunks; ++c) v += part[(int64_t)c * n + i];
+  v = round_bf16(v);
+  if (scale != 1.0f) v = round_bf16(v * scale);
+  const int64_t rho = i / K, k = i % K;
+  const int64_t o = transpose ? k * RP + rho : i;
+  if (out_f32) reinterpret_cast<float*>(out)[o] = v;
+  else reinterpret_cast<uint16_t*>(out)[o] = bf(v);
+}
+
+// ------------------------------------------------------------------------------- backward partial sums
+struct FinishArgs {
+  const float *dxa_part, *dbg_part, *dbu_part, *dad_part;
+  int ncg, nsb, T, N, R;
+  float s_g, s_u;
+  uint16_t *dxa, *xsd;        // [T, 2r] bf16 (scaled), [T, r] bf16
+  float *dbg, *dbu, *dad;     // [N, r], [N, r], [r, N] fp32
+};
+
+// One thread per output element of dxa | xsd, dB_g, dB_u, dA_d; partials added in order (fused_mlp.py:258,
+// :319-326).
+__global__ __launch_bounds__(256) void finish_kernel(FinishArgs a, int64_t total) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t R = a.R;
+  int64_t n = (int64_t)a.T * 3 * R;
+  if (i < n) {
+    const int64_t cnt = n;
+    float v = a.dxa_part[i];
+    for (int c = 1; c < a.ncg; ++c) v += a.dxa_part[(int64_t)c * cnt + i];
+    const int64_t t = i / (3 * R), c = i % (3 * R);
+    if (c < 2 * R) a.dxa[t * 2 * R + c] = bf(v * (c < R ? a.s_g : a.s_u));
+    else a.xsd[t * R + c - 2 * R] = bf(v);
+    return;
+  }
+  i -= n;
+  n = (int64_t)a.N * R;
+  const float* src;
+  float* dst;
+  float sc;
+  if (i < n) { src = a.dbg_part; dst = a.dbg; sc = a.s_g; }
+  else if (i < 2 * n) { i -= n; src = a.dbu_part; dst = a.dbu; sc = a.s_u; }
+  else { i -= 2 * n; src = a.dad_part; dst = a.dad; sc = 1.0f; }
+  float v = src[i];
+  for (int c = 1; c < a.nsb; ++c) v += src[(int64_t)c * n + i];
+  dst[i] = sc == 1.0f ? v : v * sc;
+}
+
+}  // namespace
+
+extern "C" int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg, const float* Bu, const float* Ad,
+                               const float* Bd, int64_t R, int64_t K, int64_t N, void* S, void* ST, void* bg, void* bu,
+                               void* bgT, void* buT, void* ad, void* adT, void* bd, void* bdT, void* stream) {
+  MX_CHECK_ARG(Ag && Au && Bg && Bu && Ad && Bd && S && ST && bg && bu && bgT && buT && ad && adT && bd && bdT,
+               "mxfp8_lora_prep: null pointer");
+  MX_CHECK_ARG(R > 0 && R <= 64 && K > 0 && N > 0 && K < (1 << 24) && N < (1 << 24), "mxfp8_lora_prep: bad shape");
+  const int64_t total = 4 * R * K + 6 * N * R + 2 * K * R;
+  PrepArgs a{Ag, Au, Bg, Bu, Ad, Bd, (uint16_t*)S, (uint16_t*)ST, (uint16_t*)bg, (uint16_t*)bu, (uint16_t*)bgT,
+             (uint16_t*)buT, (uint16_t*)ad, (uint16_t*)adT, (uint16_t*)bd, (uint16_t*)bdT, (int)R, (int)K, (int)N};
+  prep_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total);
+  MX_CHECK_LAUNCH("mxfp8_lora_prep");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* w, int64_t rp, float scale,
+                             void* out, void* outT, int64_t Tpad, void* stream) {
+  MX_CHECK_ARG(x && w && out, "mxfp8_lora_nt: null pointer");
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 256 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
+               "mxfp8_lora_nt: need K %% 256 == 0, rp in {16, 32, 64}");
+  MX_CHECK_ARG(!outT || (Tpad >= T && Tpad % 32 == 0), "mxfp8_lora_nt: Tpad must be >= T and a multiple of 32");
+  MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(w, 16), "mxfp8_lora_nt: misaligned buffer");
+  MX_CHECK_ARG(T < (1LL << 31) && (outT ? Tpad : T) / 32 < (1LL << 31), "mxfp8_lora_nt: too many rows");
+  const int64_t rows = outT ? Tpad : (T + 31) / 32 * 32;
+  dim3 grid((unsigned)(rows / 32));
+  hipStream_t stm = (hipStream_t)stream;
+#define NT_ARGS (const uint16_t*)x, ld_x, (const uint16_t*)w, (int)T, (int)(outT ? Tpad : 0), (int)K, scale, \
+                (uint16_t*)out, (uint16_t*)outT
+  if (rp == 16) nt_kernel<16><<<grid, 256, 0, stm>>>(NT_ARGS);
+  else if (rp == 32) nt_kernel<32><<<grid, 256, 0, stm>>>(NT_ARGS);
+  else nt_kernel<64><<<grid, 256, 0, stm>>>(NT_ARGS);
+#undef NT_ARGS
+  MX_CHECK_LAUNCH("mxfp8_lora_nt");
+  return MXFP8_OK;
+}
+
+extern "C" int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K) {
+  if (T <= 0 || K <= 0 || K % 128) return 0;
+  // enough workgroups to fill the GPU twice over (K / 128 column blocks x chunks of a multiple of 32 tokens)
+  const int64_t cols = K / 128, want = (512 + cols - 1) / cols;
+  const int64_t blocks = (T + 31) / 32;
+  const int64_t per = (blocks + want - 1) / want;
+  return (blocks + per - 1) / per;
+}
+
+extern "C" int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp,
+                             int64_t chunks, float* part, float scale, int64_t transpose, int64_t out_f32, void* out,
+                             void* stream) {
+  MX_CHECK_ARG(x && p && part && out, "mxfp8_lora_tn: null pointer");
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
+               "mxfp8_lora_tn: need K %% 128 == 0, rp in {16, 32, 64}");
+  MX_CHECK_ARG(chunks > 0 && chunks <= 65535, "mxfp8_lora_tn: bad chunk count");
+  MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(p, 16) && mx_aligned(part, 16), "mxfp8_lora_tn: misaligned buffer");
+  const int64_t blocks = (T + 31) / 32;
+  const int64_t chunk = (blocks + chunks - 1) / chunks * 32;
+  const int64_t used = (T + chunk - 1) / chunk;
+  hipStream_t stm = (hipStream_t)stream;
+  dim3 grid((unsigned)(K / 128), (unsigned)used);
+#define TN_ARGS (const uint16_t*)x, ld_x, (const uint16_t*)p, (int)T, (int)K, (int)chunk, part
+  if (rp == 16) tn_kernel<16><<<grid, 256, 0, stm>>>(TN_ARGS);
+  else if (rp == 32) tn_kernel<32><<<grid, 256, 0, stm>>>(TN_ARGS);
+  else tn_kernel<64><<<grid, 256, 0, stm>>>(TN_ARGS);
+#undef TN_ARGS
+  MX_CHECK_LAUNCH("mxfp8_lora_tn");
+  const int64_t n = rp * K;
+  tn_sum_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stm>>>(part, (int)used, (int)rp, (int)K, scale, (int)transpose,
+                                                              (int)out_f32, out);
+  MX_CHECK_LAUNCH("mxfp8_lora_tn");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part, const float* dbu_part,
+                                    const float* dad_part, int64_t ncg, int64_t nsb, int64_t T, int64_t N, int64_t r,
+                                    float s_g, float s_u, void* dxa, void* xsd, float* dbg, float* dbu, float* dad,
+                                    void* stream) {
+  MX_CHECK_ARG(dxa_part && dbg_part && dbu_part && dad_part && dxa && xsd && dbg && dbu && dad,
+               "mxfp8_mlp_bwd_finish: null pointer");
+  MX_CHECK_ARG(ncg > 0 && nsb > 0 && T > 0 && N > 0 && (r == 16 || r == 32), "mxfp8_mlp_bwd_finish: bad shape");
+  const int64_t total = T * 3 * r + 3 * N * r;
+  FinishArgs a{dxa_part, dbg_part, dbu_part, dad_part, (int)ncg, (int)nsb, (int)T, (int)N, (int)r, s_g, s_u,
+               (uint16_t*)dxa, (uint16_t*)xsd, dbg, dbu, dad};
+  finish_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total);
+  MX_CHECK_LAUNCH("mxfp8_mlp_bwd_finish");
+  return MXFP8_OK;
+}

@@ -29,7 +29,6 @@ using namespace mxk;
 
 namespace {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int tile_col(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
@@ -53,12 +52,6 @@ __device__ __forceinline__ float fast_sigmoid(float g) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
-__device__ __forceinline__ v8bf as_bf8(uint4 u) {
-  u32x4 v = {u.x, u.y, u.z, u.w};
-  return __builtin_bit_cast(v8bf, v);
-}
-
-__device__ __forceinline__ v8bf load_bf8(const uint16_t* p) { return as_bf8(*reinterpret_cast<const uint4*>(p)); }
 
 // 8 bf16 of row `p` at columns base + {lg*4 + 0..3} and base + 8 + {lg*4 + 0..3} (one k-step of the permuted
 // column order; lg = lane / 32)
@@ -135,13 +128,6 @@ __device__ __forceinline__ v8bf words_bf8(const uint32_t* w) { return as_bf8(mak
 // 16-byte word (the accumulator order of the previous tile layout needed four 8-byte loads and four 4-byte
 // stores per 16 values).
 __device__ __forceinline__ int pi_col(int a) { return ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3); }
-
-// 16 contiguous bf16 at p (32 bytes) as 8 packed words
-__device__ __forceinline__ void load16(const uint16_t* p, uint32_t* w) {
-  const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
-  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-}
 
 // D[a][m] = Σ_ρ W[jb + pi_col(a), ρ] · X[m, ρ] from the lane's weight-row fragments wf (lane l holds weight row
 // jb + pi_col(l % 32), k = h*16 + (l/32)*8 .. +7 in wf[h])
@@ -301,34 +287,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPe
 // operands (xs, dxd and their transposed copies, L2-resident) are issued first in each row block, so waiting
 // for them leaves the prefetch in flight.  Rows past T quantize row T - 1 again (the same bytes) and then
 // zero their values, so they add nothing to dB / dA_d.
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef short v8s16 __attribute__((ext_vector_type(8)));
-constexpr int kTrLd = 36;  // bf16 row stride of the per-wave transpose tiles (72 bytes: conflict-free reads)
-
-// 4 bf16 of rows r0 + k (k = 0..3) of column c0 + lane % 16 of a [32][kTrLd] tile.  ds_read_b64_tr_b16 gives
-// lane i of each 16-lane group E[i/4 + 4k][i % 4], E[s] being the four bf16 at lane s's address (measured on
-// gfx950); lane s therefore points at row r0 + s/4, columns c0 + 4 (s % 4) .. + 3.
-__device__ __forceinline__ v4s tr4(const uint16_t* tile, int r0, int c0, int lane) {
-  const int sl = lane & 15;
-  const uint16_t* p = tile + (r0 + (sl >> 2)) * kTrLd + c0 + 4 * (sl & 3);
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
-}
-
-// 16x16x32 A operand of the transposed tile: lane l holds column c0 + l % 16, rows 8 (l / 16) + 0..7
-__device__ __forceinline__ v8bf tr_operand(const uint16_t* tile, int c0, int lane) {
-  const int g8 = (lane >> 4) * 8;
-  const v4s lo = tr4(tile, g8, c0, lane), hi = tr4(tile, g8 + 4, c0, lane);
-  const v8s16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(v8bf, v);
-}
-
-// the lane's 16 packed values as row l % 32, columns lg*16 .. + 15 of a [32][kTrLd] tile
-__device__ __forceinline__ void tr_store(uint16_t* tile, int lane, const uint32_t* w) {
-  uint32_t* p = reinterpret_cast<uint32_t*>(tile + (lane & 31) * kTrLd + (lane >> 5) * 16);
-#pragma unroll
-  for (int k = 0; k < 8; k += 2) *reinterpret_cast<uint2*>(p + k) = make_uint2(w[k], w[k + 1]);
-}
-
 // Register budget: two waves per SIMD (<= 256 VGPRs; with three the kernel spills), i.e. two workgroups per
 // CU (the LDS, 52 KB at r = 16, would allow three).
 template <int R, bool kQuant, bool kDgu>

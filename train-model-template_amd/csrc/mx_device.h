@@ -127,4 +127,51 @@ __device__ __forceinline__ uint32_t quad_umax(uint32_t v) {
   return v;
 }
 
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v8bf as_bf8(uint4 u) {
+  u32x4 v = {u.x, u.y, u.z, u.w};
+  return __builtin_bit_cast(v8bf, v);
+}
+
+// 8 bf16 at p (16 bytes) as a matrix-instruction operand
+__device__ __forceinline__ v8bf load_bf8(const uint16_t* p) { return as_bf8(*reinterpret_cast<const uint4*>(p)); }
+
+// 16 contiguous bf16 at p (32 bytes) as 8 packed words
+__device__ __forceinline__ void load16(const uint16_t* p, uint32_t* w) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+// ---- transposes through LDS with ds_read_b64_tr_b16 (gfx950)
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s16 __attribute__((ext_vector_type(8)));
+constexpr int kTrLd = 36;  // bf16 row stride of the per-wave transpose tiles (72 bytes: conflict-free reads)
+
+// 4 bf16 of rows r0 + k (k = 0..3) of column c0 + lane % 16 of a [32][kTrLd] tile.  ds_read_b64_tr_b16 gives
+// lane i of each 16-lane group E[i/4 + 4k][i % 4], E[s] being the four bf16 at lane s's address (measured on
+// gfx950); lane s therefore points at row r0 + s/4, columns c0 + 4 (s % 4) .. + 3.
+__device__ __forceinline__ v4s tr4(const uint16_t* tile, int r0, int c0, int lane) {
+  const int sl = lane & 15;
+  const uint16_t* p = tile + (r0 + (sl >> 2)) * kTrLd + c0 + 4 * (sl & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+}
+
+// 16x16x32 A operand of the transposed tile: lane l holds column c0 + l % 16, rows 8 (l / 16) + 0..7
+__device__ __forceinline__ v8bf tr_operand(const uint16_t* tile, int c0, int lane) {
+  const int g8 = (lane >> 4) * 8;
+  const v4s lo = tr4(tile, g8, c0, lane), hi = tr4(tile, g8 + 4, c0, lane);
+  const v8s16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(v8bf, v);
+}
+
+// the lane's 16 packed values as row l % 32, columns lg*16 .. + 15 of a [32][kTrLd] tile
+__device__ __forceinline__ void tr_store(uint16_t* tile, int lane, const uint32_t* w) {
+  uint32_t* p = reinterpret_cast<uint32_t*>(tile + (lane & 31) * kTrLd + (lane >> 5) * 16);
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) *reinterpret_cast<uint2*>(p + k) = make_uint2(w[k], w[k + 1]);
+}
+
 }  // namespace mxk

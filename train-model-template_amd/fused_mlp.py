@@ -16,6 +16,8 @@ mlp_fwd, mlp_bwd), same saved-tensor set, same return dtypes and the same None f
 The heavy kernels are hand-written HIP (libmxfp8_mlp.so, _native.py); the rank-r LoRA products that are plain
 skinny GEMMs (xs, dxd, dB_d, dA) use PyTorch's bf16 GEMM on the same stream.
 """
+import types
+
 import torch
 
 import _native
@@ -92,10 +94,8 @@ def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False):
     return (q, s.view(_E8), xsd) if write_q else (None, None, xsd)
 
 
-def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=False):
-    """-> (q_dgu [T, 2N] fp8, s_dgu, [dxa_gate | dxa_up | xS_down] [T, 3R] fp32 (dxa not yet scaled by s),
-    dBg, dBu [N, R] fp32 (not scaled), dAd [R, N] fp32) (fused_mlp.py:235-259).  tiled=True writes q_dgu in
-    the MX-tiled GEMM operand layout ([ceil(T/16)*16, 2N] bytes)."""
+def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u, need_q, dgu_out, tiled):
+    """Run the backward kernel; -> (q, s, (dxa_p, dbg_p, dbu_p, dad_p)) with the partial sums unreduced."""
     T, N2 = gu.shape
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
@@ -103,12 +103,6 @@ def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=
     SB, CG = _bwd_grid(T, N, R)
     nsb, ncg = _cdiv(tpad, SB), N // CG
     LAST["bwd"] = dict(SB=SB, CG=CG, nsb=nsb, ncg=ncg)
-    # small transposed copies the kernel reads as matrix-instruction operands
-    xsT = torch.zeros((2 * R, tpad), dtype=torch.bfloat16, device=dev)
-    xsT[:, :T] = xs.t()
-    dxdT = torch.zeros((R, tpad), dtype=torch.bfloat16, device=dev)
-    dxdT[:, :T] = dxd.t()
-    bgT, buT, adT = bg.t().contiguous(), bu.t().contiguous(), ad.t().contiguous()
     if need_q:
         q = torch.empty((mxfp8.tiled_rows(T) if tiled else T, N2), dtype=_F8, device=dev)
         s = torch.empty(_cdiv(T, 128) * (N2 // 128) * 512, dtype=torch.uint8, device=dev)
@@ -120,15 +114,53 @@ def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=
     dad_p = torch.empty((nsb, R, N), dtype=torch.float32, device=dev)
     _native.mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, R, s_g, s_u, SB, CG, q, s,
                     dxa_p, dbg_p, dbu_p, dad_p, dgu_out, q_layout=int(tiled))
+    return q, (s.view(_E8) if need_q else None), (dxa_p, dbg_p, dbu_p, dad_p)
+
+
+def _transposed_padded(t, tpad):
+    out = torch.zeros((t.shape[1], tpad), dtype=t.dtype, device=t.device)
+    out[:, :t.shape[0]] = t.t()
+    return out
+
+
+def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=False):
+    """-> (q_dgu [T, 2N] fp8, s_dgu, [dxa_gate | dxa_up | xS_down] [T, 3R] fp32 (dxa not yet scaled by s),
+    dBg, dBu [N, R] fp32 (not scaled), dAd [R, N] fp32) (fused_mlp.py:235-259).  tiled=True writes q_dgu in
+    the MX-tiled GEMM operand layout ([ceil(T/16)*16, 2N] bytes)."""
+    T, N2 = gu.shape
+    N, R = N2 // 2, ad.shape[0]
+    dev = gu.device
+    tpad = _cdiv(T, 128) * 128
+    # small transposed copies the kernel reads as matrix-instruction operands
+    xsT, dxdT = _transposed_padded(xs, tpad), _transposed_padded(dxd, tpad)
+    bgT, buT, adT = bg.t().contiguous(), bu.t().contiguous(), ad.t().contiguous()
+    q, s, (dxa_p, dbg_p, dbu_p, dad_p) = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g,
+                                                     s_u, need_q, dgu_out, tiled)
     dxa = torch.empty((T, 3 * R), dtype=torch.float32, device=dev)
     dbg = torch.empty((N, R), dtype=torch.float32, device=dev)
     dbu = torch.empty((N, R), dtype=torch.float32, device=dev)
     dad = torch.empty((R, N), dtype=torch.float32, device=dev)
-    _native.sum_parts(dxa_p, ncg, T * 3 * R, dxa)
-    _native.sum_parts(dbg_p, nsb, N * R, dbg)
-    _native.sum_parts(dbu_p, nsb, N * R, dbu)
-    _native.sum_parts(dad_p, nsb, R * N, dad)
-    return (q if need_q else None, s.view(_E8) if need_q else None, dxa, dbg, dbu, dad)
+    _native.sum_parts(dxa_p, dxa_p.shape[0], T * 3 * R, dxa)
+    _native.sum_parts(dbg_p, dbg_p.shape[0], N * R, dbg)
+    _native.sum_parts(dbu_p, dbu_p.shape[0], N * R, dbu)
+    _native.sum_parts(dad_p, dad_p.shape[0], R * N, dad)
+    return q, s, dxa, dbg, dbu, dad
+
+
+def _prep(Ag, Bg, Au, Bu, Ad, Bd, dt):
+    """The step's bf16 forms of the LoRA weights (fused_mlp.py:272-276 _cast copies, plus the transposed copies
+    the kernels index), from one kernel; cached per step like fused_linear._cast."""
+    def make():
+        dev = Ag.device
+        R, K = Ag.shape
+        N = Bg.shape[0]
+        e = lambda *sh: torch.empty(sh, dtype=torch.bfloat16, device=dev)  # noqa: E731
+        out = dict(S=e(2 * R, K), ST=e(K, 2 * R), bg=e(N, R), bu=e(N, R), bgT=e(R, N), buT=e(R, N), ad=e(R, N),
+                   adT=e(N, R), bd=e(K, R), bdT=e(R, K))
+        f = lambda t: t.detach().float().contiguous()  # noqa: E731
+        _native.lora_prep(f(Ag), f(Au), f(Bg), f(Bu), f(Ad), f(Bd), out)
+        return types.SimpleNamespace(**out)
+    return _cast((("lora_prep", id(Ag), id(Au), id(Bg), id(Bu), id(Ad), id(Bd)), dt), make)
 
 
 class _MLP(torch.autograd.Function):
@@ -142,14 +174,13 @@ class _MLP(torch.autograd.Function):
         x2 = x.reshape(-1, K)
         if x2.dtype != dt or not x2.is_contiguous():
             x2 = x2.to(dt).contiguous()
-        # same cache keys as the grouped linears so both paths share one bf16 copy per step
-        S = _cast(((id(Ag), id(Au)), dt), lambda: torch.cat([Ag.detach().to(dt), Au.detach().to(dt)]))
-        bg = _cast((id(Bg), dt), lambda: Bg.detach().to(dt))
-        bu = _cast((id(Bu), dt), lambda: Bu.detach().to(dt))
-        ad = _cast(((id(Ad),), dt), lambda: torch.cat([Ad.detach().to(dt)]))
-        bd = _cast((id(Bd), dt), lambda: Bd.detach().to(dt))
-        xs = x2 @ S.t()  # [T, 2R] = xa_gate | xa_up
-        T = x2.shape[0]
+        lw = _prep(Ag, Bg, Au, Bu, Ad, Bd, dt)  # every bf16 form of the LoRA weights, one kernel per step
+        S, bg, bu, ad, bd = lw.S, lw.bg, lw.bu, lw.ad, lw.bd
+        T, R = x2.shape[0], Ad.shape[0]
+        # xs = bf16(x2 · Sᵀ) [T, 2R] = xa_gate | xa_up, and its zero-padded transpose for the backward kernel
+        xs = torch.empty((T, 2 * R), dtype=dt, device=x2.device)
+        xsT = torch.empty((2 * R, _cdiv(T, 128) * 128), dtype=dt, device=x2.device)
+        _native.lora_nt(x2, S, xs, outT=xsT)
         # GEMM operands in the MX-tiled layout (same codes and scales as mx_quant; the GEMM streams 1 KB blocks)
         q, sc = mxfp8.mx_quant_tiled(x2)
         gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=3, m=T)  # [T, 2N] gate | up
@@ -165,6 +196,7 @@ class _MLP(torch.autograd.Function):
         # the same saved set in both modes (non-reentrant checkpointing compares metadata on recompute)
         ctx.save_for_backward(x2, xs, gu, S, bg, bu, ad, bd)
         ctx.meta = (hold, down, (s_g, s_u, s_d), dt, lead, K, x.dtype)
+        ctx.lw, ctx.xsT = lw, xsT  # the other weight forms and xsᵀ (small; not part of the reference's saved set)
         return y.view(*lead, y.shape[-1])
 
     @staticmethod
@@ -178,34 +210,39 @@ class _MLP(torch.autograd.Function):
         dy2 = dy.reshape(-1, dy.shape[-1]).to(dt)
         if not dy2.is_contiguous():
             dy2 = dy2.contiguous()
-        T = dy2.shape[0]
+        T, N = dy2.shape[0], hold.n
+        lw, xsT = ctx.lw, ctx.xsT
         qd, sd = mxfp8.mx_quant_tiled(dy2)
         dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=3, m=T)  # [T, N] = MX(dy) · W_down
         del qd, sd
-        dxd = dy2 @ bd
-        if s_d != 1:
-            dxd.mul_(s_d)
-        qg, sg, dxa, dB_g, dB_u, dA_d = mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_x, tiled=True)
+        # dxd = bf16(bf16(dy2 · bd) · s_d) [T, R], and its zero-padded transpose
+        dxd = torch.empty((T, R), dtype=dt, device=dy2.device)
+        dxdT = torch.empty((R, xsT.shape[1]), dtype=dt, device=dy2.device)
+        _native.lora_nt(dy2, lw.bdT, dxd, scale=s_d, outT=dxdT)
+        qg, sg, parts = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, lw.bgT, lw.buT, ad, lw.adT, s_g, s_u,
+                                    need_x, None, True)
         del dhm
-        dB_d = dy2.t() @ dxa[:, 2 * R:].to(dt)  # xS_down in bf16, as the unfused path saved it
-        if s_d != 1:
-            dB_d.mul_(s_d)
-        dxa = dxa[:, :2 * R]
-        if s_g != 1:
-            dxa[:, :R].mul_(s_g)
-            dB_g.mul_(s_g)
-        if s_u != 1:
-            dxa[:, R:].mul_(s_u)
-            dB_u.mul_(s_u)
-        dxa = dxa.to(dt)  # [T, 2R] contiguous
+        # the partial sums, scaled and cast as fused_mlp.py:258, :319-326 do, in one kernel
+        dxa = torch.empty((T, 2 * R), dtype=dt, device=dy2.device)  # bf16(s_g dxa_g | s_u dxa_u)
+        xsd = torch.empty((T, R), dtype=dt, device=dy2.device)      # bf16(xS_down)
+        dB_g = torch.empty((N, R), dtype=torch.float32, device=dy2.device)
+        dB_u = torch.empty_like(dB_g)
+        dA_d = torch.empty((R, N), dtype=torch.float32, device=dy2.device)
+        _native.mlp_bwd_finish(*parts, T, N, R, s_g, s_u, dxa, xsd, dB_g, dB_u, dA_d)
+        del parts
+        # the token reductions (fp32 tensors holding the bf16 results the reference's bf16 GEMMs return)
+        part = torch.empty(_native.lora_tn_chunks(T, K) * 2 * R * K, dtype=torch.float32, device=dy2.device)
+        dB_d = torch.empty((K, R), dtype=torch.float32, device=dy2.device)
+        _native.lora_tn(dy2, xsd, dB_d, part[:part.numel() // 2], scale=s_d, transpose=True)  # bf16(bf16(dyᵀ xsd) s_d)
         dx = None
         if need_x:
             # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
             # fused_mlp.py:331 in its epilogue
-            dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, S.t().contiguous()), alpha=1.0, layout=3, m=T)
+            dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
-        dA = dxa.t() @ x2
+        dA = torch.empty((2 * R, K), dtype=torch.float32, device=dy2.device)
+        _native.lora_tn(x2, dxa, dA, part)  # bf16(dxaᵀ · x2)
         grads = [dA[:R], dB_g, dA[R:], dB_u, dA_d, dB_d]
         ws_in = ctx.needs_input_grad[3:]
         return (dx, None, None, *[g if ws_in[k] else None for k, g in enumerate(grads)])
@@ -237,8 +274,9 @@ def mlp(mlp_mod, x, need_out=True):
     r = Ag.shape[0]
     T = x.numel() // x.shape[-1]
     if not (_r_ok(r) and Au.shape[0] == r and Ad.shape[0] == r and x.shape[-1] == hold.w.shape[1]
-            and hold.n % 256 == 0 and Ad.shape[1] == hold.n and T > 0 and T * 2 * hold.n < 2 ** 31):
-        return None  # (32-bit element indexing in the kernels; the backward kernel tiles N by 256)
+            and hold.n % 256 == 0 and x.shape[-1] % 256 == 0 and Ad.shape[1] == hold.n and T > 0
+            and T * 2 * hold.n < 2 ** 31):
+        return None  # (32-bit element indexing in the kernels; N and K tiled by 256)
     STATS["mlp gộp"] = STATS.get("mlp gộp", 0) + 1
     ACTIVE[0] = True
     return _MLP.apply(x, (hold, db, (s_g, s_u, s_d), dt), need_out, Ag, Bg, Au, Bu, Ad, Bd)
