@@ -139,7 +139,7 @@ int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu
  * :218-259).  Inputs as in the forward plus dhm [T, N] bf16 (MX(dy)·W_down), dxd [T, r] bf16 (s_d·dy·B_d) and
  * the small transposed copies xsT [2r, Tpad], dxdT [r, Tpad] (zero past T; Tpad = ceil(T/128)*128),
  * bgT, buT [r, N], adT [N, r].  Grid: super-blocks of SB rows (SB % 128 == 0) x column groups of CG columns
- * (CG % 256 == 0, N % CG == 0).  Outputs:
+ * (CG % 128 == 0, N % CG == 0).  Outputs:
  *   q [T, 2N] + s (2N/128 tiles per row): MX(dg) in columns 0..N-1, MX(du) in N..2N-1  (skipped if q == NULL)
  *   dxa_part [N/CG, T, 3r] fp32: dxa_g | dxa_u | xS_down partial sums over each column group (unscaled)
  *   dbg_part, dbu_part [ceil(Tpad/SB), N, r] fp32 and dad_part [ceil(Tpad/SB), r, N]: per super-block sums of
