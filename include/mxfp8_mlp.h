@@ -25,9 +25,13 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 2
+#define MXFP8_MLP_ABI_VERSION 3
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
+/* mxfp8_gemm_nt layout bits */
+#define MXFP8_GEMM_A_TILED 1
+#define MXFP8_GEMM_B_TILED 2
+#define MXFP8_GEMM_WIDE 4
 
 /* Returns MXFP8_MLP_ABI_VERSION of the built library (the Python loader refuses a mismatch). */
 int mxfp8_abi_version(void);
@@ -91,12 +95,14 @@ int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
  *   C = bf16( bf16(A·Bᵀ) + alpha * P[M, r] · Q[N, r]ᵀ ),  P, Q bf16 with row strides ld_p, ld_q,
  *   r in {16, 32, 64}.
  * Requires K % 128 == 0, N % 128 == 0, lda/ldb % 16 == 0, ldc % 4 == 0.
- * layout: bit 0 set = A codes in the MX-tiled layout (mxfp8_quant_tiled / mxfp8_tile_codes, lda ignored),
- * bit 1 = the same for B.  Results are bit-identical to the row-major operands; the tiled layout lets every
- * DMA of the GEMM move a contiguous 1 KB instead of sixteen 64-byte row pieces.
- * workspace (optional, 256-byte aligned, workspace_bytes long): when it holds at least
- * mxfp8_gemm_workspace_size(M, N, K) bytes, the tiles of a last wave that would leave more than half of the
- * CUs idle are split along K; their fp32 pieces go through the workspace and are added in a fixed order
+ * layout bits: MXFP8_GEMM_A_TILED = A codes in the MX-tiled layout (mxfp8_quant_tiled / mxfp8_tile_codes,
+ * lda ignored), MXFP8_GEMM_B_TILED = the same for B (results are bit-identical to row-major operands; the
+ * tiled layout lets every DMA of the GEMM move a contiguous 1 KB instead of sixteen 64-byte row pieces);
+ * MXFP8_GEMM_WIDE = 8-wave 256 x 256 workgroups, one per CU, instead of the default 4-wave 256 x 128, two per
+ * CU (same result bits when no tile is split).
+ * workspace (optional, 256-byte aligned, workspace_bytes long; used with MXFP8_GEMM_WIDE only): when it holds
+ * at least mxfp8_gemm_workspace_size(M, N, K) bytes, the tiles of a last wave that would leave more than half
+ * of the CUs idle are split along K; their fp32 pieces go through the workspace and are added in a fixed order
  * (the result does not depend on scheduling).  Its first 4 KB are arrival counters that must be zero before
  * the first call (allocate it zeroed); every call leaves them zero.  Calls that share a workspace must not run
  * concurrently.  NULL / too small: every tile runs whole (same result bits as with the split only where no
@@ -108,8 +114,8 @@ int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, con
                   int64_t workspace_bytes, void* stream);
 
 /*
- * Bytes of workspace mxfp8_gemm_nt uses for this shape on the current device (0: no split).  No reference
- * counterpart: torch._scaled_mm (fused_mlp.py:279) manages the cuBLAS workspace itself.
+ * Bytes of workspace mxfp8_gemm_nt uses for this shape with MXFP8_GEMM_WIDE on the current device (0: no
+ * split).  No reference counterpart: torch._scaled_mm (fused_mlp.py:279) manages the cuBLAS workspace itself.
  */
 int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
 

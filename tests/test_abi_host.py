@@ -60,13 +60,13 @@ def test_argument_checks_reject_before_launch(lib):
     # GEMM epilogue rank not supported
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, p, 8, p, 8, 8, 1.0, 0, None, 0, None) == -1
     # unknown operand layout
-    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 4, None, 0, None) == -1
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 8, None, 0, None) == -1
     assert b"layout" in lib.mxfp8_last_error()
     # workspace given but misaligned
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 0,
                              ctypes.c_void_p(16), 1 << 20, None) == -1
     assert b"workspace" in lib.mxfp8_last_error()
-    # backward column group must divide N and be a multiple of 256
+    # backward column group must divide N and be a multiple of 128
     args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, 0, None]
     assert lib.mxfp8_mlp_bwd(*args) == -1
     # LoRA products: K must be a multiple of 256 (x · Wᵀ) / 128 (token reduction), rp in {16, 32, 64}
@@ -82,8 +82,9 @@ def test_argument_checks_reject_before_launch(lib):
 
 
 def test_gemm_workspace_plan(lib):
-    # without a GPU the library plans for 256 CUs (MI355X): tail waves that fill at most half of the CUs are
-    # split along K into up to 4 pieces of an even number of 64-wide K steps; 4 KB of counters come first
+    # the 8-wave shape's plan (the default 4-wave shape never splits); without a GPU the library plans for 256
+    # CUs (MI355X): tail waves that fill at most half of the CUs are split along K into up to 4 pieces of an
+    # even number of 64-wide K steps; 4 KB of counters come first
     ws = lib.mxfp8_gemm_workspace_size
     part = 256 * 256 * 4
     assert ws(10752, 12288, 2048) == 0  # 2016 tiles: last wave 224 of 256 CUs

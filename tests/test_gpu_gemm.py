@@ -31,15 +31,16 @@ def _assert_close(got, ref):
     assert bad.numel() == 0, (bad[:5].tolist(), err.max().item())
 
 
+@pytest.mark.parametrize("wide", [0, 4])
 @pytest.mark.parametrize("M,N,K", [(256, 256, 128), (300, 384, 256), (1, 128, 128), (513, 640, 1152),
                                    (256, 7168, 1024), (1000, 1024, 3584)])
-def test_gemm_random(M, N, K, gpu):
+def test_gemm_random(M, N, K, wide, gpu):
     g = torch.Generator().manual_seed(M * 31 + N * 7 + K)
     a = (torch.randn(M, K, generator=g) * torch.exp2(torch.randint(-6, 6, (M, 1), generator=g).float()))
     b = torch.randn(N, K, generator=g) * 0.02
     qa, sa = mxfp8.mx_quant(a.to(torch.bfloat16).to(gpu))
     qb, sb = mxfp8.mx_quant(b.to(torch.bfloat16).to(gpu))
-    c = mxfp8.mx_mm(qa, sa, qb, sb)
+    c = mxfp8.mx_mm(qa, sa, qb, sb, layout=wide)
     _assert_close(c, _ref_gemm_f64(qa, sa, qb, sb, M, N, K))
 
 
@@ -108,15 +109,17 @@ def _operands(M, N, K, seed, gpu):
 
 @pytest.mark.parametrize("M,N,K", [(256, 7168, 1024), (1000, 1024, 3584), (10752, 2048, 6144)])
 def test_gemm_split_tail(M, N, K, gpu):
-    # tail tiles split along K (the workspace plan) against every tile run whole: the same exact products
-    # summed in another fp32 order, so at most one bf16 step apart; repeated split runs are bit-identical
-    # (pieces are added in part order, whatever order they finish in) and leave the counters at zero
+    # 8-wave shape: tail tiles split along K (the workspace plan) against every tile run whole: the same exact
+    # products summed in another fp32 order, so at most one bf16 step apart; repeated split runs are
+    # bit-identical (pieces are added in part order, whatever order they finish in) and leave the counters at
+    # zero; the default 4-wave shape never splits and matches the whole 8-wave run bit for bit
     import _native
     assert _native.load().mxfp8_gemm_workspace_size(M, N, K) > 0
     qa, sa, qb, sb = _operands(M, N, K, M + N + K, gpu)
     whole = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
-    _native.gemm_nt(qa, sa, K, qb, sb, K, M, N, K, whole, split=False)
-    c1, c2 = mxfp8.mx_mm(qa, sa, qb, sb), mxfp8.mx_mm(qa, sa, qb, sb)
+    _native.gemm_nt(qa, sa, K, qb, sb, K, M, N, K, whole, split=False, layout=_native.GEMM_WIDE)
+    assert torch.equal(mxfp8.mx_mm(qa, sa, qb, sb), whole)
+    c1, c2 = mxfp8.mx_mm(qa, sa, qb, sb, layout=4), mxfp8.mx_mm(qa, sa, qb, sb, layout=4)
     assert torch.equal(c1, c2)
     ws, _ = _native.gemm_workspace(M, N, K, c1.device)
     assert int(torch.count_nonzero(ws[:4096])) == 0
@@ -135,8 +138,8 @@ def test_gemm_split_lora_epilogue(gpu):
     Q = (torch.randn(N, r, generator=g) * 0.5).to(torch.bfloat16)
     import _native
     assert _native.load().mxfp8_gemm_workspace_size(M, N, K) > 0
-    c0 = mxfp8.mx_mm(qa, sa, qb, sb)
-    c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P.to(gpu), Q.to(gpu)), alpha=2.0)
+    c0 = mxfp8.mx_mm(qa, sa, qb, sb, layout=4)
+    c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P.to(gpu), Q.to(gpu)), alpha=2.0, layout=4)
     ref = (c0.float().cpu() + 2.0 * (P.float() @ Q.float().t())).to(torch.bfloat16).float()
     err = (c.float().cpu() - ref).abs()
     assert (err <= ref.abs() * 2.0 ** -7 + 1e-4).all(), err.max()
@@ -148,9 +151,15 @@ def test_gemm_tiled_operands_bit_identical(M, N, K, gpu):
     qa, sa, qb, sb = _operands(M, N, K, 3 * M + N, gpu)
     ref = mxfp8.mx_mm(qa, sa, qb, sb)
     ta, tb = mxfp8.tile_codes(qa), mxfp8.tile_codes(qb)
-    for layout, a, b in ((1, ta, qb), (2, qa, tb), (3, ta, tb)):
+    for layout, a, b in ((1, ta, qb), (2, qa, tb), (3, ta, tb), (5, ta, qb), (6, qa, tb), (7, ta, tb)):
         c = mxfp8.mx_mm(a, sa, b, sb, layout=layout, m=M)
-        assert torch.equal(c, ref), layout
+        if layout & 4:  # the 8-wave shape may split tail tiles along K: compare with its own whole run
+            import _native
+            w = torch.empty_like(c)
+            _native.gemm_nt(qa, sa, K, qb, sb, K, M, N, K, w, layout=4)
+            assert torch.equal(c, w), layout
+        else:
+            assert torch.equal(c, ref), layout
     # and with the rank-r epilogue
     g = torch.Generator().manual_seed(M)
     P = torch.randn(M, 16, generator=g).to(torch.bfloat16).to(gpu)

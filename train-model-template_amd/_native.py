@@ -11,7 +11,8 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
+GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE = 1, 2, 4  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
 
@@ -144,7 +145,8 @@ def gemm_workspace(M, N, K, device):
 
 def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0, split=True, layout=0):
     """c[M, N] = bf16(A·Bᵀ) [+ alpha · P·Qᵀ with lora = (P [M, r], Q [N, r])].  layout bit 0 / 1: A / B codes
-    MX-tiled.  split=False runs every tile whole (no workspace)."""
+    MX-tiled; bit 2 (GEMM_WIDE): 8-wave 256 x 256 workgroups, whose tail tiles split along K through the cached
+    workspace unless split=False."""
     if lora is None:
         p = q = None
         ldp = ldq = r = 0
@@ -153,7 +155,7 @@ def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0, split=True
         r = p.shape[1]
         ldp, ldq = p.stride(0), q.stride(0)
     _gpu(c, "mxfp8_gemm_nt")
-    ws, ws_bytes = gemm_workspace(M, N, K, c.device) if split else (None, 0)
+    ws, ws_bytes = gemm_workspace(M, N, K, c.device) if split and layout & GEMM_WIDE else (None, 0)
     call("mxfp8_gemm_nt", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(p), ldp,
          _p(q), ldq, r, float(alpha), layout, _p(ws), ws_bytes, like=c)
 

@@ -4,13 +4,19 @@
 // Replaces torch._scaled_mm (cuBLAS block-scaled GEMM) at /root/reference/scripts/fused_mlp.py:279, :283, :309,
 // :329 and the addmm_ epilogues at :284 and :331.
 //
-// Tiling: a 512-thread workgroup computes a 256 (M) x 256 (N) tile in K steps of 64 (two scale blocks).
-// The eight waves form a 2 (N) x 4 (M) grid of 128 x 64 sub-tiles, each a 4 x 2 grid of 32 x 32 MFMA tiles
-// (128 accumulators per lane); two waves share each SIMD, so while one waits at a step's barrier or for its
-// LDS reads the other keeps the matrix pipe busy (measured: with one wave per SIMD and 128 x 128
-// sub-tiles the per-step barrier drains the pipe and the kernel is slower, although it reads LDS less).
-// The matrix instruction takes the weight (B) fragment as its first operand, so each lane's accumulators
-// cover one output row m and 16 columns n in runs of 4.
+// Tiling: a workgroup computes a 256 (M) x 128 (N) tile with four waves, two workgroups per CU (kNW = 1;
+// layout bit MXFP8_GEMM_WIDE selects the 8-wave 256 x 256 shape, kNW = 2, one workgroup per CU), in K steps
+// of 64 (two scale blocks).  Measured on the four MLP GEMMs (T=10752, d=2048, f=6144): 845-858 us at
+// kNW = 1 against 873-908 us at kNW = 2 with its best tail split.  Each wave
+// holds a 64 (M) x 128 (N) sub-tile as a 2 x 4 grid of 32 x 32 MFMA tiles (128 accumulators per lane), so two
+// waves share each SIMD; with two independent workgroups per CU one workgroup's pipeline fill, barrier waits
+// and epilogue overlap the other's matrix work.  The matrix instruction takes the weight (B) fragment as its
+// first operand, so each lane's accumulators cover one output row m and 16 columns n in runs of 4.
+//
+// What bounds it (rocprofv3 counters on the MLP GEMMs): the CU's vector-memory path that carries the
+// operand DMA (TA / TD busy 65-89% of the kernel, TD waiting on L1/L2 data about 45% of the time) while the
+// matrix pipe is busy ~48%.  LDS reads overlap MFMAs well on gfx950 (a software-pipelined fragment-read +
+// MFMA loop runs at 94-97% of the MFMA-only rate), and an L2 prefetch ahead of the ring made it slower.
 //
 // Operand layouts: row-major codes (row stride lda / ldb), or the MX-tiled layout (tiled_offset in
 // mx_device.h) in which each 16-row x 64-code slice is one contiguous 1 KB block in LDS order.  The GEMM is
@@ -20,23 +26,24 @@
 // bit-identical.
 //
 // Operand staging: global memory goes straight into LDS with global_load_lds_dwordx4 (no VGPR round trip)
-// through a ring of 4 stages of 34 KB: A codes 256 x 64 B, B codes 256 x 64 B, and the two 128-row blocked
-// scale tiles of each operand for the current 128-wide K tile.  Every wave issues exactly five DMA
-// instructions per stage (four 1 KB code slices plus a scale tile or a duplicate), so a fixed vmcnt bounds the wait
-// for a stage while the next two stay in flight.  Lane i of a DMA lands at base + 16 i; a row's 16-byte
-// chunk c is stored at chunk c ^ ((row >> 2) & 3): the gfx950 LDS serves a ds_read_b128 16 lanes (16
-// consecutive rows, same chunk) at a time over 64 banks, and with 64-byte rows rows r, r+4, r+8, r+12 share
-// bank groups unless their chunks differ (measured: 48% bank-conflict cycles with a (row >> 1) swizzle).
+// through a ring of 3 stages of 26 KB (kNW = 2: 4 of 34 KB): A codes 256 x 64 B, B codes 128 x 64 B, and the
+// 128-row blocked scale tiles of each operand for the current 128-wide K tile.  Every wave issues the same
+// number of DMA instructions per stage (1 KB code slices of A and of B plus a scale tile or a duplicate), so a
+// fixed vmcnt bounds the wait for a stage while the later ones stay in flight.  Lane i of a DMA lands at
+// base + 16 i; a row's 16-byte chunk c is stored at chunk c ^ ((row >> 2) & 3): the gfx950 LDS serves a
+// ds_read_b128 16 lanes (16 consecutive rows, same chunk) at a time over 64 banks, and with 64-byte rows
+// rows r, r+4, r+8, r+12 share bank groups unless their chunks differ (measured: 48% bank-conflict cycles
+// with a (row >> 1) swizzle).
 // Scale words: for a 32-row group the 16 bytes at (row % 32) * 16 of a blocked tile hold the four 32-row
 // groups' scales for one 128-wide K tile; a lane shifts its word by 8 * (lane / 32) so that op_sel 0 / 2
 // selects block 2P + lane/32 of the current half-tile P.
 // Work order: a 1-D grid in which workgroup i runs on XCD i % 8 (the dispatcher's round robin).  Tiles are
 // numbered in groups of kGroupM M-tiles (M fastest inside a group) and each XCD takes a contiguous range of
-// that order, so the ~32 tiles resident on one XCD share A and B panels in its L2.  When the last wave of
-// tiles would fill at most half of the CUs, those tail tiles are split along K into `parts` pieces run as
-// separate workgroups after the full tiles; each piece writes its fp32 accumulators to the caller's
-// workspace, and the piece that arrives last (agent-scope counter) adds the pieces in part order, which
-// makes the result independent of arrival order, runs the epilogue and resets its counter to zero.
+// that order, so the tiles resident on one XCD share A and B panels in its L2.  With the 8-wave shape, when
+// the last wave of tiles would fill at most half of the CUs, those tail tiles are split along K into `parts`
+// pieces run as separate workgroups after the full tiles; each piece writes its fp32 accumulators to the
+// caller's workspace, and the piece that arrives last (agent-scope counter) adds the pieces in part order,
+// which makes the result independent of arrival order, runs the epilogue and resets its counter to zero.
 #include <type_traits>
 
 #include "abi_common.h"
@@ -46,17 +53,30 @@ using namespace mxk;
 
 namespace {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4, kThreads = 512;
-constexpr int kCodeBytes = kBM * kBK;                 // 16 KB per operand per stage
-constexpr int kOffA = 0, kOffB = kCodeBytes, kOffSA = 2 * kCodeBytes, kOffSB = 2 * kCodeBytes + 1024;
-constexpr int kStageBytes = 2 * kCodeBytes + 2048;    // 34 KB
+constexpr int kBM = 256, kBK = 64;
+constexpr int kCodeBytes = kBM * kBK;  // A codes per stage: 16 KB
 constexpr int kGroupM = 4;
 constexpr int kMaxParts = 4;
-constexpr int64_t kPartBytes = (int64_t)kBM * kBN * 4;  // fp32 partial tile
 // Workspace layout: arrival counters at a fixed place (so every shape finds its own counters at zero, each
 // launch resets those it used), fp32 partial tiles after them.
 constexpr int64_t kCounterBytes = 4096;
 constexpr int kMaxSplitTiles = (int)(kCounterBytes / 4);
+
+// Workgroup shapes.  kNW = 2: 8 waves, 256 x 256 tile, 4-stage ring of 34 KB (one workgroup per CU).
+// kNW = 1: 4 waves, 256 x 128 tile, 3-stage ring of 26 KB (two workgroups per CU, whose barriers are
+// independent, so one workgroup's MFMAs fill the other's waits).  Every wave computes a 64 (M) x 128 (N)
+// sub-tile either way.
+template <int kNW>
+struct Shape {
+  static constexpr int kWaves = 4 * kNW, kThreads = 64 * kWaves, kBN = 128 * kNW;
+  static constexpr int kStages = kNW == 2 ? 4 : 3;
+  static constexpr int kOffA = 0, kOffB = kCodeBytes, kOffSA = kCodeBytes + kBN * kBK, kOffSB = kOffSA + 1024;
+  static constexpr int kStageBytes = kOffSB + 1024;
+  // DMA per wave and stage: kSA 1 KB slices of A, kSB of B, and one more (A's or B's scale tiles, or a
+  // repeat of the wave's last B slice), so a fixed vmcnt bounds every wait.
+  static constexpr int kSA = 16 / kWaves, kSB = (kBN / 16) / kWaves, kDma = kSA + kSB + 1;
+  static constexpr int64_t kPartBytes = (int64_t)kBM * kBN * 4;  // fp32 partial tile
+};
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -117,14 +137,13 @@ __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw
   return r;
 }
 
-template <int kR>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restrict__ A,
-                                                        const uint8_t* __restrict__ SA, int64_t lda,
-                                                        const uint8_t* __restrict__ B,
-                                                        const uint8_t* __restrict__ SB, int64_t ldb, int M, int N,
-                                                        int K, uint16_t* __restrict__ C, int64_t ldc, Lora lora,
-                                                        Plan plan, int tiled) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageBytes];
+template <int kR, int kNW>
+__global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
+    const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, int64_t lda, const uint8_t* __restrict__ B,
+    const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, uint16_t* __restrict__ C, int64_t ldc,
+    Lora lora, Plan plan, int tiled) {
+  using S = Shape<kNW>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[S::kStages * S::kStageBytes];
   __shared__ int arrived;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -150,51 +169,55 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   }
   int mt_, nt_;
   tile_coords(tile, plan.tm, plan.tn, mt_, nt_);
-  const int m0 = mt_ * kBM, n0 = nt_ * kBN;
+  const int m0 = mt_ * kBM, n0 = nt_ * S::kBN;
   const int nkt = K / 128;
 
-  // DMA roles: waves 0-3 stage A, waves 4-7 stage B; wave slot w4 = wave & 3 covers rows w4*64 + [0, 64)
-  // in four 1 KB slices (16 rows x 64 B), lane -> row slice*16 + lane/4, physical chunk lane & 3.
-  const bool dB = wave >= 4;
-  const int w4 = wave & 3;
-  const int R0 = dB ? n0 : m0, Rn = dB ? N : M;
-  const int64_t ldd = dB ? ldb : lda;
-  // Row-major operand: lane -> row slice*16 + lane/4 of the wave's rows, logical chunk chosen so that the
-  // lane's 16 bytes land at their swizzled LDS position.  MX-tiled operand (tiled_offset in mx_device.h):
-  // the slice is one contiguous 1 KB block already in LDS order, lane i copies bytes 16i..16i+15, and a K
-  // step advances 1 KB instead of 64 B.
-  const bool op_tiled = (tiled >> (dB ? 1 : 0)) & 1;
+  // DMA roles: wave w stages A rows w*16*kSA + [0, 16*kSA) and B rows w*16*kSB + [0, 16*kSB) in 1 KB slices
+  // (16 rows x 64 B).  Row-major operand: lane -> row slice*16 + lane/4, logical chunk chosen so that the
+  // lane's 16 bytes land at their swizzled LDS position.  MX-tiled operand (tiled_offset in mx_device.h): the
+  // slice is one contiguous 1 KB block already in LDS order, lane i copies bytes 16i..16i+15, and a K step
+  // advances 1 KB instead of 64 B.
+  const bool a_tiled = tiled & 1, b_tiled = (tiled >> 1) & 1;
   const int kst = K / kBK;
-  const uint8_t* gb = (dB ? B : A) + (op_tiled ? (int64_t)(R0 >> 4) * kst * 1024 : (int64_t)R0 * ldd);
-  const int sstride = op_tiled ? 1024 : kBK;
   const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3 for these rows
-  uint32_t goff[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  auto slice_off = [&](bool op_tiled, int R0, int Rn, int64_t ldd, int rbase) -> uint32_t {
     if (op_tiled) {
-      const int rg = min((R0 >> 4) + w4 * 4 + j, ((Rn + 15) >> 4) - 1) - (R0 >> 4);  // clamp past the end
-      goff[j] = (uint32_t)(rg * kst * 1024) + lane * 16;
-    } else {
-      const int row = w4 * 64 + j * 16 + (lane >> 2);
-      goff[j] = (uint32_t)((min(R0 + row, Rn - 1) - R0) * ldd) + lchunk * 16;  // clamp rows past the end
+      const int rg = min((R0 >> 4) + (rbase >> 4), ((Rn + 15) >> 4) - 1) - (R0 >> 4);  // clamp past the end
+      return (uint32_t)(rg * kst * 1024) + lane * 16;
     }
-  }
-  // Fifth DMA of the stage, without divergence: waves 0 and 4 copy the two 128-row scale tiles of their
-  // operand (1 KB, lane -> tile lane / 32, bytes (lane % 32) * 16 of it); the other waves repeat their fourth
-  // code slice (same source, same destination: a harmless duplicate).
-  const bool scl = w4 == 0;
-  const int stile = min((R0 >> 7) + (lane >> 5), (Rn - 1) >> 7);
-  const uint8_t* sgp = (dB ? SB : SA) + (int64_t)stile * nkt * 512 + (lane & 31) * 16;
-  const int dma_code_off = (dB ? kOffB : kOffA) + w4 * 4096;
-  const int dma5_off = scl ? (dB ? kOffSB : kOffSA) : dma_code_off + 3 * 1024;
+    const int row = rbase + (lane >> 2);
+    return (uint32_t)((min(R0 + row, Rn - 1) - R0) * ldd) + lchunk * 16;  // clamp rows past the end
+  };
+  const uint8_t* ga = A + (a_tiled ? (int64_t)(m0 >> 4) * kst * 1024 : (int64_t)m0 * lda);
+  const uint8_t* gb = B + (b_tiled ? (int64_t)(n0 >> 4) * kst * 1024 : (int64_t)n0 * ldb);
+  const int sa_stride = a_tiled ? 1024 : kBK, sb_stride = b_tiled ? 1024 : kBK;
+  uint32_t goa[S::kSA], gob[S::kSB];
+#pragma unroll
+  for (int j = 0; j < S::kSA; ++j) goa[j] = slice_off(a_tiled, m0, M, lda, (wave * S::kSA + j) * 16);
+#pragma unroll
+  for (int j = 0; j < S::kSB; ++j) gob[j] = slice_off(b_tiled, n0, N, ldb, (wave * S::kSB + j) * 16);
+  // Last DMA of the stage, without divergence: wave 0 copies A's two 128-row scale tiles, wave 1 B's
+  // scale tile(s) (1 KB, lane -> tile lane / 32, bytes (lane % 32) * 16 of it; for a 128-row B tile the
+  // upper half holds the next tile's, unused); the other waves repeat their last B slice (same source, same
+  // destination: a harmless duplicate).
+  const bool scl = wave < 2;
+  const int sR0 = wave == 0 ? m0 : n0, sRn = wave == 0 ? M : N;
+  const int stile = min((sR0 >> 7) + (lane >> 5), (sRn - 1) >> 7);
+  const uint8_t* sgp = (wave == 0 ? SA : SB) + (int64_t)stile * nkt * 512 + (lane & 31) * 16;
+  const int dma_a_off = S::kOffA + wave * S::kSA * 1024, dma_b_off = S::kOffB + wave * S::kSB * 1024;
+  const int dma_x_off = wave == 0 ? S::kOffSA : wave == 1 ? S::kOffSB : dma_b_off + (S::kSB - 1) * 1024;
 
   const uint32_t lds0 = lds_addr(lds);
+  const int last = s_end - 1;
   auto issue_to = [&](int s, int slot) {  // DMA stage s into ring slot `slot`
-    const uint32_t st = lds0 + slot * kStageBytes;
-    const uint8_t* g = gb + s * sstride;
+    const uint32_t st = lds0 + slot * S::kStageBytes;
+    const uint8_t* pa = ga + s * sa_stride;
+    const uint8_t* pb = gb + s * sb_stride;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(g + goff[j], st + dma_code_off + j * 1024);
-    dma16(scl ? sgp + (s >> 1) * 512 : g + goff[3], st + dma5_off);
+    for (int j = 0; j < S::kSA; ++j) dma16(pa + goa[j], st + dma_a_off + j * 1024);
+#pragma unroll
+    for (int j = 0; j < S::kSB; ++j) dma16(pb + gob[j], st + dma_b_off + j * 1024);
+    dma16(scl ? sgp + (s >> 1) * 512 : pb + gob[S::kSB - 1], st + dma_x_off);
   };
 
   v16f acc[4][2];
@@ -213,11 +236,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
     uint4 sb;
   };
   auto read = [&](int slot, Frags& f) {
-    const uint8_t* st = lds + slot * kStageBytes;
-    f.sa = *reinterpret_cast<const uint2*>(st + kOffSA + (wm >> 1) * 512 + (lane & 31) * 16 + (wm & 1) * 8);
-    f.sb = *reinterpret_cast<const uint4*>(st + kOffSB + wn * 512 + (lane & 31) * 16);
-    const uint8_t* la = st + kOffA;
-    const uint8_t* lb = st + kOffB;
+    const uint8_t* st = lds + slot * S::kStageBytes;
+    f.sa = *reinterpret_cast<const uint2*>(st + S::kOffSA + (wm >> 1) * 512 + (lane & 31) * 16 + (wm & 1) * 8);
+    f.sb = *reinterpret_cast<const uint4*>(st + S::kOffSB + wn * 512 + (lane & 31) * 16);
+    const uint8_t* la = st + S::kOffA;
+    const uint8_t* lb = st + S::kOffB;
     f.a0 = frag(la, wm * 64 + (lane & 31), c0, sw);
     f.a1 = frag(la, wm * 64 + 32 + (lane & 31), c0, sw);
     f.b0 = frag(lb, wn * 128 + (lane & 31), c0, sw);
@@ -241,28 +264,27 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   };
   // Steady state, branch-free (with conditional blocks the compiler sinks a stage's MFMAs below the next
   // barrier).  Step s: wait until stage s + 1 has landed (this wave's DMA) and this wave's reads of stage s are
-  // in registers, barrier, refill the slot of stage s with stage s + 4, read stage s + 1's fragments, then
-  // run stage s's MFMAs from registers, so LDS latency and the DMA issue overlap the matrix work.  Every step
-  // issues five DMA instructions per wave; stages past the end re-load the last stage into the slot just
-  // consumed (no later step reads it), so exactly two stages are in flight behind the one waited for.
-  const int last = s_end - 1;
+  // in registers, barrier, refill the slot of stage s with stage s + kStages, read stage s + 1's fragments,
+  // then run stage s's MFMAs from registers, so LDS latency and the DMA issue overlap the matrix work.  Every
+  // step issues kDma DMA instructions per wave; stages past the end re-load the last stage into the slot just
+  // consumed (no later step reads it), so exactly kStages - 2 stages are in flight behind the one waited for.
+  int slot = 0;  // ring slot of stage s (wave-uniform)
   auto step = [&](int s, Frags& cur, Frags& nxt, auto pc) {
-    wait_vmcnt<10>();
+    wait_vmcnt<(S::kStages - 2) * S::kDma>();
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     // Bare s_barrier: __syncthreads() adds a workgroup fence that waits for every outstanding DMA
     // (vmcnt(0)), which would drain the ring.
     __builtin_amdgcn_s_barrier();
-    issue_to(min(s + 4, last), (s - s_begin) & (kStages - 1));
-    read((s + 1 - s_begin) & (kStages - 1), nxt);
+    issue_to(min(s + S::kStages, last), slot);
+    slot = slot + 1 == S::kStages ? 0 : slot + 1;
+    read(slot, nxt);
     mma(cur, pc);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  issue_to(s_begin, 0);
-  issue_to(min(s_begin + 1, last), 1);
-  issue_to(min(s_begin + 2, last), 2);
-  issue_to(min(s_begin + 3, last), 3);
-  wait_vmcnt<15>();  // stage s_begin landed
+#pragma unroll
+  for (int q = 0; q < S::kStages; ++q) issue_to(min(s_begin + q, last), q);
+  wait_vmcnt<(S::kStages - 1) * S::kDma>();  // stage s_begin landed
   __builtin_amdgcn_s_barrier();
   Frags f0, f1;
   read(0, f0);
@@ -275,7 +297,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
   if (part >= 0) {
     // split tile: publish this piece, and let the last piece to arrive finish the tile
     const int st_ = tile - plan.full;
-    float4* wsp = plan.ws + (((int64_t)st_ * plan.parts + part) * 8 + wave) * (32 * 64) + lane;
+    float4* wsp = plan.ws + (((int64_t)st_ * plan.parts + part) * S::kWaves + wave) * (32 * 64) + lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -290,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
     __syncthreads();
     if (arrived != plan.parts - 1) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // see the other pieces' stores
-    const float4* wsb = plan.ws + ((int64_t)st_ * plan.parts * 8 + wave) * (32 * 64) + lane;
+    const float4* wsb = plan.ws + ((int64_t)st_ * plan.parts * S::kWaves + wave) * (32 * 64) + lane;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -301,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const uint8_t* __restric
           for (int p = 0; p < plan.parts; ++p) {
             const float4 v = p == part ? make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                                                      acc[i][j][4 * q + 3])
-                                       : wsb[(int64_t)p * 8 * 32 * 64 + ((i * 2 + j) * 4 + q) * 64];
+                                       : wsb[(int64_t)p * S::kWaves * 32 * 64 + ((i * 2 + j) * 4 + q) * 64];
             if (p == 0) {
               t = v;
             } else {
@@ -367,19 +389,25 @@ int cached_cus() {
   return cus[dev];
 }
 
-// Split the tail wave along K when it would leave more than half of the CUs idle (one workgroup per CU:
-// the LDS ring takes 136 KB).  Returns the workspace bytes the plan needs (0 without a split).
+// Split the tail wave along K when it would leave more than half of the workgroup slots idle (slots = CUs x
+// workgroups per CU: the LDS ring takes 136 KB at kNW = 2, 78 KB at kNW = 1).  Returns the workspace bytes
+// the plan needs (0 without a split).
+template <int kNW>
 int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
+  using S = Shape<kNW>;
+  const int slots = cus * (kNW == 2 ? 1 : 2);
   p.tm = (int)((M + kBM - 1) / kBM);
-  p.tn = (int)((N + kBN - 1) / kBN);
+  p.tn = (int)((N + S::kBN - 1) / S::kBN);
   const int total = p.tm * p.tn, ns = (int)(K / kBK);
-  const int rem = total % cus;
+  const int rem = total % slots;
   p.full = total;
   p.nsplit = 0;
   p.parts = 1;
   p.chunk = ns;
-  if (rem > 0 && 2 * rem <= cus && rem <= kMaxSplitTiles) {
-    int parts = min(kMaxParts, cus / rem);
+  // Two co-resident workgroups per CU already overlap one tile's pipeline fill and epilogue with the other's
+  // main loop; splitting the tail along K measured slower there (down: 184-199 us split vs 143-149 whole).
+  if (kNW == 2 && rem > 0 && 2 * rem <= slots && rem <= kMaxSplitTiles) {
+    int parts = min(kMaxParts, slots / rem);
     int chunk = 2 * ((ns + 2 * parts - 1) / (2 * parts));
     parts = (ns + chunk - 1) / chunk;
     if (parts >= 2 && chunk >= 4) {
@@ -392,7 +420,21 @@ int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
   p.per_full = (p.full + 7) / 8;
   p.per_split = (p.nsplit * p.parts + 7) / 8;
   if (!p.nsplit) return 0;
-  return kCounterBytes + (int64_t)p.nsplit * p.parts * kPartBytes;
+  return kCounterBytes + (int64_t)p.nsplit * p.parts * S::kPartBytes;
+}
+
+template <int kNW>
+void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, const uint8_t* SB, int64_t ldb,
+            int M, int N, int K, uint16_t* C, int64_t ldc, const Lora& lo, int r, const Plan& plan, int layout,
+            hipStream_t stm) {
+  using S = Shape<kNW>;
+  dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
+#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, C, ldc, lo, plan, layout
+  if (!lo.p) gemm_kernel<0, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 16) gemm_kernel<16, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 32) gemm_kernel<32, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else gemm_kernel<64, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+#undef GEMM_ARGS
 }
 
 }  // namespace
@@ -400,7 +442,7 @@ int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
 extern "C" int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 128 || N % 128) return 0;
   Plan p;
-  return make_plan(M, N, K, cached_cus(), p);
+  return make_plan<2>(M, N, K, cached_cus(), p);  // only the 8-wave shape splits
 }
 
 extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
@@ -412,7 +454,8 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
                "mxfp8_gemm_nt: need K %% 128 == 0 and N %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                (long long)N, (long long)K);
   MX_CHECK_ARG(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "mxfp8_gemm_nt: dimension too large");
-  MX_CHECK_ARG(layout >= 0 && layout <= 3, "mxfp8_gemm_nt: layout must be 0..3 (bit 0: A MX-tiled, bit 1: B)");
+  MX_CHECK_ARG(layout >= 0 && layout <= 7,
+               "mxfp8_gemm_nt: layout must be 0..7 (bit 0: A MX-tiled, bit 1: B MX-tiled, bit 2: 8-wave shape)");
   if (layout & 1) lda = K;  // the tiled layout has no row stride
   if (layout & 2) ldb = K;
   MX_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0 && ldc >= N && ldc % 4 == 0,
@@ -431,7 +474,8 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
   }
   if (M == 0) return MXFP8_OK;
   Plan plan;
-  const int64_t need = make_plan(M, N, K, cached_cus(), plan);
+  const bool wide = layout & MXFP8_GEMM_WIDE;
+  const int64_t need = wide ? make_plan<2>(M, N, K, cached_cus(), plan) : make_plan<1>(M, N, K, cached_cus(), plan);
   if (need > workspace_bytes) {  // no (or too small a) workspace: run every tile whole
     plan.full = plan.tm * plan.tn;
     plan.per_full = (plan.full + 7) / 8;
@@ -441,24 +485,15 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
   }
   plan.cnt = plan.nsplit ? (int*)workspace : nullptr;
   plan.ws = plan.nsplit ? (float4*)((char*)workspace + kCounterBytes) : nullptr;
-  dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
   Lora lo{(const uint16_t*)lora_p, ld_p, (const uint16_t*)lora_q, ld_q, alpha};
-  hipStream_t stm = (hipStream_t)stream;
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
-  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
-  uint16_t* Cp = (uint16_t*)c;
-  if (!lora_p)
-    gemm_kernel<0><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
-                                                (int)layout);
-  else if (r == 16)
-    gemm_kernel<16><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
-                                                (int)layout);
-  else if (r == 32)
-    gemm_kernel<32><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
-                                                (int)layout);
+  const int tiled = (int)(layout & 3);
+  if (wide)
+    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo, (int)r, plan, tiled,
+              (hipStream_t)stream);
   else
-    gemm_kernel<64><<<grid, kThreads, 0, stm>>>(A, SA, lda, B, SB, ldb, Mi, Ni, Ki, Cp, ldc, lo, plan,
-                                                (int)layout);
+    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo, (int)r, plan, tiled,
+              (hipStream_t)stream);
   MX_CHECK_LAUNCH("mxfp8_gemm_nt");
   return MXFP8_OK;
 }

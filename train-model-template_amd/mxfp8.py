@@ -117,7 +117,7 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     wq may be a row slice/stride view (row stride wq.stride(0)); optional rank-r epilogue
     out = bf16(out + alpha · P · Qᵀ) with lora = (P [M, r], Q [N, r]) (the addmm_ after the GEMM).
     layout bit 0 / 1: q / wq hold MX-tiled codes (mx_quant_tiled, tile_codes); then M = m (q has the rows
-    padded to 16)."""
+    padded to 16).  Bit 2: 8-wave 256 x 256 workgroups (see _native.gemm_nt)."""
     M, K = q.shape
     if m is not None:
         M = m
