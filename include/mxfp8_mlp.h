@@ -32,6 +32,7 @@ extern "C" {
 #define MXFP8_GEMM_A_TILED 1
 #define MXFP8_GEMM_B_TILED 2
 #define MXFP8_GEMM_WIDE 4
+#define MXFP8_GEMM_C_FT 8
 
 /* Returns MXFP8_MLP_ABI_VERSION of the built library (the Python loader refuses a mismatch). */
 int mxfp8_abi_version(void);
@@ -99,7 +100,12 @@ int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
  * lda ignored), MXFP8_GEMM_B_TILED = the same for B (results are bit-identical to row-major operands; the
  * tiled layout lets every DMA of the GEMM move a contiguous 1 KB instead of sixteen 64-byte row pieces);
  * MXFP8_GEMM_WIDE = 8-wave 256 x 256 workgroups, one per CU, instead of the default 4-wave 256 x 128, two per
- * CU (same result bits when no tile is split).
+ * CU (same result bits when no tile is split); MXFP8_GEMM_C_FT = C in the fused-tile (FT) layout instead of
+ * row-major (ldc ignored; c holds ceil(M/32)*32 rows, rows past M not written).
+ * FT layout of a bf16 [R, C] matrix (C % 32 == 0): 32 x 32 blocks of 2 KB, block (r/32, c/32) at
+ * ((r/32) * (C/32) + c/32) * 1024 elements; element (r, c) inside it at ((c/8) % 2) * 512 +
+ * (r%32 + 32 * ((c/16) % 2)) * 8 + c % 8.  It is the order in which the fused kernels' waves read a 32 x 32 tile
+ * (two contiguous 1 KB pieces); no reference counterpart (the reference keeps gu and dhm row-major).
  * workspace (optional, 256-byte aligned, workspace_bytes long; used with MXFP8_GEMM_WIDE only): when it holds
  * at least mxfp8_gemm_workspace_size(M, N, K) bytes, the tiles of a last wave that would leave more than half
  * of the CUs idle are split along K; their fp32 pieces go through the workspace and are added in a fixed order
@@ -127,7 +133,8 @@ int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K);
  *   q_h [T, N] + s_h (blocked, N/128 tiles per row, padded rows 0)   = MX(h)       (skipped if q_h == NULL)
  *   part [n_groups, T, r] fp32: xS_down partial sums h·adᵀ over the columns of each of n_groups groups
  *   h_out [T, N] bf16 (optional, may be NULL; needs q_h): h itself, for checks
- *   q_layout: 0 = q_h row-major, 1 = MX-tiled (see mxfp8_quant_tiled; ceil(T/16)*16 rows)
+ *   q_layout bit 0: q_h MX-tiled (see mxfp8_quant_tiled; ceil(T/16)*16 rows) instead of row-major;
+ *   q_layout bit 1: gu in the FT layout (see mxfp8_gemm_nt) instead of row-major
  * Requires N % 128 == 0, (N / 32) % n_groups == 0, r in {16, 32}, T * 2N < 2^31.
  */
 /*
@@ -151,7 +158,8 @@ int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu
  *   dbg_part, dbu_part [ceil(Tpad/SB), N, r] fp32 and dad_part [ceil(Tpad/SB), r, N]: per super-block sums of
  *     dgᵀ·xs_g, duᵀ·xs_u and (hᵀ·dxd)ᵀ (unscaled)
  *   dgu_out [T, 2N] bf16 (optional, may be NULL): dg | du themselves, for checks
- *   q_layout: 0 = q row-major, 1 = MX-tiled with 2N codes per row (see mxfp8_quant_tiled)
+ *   q_layout bit 0: q MX-tiled with 2N codes per row (see mxfp8_quant_tiled) instead of row-major;
+ *   q_layout bit 1: gu and dhm in the FT layout (see mxfp8_gemm_nt) instead of row-major
  */
 int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, const void* dhm, const void* dxd,
                   const void* dxdT, const void* bg, const void* bu, const void* bgT, const void* buT, const void* ad,

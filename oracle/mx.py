@@ -180,3 +180,27 @@ def from_tiled(t, R, K):
         for c in range(4):
             out[:, r, :, c, :] = a[:, r, :, c ^ sw, :]
     return out.reshape(Rp, K)[:R]
+
+
+def to_ft(x):
+    """Row-major bf16 [R, C] (as uint16, or any element array; C % 32 == 0) -> the fused-tile (FT) layout as a
+    flat array of ceil(R/32)*32*C elements (padding rows zero): 32 x 32 blocks, block (r//32, c//32) at
+    ((r//32)*(C//32) + c//32)*1024; inside it the 16 columns 16*lg + i of row r%32 belong to lane r%32 + 32*lg,
+    and the block holds every lane's i = 0..7 (8 elements per lane, lane order), then every lane's i = 8..15.
+    Written as a reshape/permute of the padded array.  No reference counterpart: the order in which this
+    build's fused kernels read gu and dhm (include/mxfp8_mlp.h, MXFP8_GEMM_C_FT)."""
+    x = np.asarray(x)
+    R, C = x.shape
+    Rp = -(-R // 32) * 32
+    a = np.zeros((Rp, C), x.dtype)
+    a[:R] = x
+    # [rb, r32, cb, lg, half, e8] -> [rb, cb, half, lg, r32, e8]
+    a = a.reshape(Rp // 32, 32, C // 32, 2, 2, 8).transpose(0, 2, 4, 3, 1, 5)
+    return np.ascontiguousarray(a).reshape(-1)
+
+
+def from_ft(t, R, C):
+    """Inverse of to_ft: the first R rows of the row-major [R, C] matrix."""
+    Rp = -(-R // 32) * 32
+    a = np.asarray(t).reshape(Rp // 32, C // 32, 2, 2, 32, 8).transpose(0, 4, 1, 3, 2, 5)
+    return np.ascontiguousarray(a).reshape(Rp, C)[:R]

@@ -60,7 +60,7 @@ def test_argument_checks_reject_before_launch(lib):
     # GEMM epilogue rank not supported
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, p, 8, p, 8, 8, 1.0, 0, None, 0, None) == -1
     # unknown operand layout
-    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 8, None, 0, None) == -1
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 16, None, 0, None) == -1
     assert b"layout" in lib.mxfp8_last_error()
     # workspace given but misaligned
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 0,

@@ -166,3 +166,25 @@ def test_gemm_tiled_operands_bit_identical(M, N, K, gpu):
     Q = torch.randn(N, 16, generator=g).to(torch.bfloat16).to(gpu)
     assert torch.equal(mxfp8.mx_mm(ta, sa, tb, sb, lora=(P, Q), alpha=2.0, layout=3, m=M),
                        mxfp8.mx_mm(qa, sa, qb, sb, lora=(P, Q), alpha=2.0))
+
+
+@pytest.mark.parametrize("M,N,K,r", [(300, 384, 512, 0), (1000, 1024, 3584, 16), (64, 12288, 2048, 0)])
+def test_gemm_ft_output(M, N, K, r, gpu):
+    # C in the fused-tile layout holds exactly the row-major result, rearranged (oracle.mx.to_ft)
+    import numpy as np
+    qa, sa, qb, sb = _operands(M, N, K, 5 * M + N, gpu)
+    lora = None
+    if r:
+        g = torch.Generator().manual_seed(N)
+        lora = (torch.randn(M, r, generator=g).to(torch.bfloat16).to(gpu),
+                torch.randn(N, r, generator=g).to(torch.bfloat16).to(gpu))
+    ref = mxfp8.mx_mm(qa, sa, qb, sb, lora=lora, alpha=2.0)
+    ta, tb = mxfp8.tile_codes(qa), mxfp8.tile_codes(qb)
+    for layout, a, b in ((8, qa, qb), (11, ta, tb)):
+        c = mxfp8.mx_mm(a, sa, b, sb, lora=lora, alpha=2.0, layout=layout, m=M)
+        assert c.shape == (mxfp8.ft_rows(M), N)
+        want = mx.to_ft(ref.view(torch.uint16).cpu().numpy())
+        got = c.view(torch.uint16).cpu().numpy().reshape(-1)
+        # compare the elements of rows < M (the padding rows are not written)
+        live = mx.from_ft(np.arange(want.size), mxfp8.ft_rows(M), N)[:M].reshape(-1)
+        assert np.array_equal(got[live], want[live]), layout

@@ -122,6 +122,12 @@ def test_fwd_kernel_elementwise_and_codes(cfg, T, gpu):
     qt, st, xsd_t = fused_mlp.mlp_fwd(g(f["gu"]), g(f["xs"]), g(bg), g(bu), g(ad), s, s, True, tiled=True)
     assert torch.equal(st, sh) and torch.equal(xsd_t, xsd)
     assert np.array_equal(mx.from_tiled(qt.view(torch.uint8).cpu().numpy().reshape(-1), T, N), qr.numpy())
+    # gu in the fused-tile layout (what the fused path's GEMM writes): bit-identical results
+    gu_ft = torch.from_numpy(mx.to_ft(f["gu"].view(torch.uint16).numpy()).view(np.int16)).view(torch.bfloat16)
+    qf, sf, xsd_f = fused_mlp.mlp_fwd(g(gu_ft.view(-1, 2 * N)), g(f["xs"]), g(bg), g(bu), g(ad), s, s, True,
+                                      tiled=True, gu_ft=True)
+    live = lambda qq, C: mx.from_tiled(qq.view(torch.uint8).cpu().numpy().reshape(-1), T, C)  # noqa: E731
+    assert np.array_equal(live(qf, N), live(qt, N)) and torch.equal(sf, st) and torch.equal(xsd_f, xsd)
 
 
 @pytest.mark.parametrize("cfg,T", [(2, 512), (3, 300), (5, 1024)])
@@ -141,6 +147,18 @@ def test_bwd_kernel_elementwise_and_codes(cfg, T, gpu):
                                 tiled=True)[:2]
     assert torch.equal(sct, sc)
     assert np.array_equal(mx.from_tiled(qt.view(torch.uint8).cpu().numpy().reshape(-1), T, 2 * N), qr.numpy())
+    # gu and dhm in the fused-tile layout: bit-identical results
+    ft = lambda t: torch.from_numpy(mx.to_ft(t.view(torch.uint16).numpy()).view(np.int16)).view(  # noqa: E731
+        torch.bfloat16).view(-1, t.shape[1])
+    outs_rm = fused_mlp.mlp_bwd(g(f["gu"]), g(f["xs"]), g(b["dhm"]), g(b["dxd"]), g(bg), g(bu), g(ad), s, s, True,
+                                tiled=True)
+    outs_ft = fused_mlp.mlp_bwd(g(ft(f["gu"])), g(f["xs"]), g(ft(b["dhm"])), g(b["dxd"]), g(bg), g(bu), g(ad), s, s,
+                                True, tiled=True, gu_ft=True)
+    # (the tiled code buffer's padding rows past T are never written: compare its live rows)
+    assert np.array_equal(mx.from_tiled(outs_rm[0].view(torch.uint8).cpu().numpy().reshape(-1), T, 2 * N),
+                          mx.from_tiled(outs_ft[0].view(torch.uint8).cpu().numpy().reshape(-1), T, 2 * N))
+    for a_, b_ in zip(outs_rm[1:], outs_ft[1:]):
+        assert torch.equal(a_, b_)
     # partial-sum products from the GPU's own dg / du and the oracle's h, in float64
     dg64, du64 = dgu[:, :N].cpu().double(), dgu[:, N:].cpu().double()
     h64 = b["h"].double()

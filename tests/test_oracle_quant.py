@@ -259,3 +259,26 @@ def test_tiled_layout_is_the_gemm_lds_image():
                 assert np.array_equal(blk[16 * i:16 * i + 16], qp[row, kb * 64 + 16 * c:kb * 64 + 16 * c + 16])
     assert np.array_equal(mx.from_tiled(t, R, K), q)
     assert not t.reshape(Rp // 16, K // 64, 16, 64)[-1, :, R - 32:].any()  # rows 45..47 are zero padding
+
+
+def test_ft_layout_matches_lane_order():
+    # the fused-tile layout (gu, dhm between the GEMM and the fused kernels), built element by element from its
+    # definition: in block (rb, cb), lane l = r%32 + 32*lg holds columns 16*lg + 0..15 of row r; the block
+    # stores all lanes' first 8 columns (8 per lane, lane order), then all lanes' last 8
+    R, C = 45, 96
+    x = np.arange(R * C, dtype=np.int64).reshape(R, C) + 1
+    t = mx.to_ft(x)
+    Rp = 64
+    want = np.zeros(Rp * C, np.int64)
+    pos = 0
+    for rb in range(Rp // 32):
+        for cb in range(C // 32):
+            for half in range(2):
+                for lane in range(64):
+                    r, lg = rb * 32 + lane % 32, lane // 32
+                    for e in range(8):
+                        c = cb * 32 + lg * 16 + half * 8 + e
+                        want[pos] = x[r, c] if r < R else 0
+                        pos += 1
+    assert pos == Rp * C and np.array_equal(t, want)
+    assert np.array_equal(mx.from_ft(t, R, C), x)

@@ -12,7 +12,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
 ABI_VERSION = 3
-GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE = 1, 2, 4  # mxfp8_gemm_nt layout bits
+GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT = 1, 2, 4, 8  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
 

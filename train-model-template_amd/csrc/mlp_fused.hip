@@ -172,14 +172,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPe
     const uint16_t* __restrict__ gu, const uint16_t* __restrict__ xs, const uint16_t* __restrict__ bg,
     const uint16_t* __restrict__ bu, const uint16_t* __restrict__ ad, int T, int Tpad, int N, int tiles_per_group,
     float s_g, float s_u, uint8_t* __restrict__ q, uint8_t* __restrict__ s, float* __restrict__ part,
-    uint16_t* __restrict__ h_out, bool q_tiled) {
+    uint16_t* __restrict__ h_out, bool q_tiled, bool gu_ft) {
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int rb = blockIdx.x * 4 + w;
   if (rb * 32 >= Tpad) return;  // wave-uniform
   const int m = rb * 32 + (lane & 31);
   const bool live = m < T;
   const int mc = live ? m : T - 1;
-  const uint16_t* grow = gu + (int64_t)mc * 2 * N + lg * 16;  // this lane's 16 columns of a tile: grow + jb
   v8bf xg[R / 16], xu[R / 16];
 #pragma unroll
   for (int h = 0; h < R / 16; ++h) {
@@ -199,8 +198,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPe
   };
   auto fetch = [&](int t, TileIn& in) {
     const int jb = t * 32;
-    load16(grow + jb, in.g);
-    load16(grow + N + jb, in.u);
+    load16_rc(gu, mc, jb + lg * 16, 2 * N, gu_ft, in.g);  // this lane's 16 columns of the tile
+    load16_rc(gu, mc, N + jb + lg * 16, 2 * N, gu_ft, in.u);
     const int64_t wr = (int64_t)(jb + pi_col(lane & 31)) * R + lg * 8;
 #pragma unroll
     for (int h = 0; h < R / 16; ++h) {
@@ -297,7 +296,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     const uint16_t* __restrict__ buT, const uint16_t* __restrict__ ad, const uint16_t* __restrict__ adT, int T,
     int Tpad, int N, int SB, int CG, float s_g, float s_u, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
     float* __restrict__ dxa_part, float* __restrict__ dbg_part, float* __restrict__ dbu_part,
-    float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out, bool q_tiled) {
+    float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out, bool q_tiled, bool gu_ft) {
   __shared__ float red[4][32][3 * R + 1];                              // per-wave dxa | dxa_u | xS products
   __shared__ __attribute__((aligned(16))) uint16_t trt[4][3][32 * kTrLd];  // per-wave dg, du, h rows
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
@@ -338,10 +337,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       for (int h = 0; h < R / 16; ++h) dbg[jh][h] = dbu[jh][h] = dad[jh][h] = v4f{};
     auto fetch = [&](int rb, RowIn& in) {
       const int mc = min(rb + (lane & 31), T - 1);
-      const uint16_t* row = gu + (int64_t)mc * 2 * N + jb + lg * 16;
-      load16(row, in.g);
-      load16(row + N, in.u);
-      load16(dhm + (int64_t)mc * N + jb + lg * 16, in.d);
+      load16_rc(gu, mc, jb + lg * 16, 2 * N, gu_ft, in.g);
+      load16_rc(gu, mc, N + jb + lg * 16, 2 * N, gu_ft, in.u);
+      load16_rc(dhm, mc, jb + lg * 16, N, gu_ft, in.d);
     };
     auto block = [&](int rb, const RowIn& cur, RowIn& nxt) {
       const int m = rb + (lane & 31);
@@ -551,7 +549,8 @@ extern "C" int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, con
                              int64_t N, int64_t r, float s_g, float s_u, void* q_h, void* s_h, float* part,
                              int64_t n_groups, void* h_out, int64_t q_layout, void* stream) {
   MX_CHECK_ARG(gu && xs && bg && bu && ad && part, "mxfp8_mlp_fwd: null pointer");
-  MX_CHECK_ARG(q_layout == 0 || q_layout == 1, "mxfp8_mlp_fwd: q_layout must be 0 (row-major) or 1 (MX-tiled)");
+  MX_CHECK_ARG(q_layout >= 0 && q_layout <= 3,
+               "mxfp8_mlp_fwd: q_layout must be 0..3 (bit 0: q_h MX-tiled, bit 1: gu in the FT layout)");
   MX_CHECK_ARG((q_h == nullptr) == (s_h == nullptr), "mxfp8_mlp_fwd: q_h and s_h go together");
   MX_CHECK_ARG(!h_out || q_h, "mxfp8_mlp_fwd: h_out needs q_h");
   MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && (r == 16 || r == 32), "mxfp8_mlp_fwd: bad shape");
@@ -567,7 +566,7 @@ extern "C" int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, con
   hipStream_t stm = (hipStream_t)stream;
 #define FWD_ARGS (const uint16_t*)gu, (const uint16_t*)xs, (const uint16_t*)bg, (const uint16_t*)bu, (const uint16_t*)ad, \
                  (int)T, (int)Tpad, (int)N, tpg, s_g, s_u, (uint8_t*)q_h, (uint8_t*)s_h, part, (uint16_t*)h_out, \
-                 q_layout == 1
+                 (q_layout & 1) != 0, (q_layout & 2) != 0
   if (r == 16) {
     if (h_out) fwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(FWD_ARGS);
     else if (q_h) fwd_kernel<16, true, false><<<grid, 256, 0, stm>>>(FWD_ARGS);
@@ -587,7 +586,8 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                              const void* ad, const void* adT, int64_t T, int64_t N, int64_t r, float s_g, float s_u,
                              int64_t SB, int64_t CG, void* q, void* s, float* dxa_part, float* dbg_part,
                              float* dbu_part, float* dad_part, void* dgu_out, int64_t q_layout, void* stream) {
-  MX_CHECK_ARG(q_layout == 0 || q_layout == 1, "mxfp8_mlp_bwd: q_layout must be 0 (row-major) or 1 (MX-tiled)");
+  MX_CHECK_ARG(q_layout >= 0 && q_layout <= 3,
+               "mxfp8_mlp_bwd: q_layout must be 0..3 (bit 0: q MX-tiled, bit 1: gu and dhm in the FT layout)");
   MX_CHECK_ARG(gu && xs && xsT && dhm && dxd && dxdT && bg && bu && bgT && buT && ad && adT && dxa_part &&
                    dbg_part && dbu_part && dad_part,
                "mxfp8_mlp_bwd: null pointer");
@@ -608,7 +608,7 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                  (const uint16_t*)dxdT, (const uint16_t*)bg, (const uint16_t*)bu, (const uint16_t*)bgT,                    \
                  (const uint16_t*)buT, (const uint16_t*)ad, (const uint16_t*)adT, (int)T, (int)Tpad, (int)N, (int)SB,     \
                  (int)CG, s_g, s_u, (uint8_t*)q, (uint8_t*)s, dxa_part, dbg_part, dbu_part, dad_part, (uint16_t*)dgu_out, \
-                 q_layout == 1
+                 (q_layout & 1) != 0, (q_layout & 2) != 0
   MX_CHECK_ARG(!dgu_out || q, "mxfp8_mlp_bwd: dgu_out needs q");
   if (r == 16) {
     if (dgu_out) bwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(BWD_ARGS);

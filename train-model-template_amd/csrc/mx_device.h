@@ -90,6 +90,18 @@ __device__ __forceinline__ int64_t tiled_offset(int64_t r, int64_t k, int64_t K)
          (k & 15);
 }
 
+// Element offset of (row r, column c) in the fused-tile (FT) layout of a bf16 [R, C] matrix (C % 32 == 0, rows
+// padded to a multiple of 32): 32 x 32 blocks of 2 KB, block (r/32, c/32) at ((r/32) * (C/32) + c/32) * 1024
+// elements.  Inside a block, columns c%32 = 16 lg + i of row r%32 belong to lane l = r%32 + 32 lg of the fused
+// kernels' tile order (a lane's 16 contiguous columns); the block holds first every lane's columns i = 0..7
+// (16 bytes per lane, in lane order), then every lane's i = 8..15.  So a wave's two 16-byte loads of a tile
+// read two contiguous 1 KB pieces (8 full cache lines each, against 32 half-used lines for a row-major
+// matrix), and 4 consecutive columns (c % 4 == 0) are 8 contiguous bytes, the GEMM epilogue's store unit.
+__device__ __forceinline__ int64_t ft_offset(int64_t r, int64_t c, int64_t C) {
+  return ((r >> 5) * (C >> 5) + (c >> 5)) * 1024 + ((c >> 3) & 1) * 512 + ((r & 31) + 32 * ((c >> 4) & 1)) * 8 +
+         (c & 7);
+}
+
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -141,6 +153,15 @@ __device__ __forceinline__ v8bf load_bf8(const uint16_t* p) { return as_bf8(*rei
 // 16 contiguous bf16 at p (32 bytes) as 8 packed words
 __device__ __forceinline__ void load16(const uint16_t* p, uint32_t* w) {
   const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+// 16 bf16 of row r, columns c0..c0+15 (c0 % 16 == 0) of a [*, C] matrix, row-major (row stride C) or FT
+__device__ __forceinline__ void load16_rc(const uint16_t* base, int64_t r, int64_t c0, int64_t C, bool ft,
+                                          uint32_t* w) {
+  const uint16_t* p = base + (ft ? ft_offset(r, c0, C) : r * C + c0);
+  const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + (ft ? 512 : 8));
   w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
   w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
 }

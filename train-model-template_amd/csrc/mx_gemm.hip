@@ -177,7 +177,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   // lane's 16 bytes land at their swizzled LDS position.  MX-tiled operand (tiled_offset in mx_device.h): the
   // slice is one contiguous 1 KB block already in LDS order, lane i copies bytes 16i..16i+15, and a K step
   // advances 1 KB instead of 64 B.
-  const bool a_tiled = tiled & 1, b_tiled = (tiled >> 1) & 1;
+  const bool a_tiled = tiled & 1, b_tiled = (tiled >> 1) & 1, c_ft = (tiled >> 3) & 1;
   const int kst = K / kBK;
   const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3 for these rows
   auto slice_off = [&](bool op_tiled, int R0, int Rn, int64_t ldd, int rbase) -> uint32_t {
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
           const int n = nb + g * 8 + (lane >> 5) * 4;
           if (n < N) {
             uint2 w = make_uint2(pack_bf16x2(o[4 * g], o[4 * g + 1]), pack_bf16x2(o[4 * g + 2], o[4 * g + 3]));
-            *reinterpret_cast<uint2*>(C + (int64_t)m * ldc + n) = w;
+            *reinterpret_cast<uint2*>(C + (c_ft ? ft_offset(m, n, N) : (int64_t)m * ldc + n)) = w;
           }
         }
       }
@@ -454,10 +454,12 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
                "mxfp8_gemm_nt: need K %% 128 == 0 and N %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                (long long)N, (long long)K);
   MX_CHECK_ARG(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "mxfp8_gemm_nt: dimension too large");
-  MX_CHECK_ARG(layout >= 0 && layout <= 7,
-               "mxfp8_gemm_nt: layout must be 0..7 (bit 0: A MX-tiled, bit 1: B MX-tiled, bit 2: 8-wave shape)");
-  if (layout & 1) lda = K;  // the tiled layout has no row stride
+  MX_CHECK_ARG(layout >= 0 && layout <= 15,
+               "mxfp8_gemm_nt: layout must be 0..15 (bit 0: A MX-tiled, bit 1: B MX-tiled, bit 2: 8-wave shape, "
+               "bit 3: C in the FT layout)");
+  if (layout & 1) lda = K;  // the tiled layouts have no row stride
   if (layout & 2) ldb = K;
+  if (layout & MXFP8_GEMM_C_FT) ldc = N;
   MX_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0 && ldc >= N && ldc % 4 == 0,
                "mxfp8_gemm_nt: bad strides");
   MX_CHECK_ARG(256LL * lda < (1LL << 32) && 256LL * ldb < (1LL << 32), "mxfp8_gemm_nt: stride too large");
@@ -487,7 +489,7 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
   plan.ws = plan.nsplit ? (float4*)((char*)workspace + kCounterBytes) : nullptr;
   Lora lo{(const uint16_t*)lora_p, ld_p, (const uint16_t*)lora_q, ld_q, alpha};
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
-  const int tiled = (int)(layout & 3);
+  const int tiled = (int)(layout & ~MXFP8_GEMM_WIDE);
   if (wide)
     launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo, (int)r, plan, tiled,
               (hipStream_t)stream);

@@ -73,11 +73,12 @@ def _bwd_grid(T, N, R):
     return best[1], best[2]
 
 
-def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False):
+def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False, gu_ft=False):
     """gu [T, 2N] bf16, xs [T, 2R] bf16 (xa_gate | xa_up), bg/bu [N, R], ad [R, N] bf16 -> (q_h, s_h, xS_down
     bf16) (fused_mlp.py:198-215).  h_out (optional [T, N] bf16) receives h for checks; tiled=True writes q_h
-    in the MX-tiled GEMM operand layout ([ceil(T/16)*16, N] bytes, see mxfp8.mx_quant_tiled)."""
-    T, N2 = gu.shape
+    in the MX-tiled GEMM operand layout ([ceil(T/16)*16, N] bytes, see mxfp8.mx_quant_tiled); gu_ft=True reads
+    gu in the fused-tile layout ([ceil(T/32)*32, 2N], T taken from xs)."""
+    T, N2 = xs.shape[0], gu.shape[1]
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
     ng = _fwd_groups(T, N, R)
@@ -88,15 +89,18 @@ def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False):
         q = s = None
     part = torch.empty((ng, T, R), dtype=torch.float32, device=dev)
     LAST["fwd"] = dict(n_groups=ng)
-    _native.mlp_fwd(gu, xs, bg, bu, ad, T, N, R, s_g, s_u, q, s, part, ng, h_out, q_layout=int(tiled))
+    _native.mlp_fwd(gu, xs, bg, bu, ad, T, N, R, s_g, s_u, q, s, part, ng, h_out,
+                    q_layout=int(tiled) | (2 if gu_ft else 0))
     xsd = torch.empty((T, R), dtype=torch.bfloat16, device=dev)
     _native.sum_parts(part, ng, T * R, xsd)
     return (q, s.view(_E8), xsd) if write_q else (None, None, xsd)
 
 
-def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u, need_q, dgu_out, tiled):
-    """Run the backward kernel; -> (q, s, (dxa_p, dbg_p, dbu_p, dad_p)) with the partial sums unreduced."""
-    T, N2 = gu.shape
+def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u, need_q, dgu_out, tiled,
+                gu_ft=False):
+    """Run the backward kernel; -> (q, s, (dxa_p, dbg_p, dbu_p, dad_p)) with the partial sums unreduced.
+    gu_ft: gu and dhm in the fused-tile layout (T taken from xs)."""
+    T, N2 = xs.shape[0], gu.shape[1]
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
     tpad = _cdiv(T, 128) * 128
@@ -113,7 +117,7 @@ def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u
     dbu_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
     dad_p = torch.empty((nsb, R, N), dtype=torch.float32, device=dev)
     _native.mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, R, s_g, s_u, SB, CG, q, s,
-                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out, q_layout=int(tiled))
+                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out, q_layout=int(tiled) | (2 if gu_ft else 0))
     return q, (s.view(_E8) if need_q else None), (dxa_p, dbg_p, dbu_p, dad_p)
 
 
@@ -123,11 +127,12 @@ def _transposed_padded(t, tpad):
     return out
 
 
-def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=False):
+def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=False, gu_ft=False):
     """-> (q_dgu [T, 2N] fp8, s_dgu, [dxa_gate | dxa_up | xS_down] [T, 3R] fp32 (dxa not yet scaled by s),
     dBg, dBu [N, R] fp32 (not scaled), dAd [R, N] fp32) (fused_mlp.py:235-259).  tiled=True writes q_dgu in
-    the MX-tiled GEMM operand layout ([ceil(T/16)*16, 2N] bytes)."""
-    T, N2 = gu.shape
+    the MX-tiled GEMM operand layout ([ceil(T/16)*16, 2N] bytes); gu_ft=True reads gu and dhm in the
+    fused-tile layout (T taken from xs)."""
+    T, N2 = xs.shape[0], gu.shape[1]
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
     tpad = _cdiv(T, 128) * 128
@@ -135,7 +140,7 @@ def mlp_bwd(gu, xs, dhm, dxd, bg, bu, ad, s_g, s_u, need_q, dgu_out=None, tiled=
     xsT, dxdT = _transposed_padded(xs, tpad), _transposed_padded(dxd, tpad)
     bgT, buT, adT = bg.t().contiguous(), bu.t().contiguous(), ad.t().contiguous()
     q, s, (dxa_p, dbg_p, dbu_p, dad_p) = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g,
-                                                     s_u, need_q, dgu_out, tiled)
+                                                     s_u, need_q, dgu_out, tiled, gu_ft)
     dxa = torch.empty((T, 3 * R), dtype=torch.float32, device=dev)
     dbg = torch.empty((N, R), dtype=torch.float32, device=dev)
     dbu = torch.empty((N, R), dtype=torch.float32, device=dev)
@@ -163,6 +168,10 @@ def _prep(Ag, Bg, Au, Bu, Ad, Bd, dt):
     return _cast((("lora_prep", id(Ag), id(Au), id(Bg), id(Bu), id(Ad), id(Bd)), dt), make)
 
 
+# GEMM layout of the MLP's own products: both operands MX-tiled, output in the fused-tile layout
+_LAYOUT_FT = _native.GEMM_A_TILED | _native.GEMM_B_TILED | _native.GEMM_C_FT
+
+
 class _MLP(torch.autograd.Function):
     """fused_mlp.py:262-336."""
 
@@ -182,11 +191,12 @@ class _MLP(torch.autograd.Function):
         xsT = torch.empty((2 * R, _cdiv(T, 128) * 128), dtype=dt, device=x2.device)
         _native.lora_nt(x2, S, xs, outT=xsT)
         # GEMM operands in the MX-tiled layout (same codes and scales as mx_quant; the GEMM streams 1 KB blocks)
+        # gu = gate | up [T, 2N] in the fused-tile layout the fused kernels read (32 x 32 blocks of 2 KB)
         q, sc = mxfp8.mx_quant_tiled(x2)
-        gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=3, m=T)  # [T, 2N] gate | up
+        gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=_LAYOUT_FT, m=T)
         del q, sc
         if need_out:
-            qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True)
+            qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True, gu_ft=True)
             # y = bf16(bf16(MX(h)·W_downᵀ) + s_d · xS_down · B_dᵀ): the addmm_ of fused_mlp.py:284 in the epilogue
             y = mxfp8.mx_mm(qh, sh, down._mx_w_tl, down._mx_ws, lora=(xsd, bd), alpha=s_d, layout=3, m=T)
             del qh, sh, xsd
@@ -213,14 +223,14 @@ class _MLP(torch.autograd.Function):
         T, N = dy2.shape[0], hold.n
         lw, xsT = ctx.lw, ctx.xsT
         qd, sd = mxfp8.mx_quant_tiled(dy2)
-        dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=3, m=T)  # [T, N] = MX(dy) · W_down
+        dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)  # MX(dy) · W_down, FT
         del qd, sd
         # dxd = bf16(bf16(dy2 · bd) · s_d) [T, R], and its zero-padded transpose
         dxd = torch.empty((T, R), dtype=dt, device=dy2.device)
         dxdT = torch.empty((R, xsT.shape[1]), dtype=dt, device=dy2.device)
         _native.lora_nt(dy2, lw.bdT, dxd, scale=s_d, outT=dxdT)
         qg, sg, parts = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, lw.bgT, lw.buT, ad, lw.adT, s_g, s_u,
-                                    need_x, None, True)
+                                    need_x, None, True, gu_ft=True)
         del dhm
         # the partial sums, scaled and cast as fused_mlp.py:258, :319-326 do, in one kernel
         dxa = torch.empty((T, 2 * R), dtype=dt, device=dy2.device)  # bf16(s_g dxa_g | s_u dxa_u)

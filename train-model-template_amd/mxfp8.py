@@ -54,6 +54,11 @@ def tiled_rows(R):
     return _cdiv(R, 16) * 16
 
 
+def ft_rows(R):
+    """Rows held by a bf16 buffer of R rows in the fused-tile (FT) layout (32-row blocks)."""
+    return _cdiv(R, 32) * 32
+
+
 def mx_quant_tiled(x2d):
     """mx_quant with the codes in the MX-tiled operand layout of the GEMM (16-row x 64-code blocks of 1 KB, see
     include/mxfp8_mlp.h): same codes and scales in another byte order.  The code tensor is [ceil(R/16)*16, K]
@@ -117,7 +122,8 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     wq may be a row slice/stride view (row stride wq.stride(0)); optional rank-r epilogue
     out = bf16(out + alpha · P · Qᵀ) with lora = (P [M, r], Q [N, r]) (the addmm_ after the GEMM).
     layout bit 0 / 1: q / wq hold MX-tiled codes (mx_quant_tiled, tile_codes); then M = m (q has the rows
-    padded to 16).  Bit 2: 8-wave 256 x 256 workgroups (see _native.gemm_nt)."""
+    padded to 16).  Bit 2: 8-wave 256 x 256 workgroups (see _native.gemm_nt).  Bit 3: out in the fused-tile
+    layout (pass out with ft_rows(M) rows)."""
     M, K = q.shape
     if m is not None:
         M = m
@@ -125,7 +131,7 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     assert wq.shape[1] == K and q.stride(1) == 1 and wq.stride(1) == 1, (q.shape, wq.shape)
     assert not (layout & 1) or q.shape[0] == tiled_rows(M), (q.shape, M)
     if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=q.device)
+        out = torch.empty((ft_rows(M) if layout & 8 else M, N), dtype=torch.bfloat16, device=q.device)
     if M:
         ev = GEMM_EVENTS
         if ev is not None:
