@@ -154,7 +154,7 @@ int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu
  * bgT, buT [r, N], adT [N, r].  Grid: super-blocks of SB rows (SB % 128 == 0) x column groups of CG columns
  * (CG % 128 == 0, N % CG == 0).  Outputs:
  *   q [T, 2N] + s (2N/128 tiles per row): MX(dg) in columns 0..N-1, MX(du) in N..2N-1  (skipped if q == NULL)
- *   dxa_part [N/CG, T, 3r] fp32: dxa_g | dxa_u | xS_down partial sums over each column group (unscaled)
+ *   dxa_part [N/128, T, 3r] fp32: dxa_g | dxa_u | xS_down partial sums over each 128-column quad (unscaled)
  *   dbg_part, dbu_part [ceil(Tpad/SB), N, r] fp32 and dad_part [ceil(Tpad/SB), r, N]: per super-block sums of
  *     dgᵀ·xs_g, duᵀ·xs_u and (hᵀ·dxd)ᵀ (unscaled)
  *   dgu_out [T, 2N] bf16 (optional, may be NULL): dg | du themselves, for checks

@@ -223,7 +223,15 @@ __global__ __launch_bounds__(256) void tn_sum_kernel(const float* __restrict__ p
   const int64_t n = (int64_t)RP * K;
   if (i >= n) return;
   float v = part[i];
-  for (int c = 1; c < chunks; ++c) v += part[(int64_t)c * n + i];
+  int c = 1;
+  for (; c + 7 < chunks; c += 8) {  // eight loads in flight, added in chunk order
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = part[(int64_t)(c + u) * n + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += x[u];
+  }
+  for (; c < chunks; ++c) v += part[(int64_t)c * n + i];
   v = round_bf16(v);
   if (scale != 1.0f) v = round_bf16(v * scale);
   const int64_t rho = i / K, k = i % K;
@@ -241,33 +249,52 @@ struct FinishArgs {
   float *dbg, *dbu, *dad;     // [N, r], [N, r], [r, N] fp32
 };
 
-// One thread per output element of dxa | xsd, dB_g, dB_u, dA_d; partials added in order (fused_mlp.py:258,
-// :319-326).
-__global__ __launch_bounds__(256) void finish_kernel(FinishArgs a, int64_t total) {
+// Four consecutive output elements per thread (16-byte loads) of dxa | xsd, dB_g, dB_u, dA_d; the partials
+// are added in ascending order, four loads in flight at a time (fused_mlp.py:258, :319-326).
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 sum_ordered(const float4* __restrict__ p, int64_t stride, int n) {
+  float4 v = p[0];
+  int c = 1;
+  for (; c + 3 < n; c += 4) {
+    const float4 x0 = p[c * stride], x1 = p[(c + 1) * stride], x2 = p[(c + 2) * stride], x3 = p[(c + 3) * stride];
+    v = add4(add4(add4(add4(v, x0), x1), x2), x3);
+  }
+  for (; c < n; ++c) v = add4(v, p[c * stride]);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void finish_kernel(FinishArgs a, int64_t total4) {
   int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
+  if (i >= total4) return;
   const int64_t R = a.R;
-  int64_t n = (int64_t)a.T * 3 * R;
-  if (i < n) {
-    const int64_t cnt = n;
-    float v = a.dxa_part[i];
-    for (int c = 1; c < a.ncg; ++c) v += a.dxa_part[(int64_t)c * cnt + i];
-    const int64_t t = i / (3 * R), c = i % (3 * R);
-    if (c < 2 * R) a.dxa[t * 2 * R + c] = bf(v * (c < R ? a.s_g : a.s_u));
-    else a.xsd[t * R + c - 2 * R] = bf(v);
+  int64_t n4 = (int64_t)a.T * 3 * R / 4;
+  if (i < n4) {
+    const float4 v = sum_ordered(reinterpret_cast<const float4*>(a.dxa_part) + i, n4, a.ncg);
+    const int64_t t = (4 * i) / (3 * R), c = (4 * i) % (3 * R);  // 3R % 4 == 0: the four share row t
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    if (c < 2 * R) {
+      const float sc = c < R ? a.s_g : a.s_u;  // R % 4 == 0: the four share the scale
+      const uint2 w = make_uint2(pack_bf16x2(f[0] * sc, f[1] * sc), pack_bf16x2(f[2] * sc, f[3] * sc));
+      *reinterpret_cast<uint2*>(a.dxa + t * 2 * R + c) = w;
+    } else {
+      *reinterpret_cast<uint2*>(a.xsd + t * R + c - 2 * R) =
+          make_uint2(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]));
+    }
     return;
   }
-  i -= n;
-  n = (int64_t)a.N * R;
+  i -= n4;
+  n4 = (int64_t)a.N * R / 4;
   const float* src;
   float* dst;
   float sc;
-  if (i < n) { src = a.dbg_part; dst = a.dbg; sc = a.s_g; }
-  else if (i < 2 * n) { i -= n; src = a.dbu_part; dst = a.dbu; sc = a.s_u; }
-  else { i -= 2 * n; src = a.dad_part; dst = a.dad; sc = 1.0f; }
-  float v = src[i];
-  for (int c = 1; c < a.nsb; ++c) v += src[(int64_t)c * n + i];
-  dst[i] = sc == 1.0f ? v : v * sc;
+  if (i < n4) { src = a.dbg_part; dst = a.dbg; sc = a.s_g; }
+  else if (i < 2 * n4) { i -= n4; src = a.dbu_part; dst = a.dbu; sc = a.s_u; }
+  else { i -= 2 * n4; src = a.dad_part; dst = a.dad; sc = 1.0f; }
+  float4 v = sum_ordered(reinterpret_cast<const float4*>(src) + i, n4, a.nsb);
+  if (sc != 1.0f) v = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+  reinterpret_cast<float4*>(dst)[i] = v;
 }
 
 }  // namespace
@@ -349,10 +376,14 @@ extern "C" int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part
   MX_CHECK_ARG(dxa_part && dbg_part && dbu_part && dad_part && dxa && xsd && dbg && dbu && dad,
                "mxfp8_mlp_bwd_finish: null pointer");
   MX_CHECK_ARG(ncg > 0 && nsb > 0 && T > 0 && N > 0 && (r == 16 || r == 32), "mxfp8_mlp_bwd_finish: bad shape");
-  const int64_t total = T * 3 * r + 3 * N * r;
+  MX_CHECK_ARG(mx_aligned(dxa_part, 16) && mx_aligned(dbg_part, 16) && mx_aligned(dbu_part, 16) &&
+                   mx_aligned(dad_part, 16) && mx_aligned(dxa, 8) && mx_aligned(xsd, 8) && mx_aligned(dbg, 16) &&
+                   mx_aligned(dbu, 16) && mx_aligned(dad, 16),
+               "mxfp8_mlp_bwd_finish: misaligned buffer");
+  const int64_t total4 = (T * 3 * r + 3 * N * r) / 4;
   FinishArgs a{dxa_part, dbg_part, dbu_part, dad_part, (int)ncg, (int)nsb, (int)T, (int)N, (int)r, s_g, s_u,
                (uint16_t*)dxa, (uint16_t*)xsd, dbg, dbu, dad};
-  finish_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total);
+  finish_kernel<<<(unsigned)((total4 + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total4);
   MX_CHECK_LAUNCH("mxfp8_mlp_bwd_finish");
   return MXFP8_OK;
 }

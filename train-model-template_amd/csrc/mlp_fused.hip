@@ -461,16 +461,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
           dad[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, td[h], dad[jh][h], 0, 0, 0);
         }
       }
-      // sum the 4 waves' products (fixed order) into the column group's partial
+      // sum the 4 waves' products (fixed order) into the quad's own partial (stores only: a read-modify-write
+      // here would wait behind the next row block's prefetch, the memory counter completing in order)
       __syncthreads();
+      float* qpart = dxa_part + ((int64_t)(blockIdx.y * (CG / 128) + oc) * T + rb) * 3 * R;
       for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 256) {
         const int mm = idx / (3 * R), cc = idx % (3 * R);
-        const int row = rb + mm;
-        if (row < T) {
-          const float v = ((red[0][mm][cc] + red[1][mm][cc]) + red[2][mm][cc]) + red[3][mm][cc];
-          float* dst = dxa_part + ((int64_t)blockIdx.y * T + row) * 3 * R + cc;
-          *dst = oc == 0 ? v : *dst + v;
-        }
+        if (rb + mm < T) qpart[idx] = ((red[0][mm][cc] + red[1][mm][cc]) + red[2][mm][cc]) + red[3][mm][cc];
       }
       __syncthreads();
     };

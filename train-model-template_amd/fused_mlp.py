@@ -56,8 +56,8 @@ def _fwd_groups(T, N, R=16):
 def _bwd_grid(T, N, R):
     """(SB, CG) of the backward kernel (SB, CG multiples of 128; two 4-wave workgroups per CU).  Every
     workgroup of a round runs at the same pace, so the time goes as rounds x (SB/32 row blocks x CG/128 column
-    quads); pick the least of that, then the fewest partial-sum bytes (per super-block dB / dA_d partials plus
-    per column-group dxa partials, as in fused_mlp.py:218-232)."""
+    quads); pick the least of that, then the fewest partial-sum bytes (per super-block dB / dA_d partials; the
+    dxa partials are one per 128-column quad whatever the grid; the trade-off of fused_mlp.py:218-232)."""
     tpad = _cdiv(T, 128) * 128
     cap = 2 * _n_cu()
     best = None
@@ -66,7 +66,7 @@ def _bwd_grid(T, N, R):
         for sb in range(128, tpad + 128, 128):
             nsb = _cdiv(tpad, sb)
             work = _cdiv(nsb * ncg, cap) * (sb // 32) * (cg // 128)
-            partial = nsb * N * R * 3 * 4 + ncg * T * 3 * R * 4
+            partial = nsb * N * R * 3 * 4
             key = (work, partial)
             if best is None or key < best[0]:
                 best = (key, sb, cg)
@@ -112,7 +112,7 @@ def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u
         s = torch.empty(_cdiv(T, 128) * (N2 // 128) * 512, dtype=torch.uint8, device=dev)
     else:
         q = s = None
-    dxa_p = torch.empty((ncg, T, 3 * R), dtype=torch.float32, device=dev)
+    dxa_p = torch.empty((N // 128, T, 3 * R), dtype=torch.float32, device=dev)  # one partial per 128 columns
     dbg_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
     dbu_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
     dad_p = torch.empty((nsb, R, N), dtype=torch.float32, device=dev)
