@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 3
+#define MXFP8_MLP_ABI_VERSION 4
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -193,6 +193,17 @@ int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg, const flo
  */
 int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* w, int64_t rp, float scale, void* out,
                   void* outT, int64_t Tpad, void* stream);
+
+/*
+ * One pass over x [T, K] bf16 (row stride ld_x) giving both mxfp8_quant_tiled(x) (codes q in the MX-tiled
+ * layout, ceil(T/16)*16 rows; scales s blocked with K/128 tiles per row, padded rows 0) and
+ * mxfp8_lora_nt(x, w, rp, scale, out, outT, Tpad) (out [T, rp] bf16, outT [rp, Tpad] or NULL).  Replaces
+ * mx_quant(x2) followed by xs = x2 @ S.t() (/root/reference/scripts/fused_mlp.py:277-279), and mx_quant(dy2)
+ * with dxd = (dy2 @ bd).mul_(s_d) (:309-313), each reading the activation once.  K % 128 == 0, rp in {16, 32},
+ * Tpad = ceil(T/128)*128.
+ */
+int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w, int64_t rp,
+                     float scale, void* out, void* outT, int64_t Tpad, void* stream);
 
 /* Token chunks mxfp8_lora_tn uses for [T, K] (its partial buffer holds chunks * rp * K floats). */
 int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);

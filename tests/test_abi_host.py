@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 18, names
+    assert len(names) == 19, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -72,6 +72,11 @@ def test_argument_checks_reject_before_launch(lib):
     # LoRA products: K must be a multiple of 256 (x · Wᵀ) / 128 (token reduction), rp in {16, 32, 64}
     assert lib.mxfp8_lora_nt(p, 4, 200, 200, p, 16, 1.0, p, None, 0, None) == -1
     assert lib.mxfp8_lora_nt(p, 4, 256, 256, p, 8, 1.0, p, None, 0, None) == -1
+    # fused quantizer + rank-r product: K % 128, rp in {16, 32}, Tpad = ceil(T/128)*128
+    assert lib.mxfp8_quant_lora(p, 4, 200, 200, p, p, p, 16, 1.0, p, None, 128, None) == -1
+    assert lib.mxfp8_quant_lora(p, 4, 256, 256, p, p, p, 64, 1.0, p, None, 128, None) == -1
+    assert lib.mxfp8_quant_lora(p, 4, 256, 256, p, p, p, 16, 1.0, p, None, 256, None) == -1
+    assert b"Tpad" in lib.mxfp8_last_error()
     assert lib.mxfp8_lora_tn(p, 4, 96, 96, p, 16, 1, ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), 1.0, 0, 0, p,
                              None) == -1
     assert lib.mxfp8_lora_tn_chunks(10752, 2048) > 0 and lib.mxfp8_lora_tn_chunks(10752, 100) == 0

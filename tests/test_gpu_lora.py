@@ -113,3 +113,29 @@ def test_bwd_finish_matches_reference_reduction(gpu):
     assert torch.equal(dxa.cpu(), ref_dxa) and torch.equal(xsd.cpu(), sx[:, 2 * R:].to(torch.bfloat16))
     assert torch.equal(dbg.cpu(), ordered(dbg_p) * s_g) and torch.equal(dbu.cpu(), ordered(dbu_p) * s_u)
     assert torch.equal(dad.cpu(), ordered(dad_p))
+
+
+@pytest.mark.parametrize("T,K,rp,scale", [(300, 1024, 32, 1.0), (4096, 2048, 16, 2.0), (1, 128, 16, 1.0),
+                                          (8896, 2048, 32, 1.0)])
+def test_quant_lora_matches_quantizer_and_product(T, K, rp, scale, gpu):
+    # one read of x: codes and scales bit-identical to mxfp8_quant_tiled; out / outT as lora_nt's contract
+    import mxfp8
+    from oracle import mx
+    g = torch.Generator().manual_seed(T + K + rp)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(rp, K, generator=g) * 0.02).to(torch.bfloat16)
+    q, s, out, outT = mxfp8.mx_quant_lora(x.to(gpu), w.to(gpu), scale=scale)
+    qr, sr = mxfp8.mx_quant_tiled(x.to(gpu))
+    live = lambda qq: mx.from_tiled(qq.view(torch.uint8).cpu().numpy().reshape(-1), T, K)  # noqa: E731
+    import numpy as np
+    assert np.array_equal(live(q), live(qr))
+    assert torch.equal(s.view(torch.uint8), sr.view(torch.uint8))
+    exact = x.double() @ w.double().t()
+    absum = x.double().abs() @ w.double().abs().t()
+    if scale != 1.0:
+        exact = exact.float().to(torch.bfloat16).double() * scale
+        absum = absum * scale
+    _bf16_step_ok(out, exact, absum)
+    tpad = -(-T // 128) * 128
+    assert outT.shape == (rp, tpad) and torch.equal(outT[:, :T].t().cpu(), out.cpu())
+    assert int(torch.count_nonzero(outT[:, T:])) == 0

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT = 1, 2, 4, 8  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -36,6 +36,7 @@ SIGNATURES = {
     "mxfp8_sum_parts": [_ptr, _i64, _i64, _f32, _ptr, _int, _ptr],
     "mxfp8_lora_prep": [_ptr] * 6 + [_i64, _i64, _i64] + [_ptr] * 10 + [_ptr],
     "mxfp8_lora_nt": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
+    "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_lora_tn_chunks": [_i64, _i64],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
@@ -192,6 +193,13 @@ def lora_nt(x, w, out, scale=1.0, outT=None):
     T, K = x.shape
     call("mxfp8_lora_nt", _p(x), T, K, x.stride(0), _p(w), w.shape[0], float(scale), _p(out), _p(outT),
          outT.shape[1] if outT is not None else 0, like=x)
+
+
+def quant_lora(x, q, s, w, out, scale=1.0, outT=None):
+    """mxfp8.mx_quant_tiled(x) into (q, s) and lora_nt(x, w, out, scale, outT) from one read of x."""
+    T, K = x.shape
+    call("mxfp8_quant_lora", _p(x), T, K, x.stride(0), _p(q), _p(s), _p(w), w.shape[0], float(scale), _p(out),
+         _p(outT), -(-T // 128) * 128, like=x)
 
 
 def lora_tn(x, p, out, part, scale=1.0, transpose=False):

@@ -135,6 +135,102 @@ __global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X,
   }
 }
 
+// ------------------------------------------------------------- MX quantization fused with x · Wᵀ
+// One pass over X [T, K] bf16 giving both its MX operand (codes in the MX-tiled layout and blocked scales:
+// the bytes of mxfp8_quant_tiled) and out = bf16(X · Wᵀ) (then bf16(· scale) when scale != 1), W [RP, K]
+// bf16, RP in {16, 32}, with the zero-padded transposed copy outT.  Grid: Tpad / 32 row blocks (Tpad =
+// ceil(T/128)*128, so the padded rows of the last scale tiles get scale 0), 4 waves.  The workgroup streams K
+// in 128-column tiles through a 4-stage LDS ring (the X tile and the W tile, 32 rows x 256 B each) filled by
+// global_load_lds_dwordx4: lane i of a DMA takes row 4j + i/16 and the 16-byte chunk (i%16) ^ (row%16) of that
+// row's tile piece, so a DMA reads four whole 256-byte row pieces and the LDS reads below, 16 rows at a time at
+// one logical chunk, hit 16 distinct chunk positions.  Wave w takes columns 32w..32w+31 of each tile: lane l
+// reads 16 contiguous values of row l%32 (columns 32w + 16(l/32) + 0..15), which with lane l^32 form one
+// 32-block; it quantizes them (one 16-byte code store, the scale byte) and feeds them, as two k steps in a
+// permuted column order that the W operand follows, to the 32x32x16 MFMA.  The waves' partial products are
+// added in LDS in a fixed order.  Rows past T read row T - 1 (and store its codes again, the same bytes).
+template <int RP>
+__global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restrict__ X, int64_t ldx, int T, int K,
+                                                         const uint16_t* __restrict__ W, uint8_t* __restrict__ q,
+                                                         uint8_t* __restrict__ s, float scale,
+                                                         uint16_t* __restrict__ out, uint16_t* __restrict__ outT,
+                                                         int Tpad) {
+  constexpr int kStages = 4, kTileB = 32 * 256, kStageB = 2 * kTileB;
+  constexpr int kWDma = RP / 16;      // W DMAs per wave (RP rows x 256 B = RP / 4 KB per stage)
+  constexpr int kDma = 2 + kWDma;     // X DMAs: 8 KB per stage, two per wave
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
+  const int r0 = blockIdx.x * 32, nt = K / 128;
+  // DMA sources (element pointers at tile 0)
+  const int pc = lane & 15;
+  const uint16_t* xsrc[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int xr = 4 * (2 * w + jj) + (lane >> 4);
+    xsrc[jj] = X + (int64_t)min(r0 + xr, T - 1) * ldx + (pc ^ (xr & 15)) * 8;
+  }
+  const uint16_t* wsrc[kWDma];
+#pragma unroll
+  for (int jj = 0; jj < kWDma; ++jj) {
+    const int wr = 4 * (w * kWDma + jj) + (lane >> 4);  // < RP
+    wsrc[jj] = W + (int64_t)wr * K + (pc ^ (wr & 15)) * 8;
+  }
+  const uint32_t lds0 = lds_addr(lds);
+  auto issue = [&](int t, int slot) {  // tile t into ring slot `slot`
+    const uint32_t st = lds0 + slot * kStageB;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) dma16(xsrc[jj] + t * 128, st + (2 * w + jj) * 1024);
+#pragma unroll
+    for (int jj = 0; jj < kWDma; ++jj) dma16(wsrc[jj] + t * 128, st + kTileB + (w * kWDma + jj) * 1024);
+  };
+  const int row = lane & 31;
+  const int m = r0 + row;
+  const bool live = m < T;
+  const int mc = live ? m : T - 1;
+  const int cx = 4 * w + 2 * lg;  // the lane's first logical 16-byte chunk of a tile row
+  const int sx0 = ((cx ^ (row & 15)) << 4), sx1 = (((cx + 1) ^ (row & 15)) << 4);
+  v16f acc = v16f{};
+  // Stages past the end re-load the last tile into the slot just consumed (no later step reads it).  The wait
+  // leaves the DMA of the (kStages - 2) later tiles in flight (and, if stores count too, waits a little longer).
+#pragma unroll
+  for (int j = 0; j < kStages - 1; ++j) issue(min(j, nt - 1), j);
+  int slot = 0;
+  for (int t = 0; t < nt; ++t) {
+    wait_vmcnt<(kStages - 2) * kDma>();
+    __builtin_amdgcn_s_barrier();  // every wave's DMA of tile t landed; every wave is done with tile t - 1's slot
+    issue(min(t + kStages - 1, nt - 1), slot == 0 ? kStages - 1 : slot - 1);
+    const uint8_t* st = lds + slot * kStageB;
+    const uint4 a = *reinterpret_cast<const uint4*>(st + row * 256 + sx0);
+    const uint4 b = *reinterpret_cast<const uint4*>(st + row * 256 + sx1);
+    const uint4 wa = *reinterpret_cast<const uint4*>(st + kTileB + row * 256 + sx0);
+    const uint4 wb = *reinterpret_cast<const uint4*>(st + kTileB + row * 256 + sx1);
+    const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    quant16(v, lane, m, live, q, mc, K, true, (int64_t)t * 128 + 32 * w + 16 * lg, s, K / 128);
+    // D[ρ][t] += W[ρ, cols] · X[t, cols] over the lane pair's 32 columns (rows ρ >= RP of the W tile: zero)
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row < RP ? as_bf8(wa) : v8bf{}, as_bf8(a), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row < RP ? as_bf8(wb) : v8bf{}, as_bf8(b), acc, 0, 0, 0);
+    slot = slot + 1 == kStages ? 0 : slot + 1;
+  }
+  wait_vmcnt<0>();       // the tail's repeated DMAs have landed: the ring can be reused
+  __syncthreads();
+  float(*red)[32][RP + 1] = reinterpret_cast<float(*)[32][RP + 1]>(lds);  // [4 waves][32 rows t][RP]
+  // acc lane l: t = l % 32, ρ = (i/4)*8 + (l/32)*4 + i%4
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int rho = (i >> 2) * 8 + lg * 4 + (i & 3);
+    if (rho < RP) red[w][row][rho] = acc[i];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 32 * RP; idx += 256) {
+    const int tt = idx / RP, rho = idx % RP;
+    const int r = r0 + tt;
+    float v = ((red[0][tt][rho] + red[1][tt][rho]) + red[2][tt][rho]) + red[3][tt][rho];
+    v = round_bf16(v);
+    if (scale != 1.0f) v = round_bf16(v * scale);
+    if (r < T) out[(int64_t)r * RP + rho] = bf(v);
+    if (outT) outT[(int64_t)rho * Tpad + r] = r < T ? bf(v) : (uint16_t)0;
+  }
+}
+
 // ------------------------------------------------------------------------------------- Pᵀ · X (tn)
 // part[c, ρ, k] = Σ_{t in chunk c} P[t, ρ] X[t, k], P [T, RP] bf16, X [T, K] bf16 (row stride ldx).  Grid
 // (K / 128, chunks), 4 waves, wave w on columns blockIdx.x * 128 + 32 w .. + 31.  Per 32-token step the wave
@@ -385,5 +481,25 @@ extern "C" int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part
                (uint16_t*)dxa, (uint16_t*)xsd, dbg, dbu, dad};
   finish_kernel<<<(unsigned)((total4 + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total4);
   MX_CHECK_LAUNCH("mxfp8_mlp_bwd_finish");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w,
+                                int64_t rp, float scale, void* out, void* outT, int64_t Tpad, void* stream) {
+  MX_CHECK_ARG(x && q && s && w && out, "mxfp8_quant_lora: null pointer");
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32),
+               "mxfp8_quant_lora: need K %% 128 == 0, rp in {16, 32}");
+  MX_CHECK_ARG(Tpad == (T + 127) / 128 * 128, "mxfp8_quant_lora: Tpad must be ceil(T / 128) * 128");
+  MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(w, 16) && mx_aligned(q, 16) && mx_aligned(s, 16),
+               "mxfp8_quant_lora: misaligned buffer");
+  MX_CHECK_ARG(Tpad / 32 < (1LL << 31) && T * K < (1LL << 40), "mxfp8_quant_lora: too large");
+  dim3 grid((unsigned)(Tpad / 32));
+  hipStream_t stm = (hipStream_t)stream;
+#define QL_ARGS (const uint16_t*)x, ld_x, (int)T, (int)K, (const uint16_t*)w, (uint8_t*)q, (uint8_t*)s, scale, \
+                (uint16_t*)out, (uint16_t*)outT, (int)Tpad
+  if (rp == 16) quant_lora_kernel<16><<<grid, 256, 0, stm>>>(QL_ARGS);
+  else quant_lora_kernel<32><<<grid, 256, 0, stm>>>(QL_ARGS);
+#undef QL_ARGS
+  MX_CHECK_LAUNCH("mxfp8_quant_lora");
   return MXFP8_OK;
 }

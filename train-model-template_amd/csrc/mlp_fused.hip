@@ -139,24 +139,6 @@ __device__ __forceinline__ v16f lora_pi(const v8bf* wf, const v8bf* xf) {
   return d;
 }
 
-// MX-quantize the 16 contiguous values w (8 packed pairs) of row mc, columns k0..k0+15, which with the partner
-// lane's 16 form one 32-block: one 16-byte code store (row-major with Kq codes per row, or MX-tiled), scale
-// byte of row m (0 for padded rows).
-__device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
-                                        int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
-  u16x2 mm = {0, 0};
-#pragma unroll
-  for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
-  uint32_t am = amax_bits(mm);
-  am = max(am, (uint32_t)__shfl_xor((int)am, 32));
-  const uint32_t e = e8m0_from_amax_bits(am);
-  const uint4 c = make_uint4(encode4_bf16(w[0], w[1], e), encode4_bf16(w[2], w[3], e), encode4_bf16(w[4], w[5], e),
-                             encode4_bf16(w[6], w[7], e));
-  *reinterpret_cast<uint4*>(q + (tiled ? tiled_offset(mc, k0, Kq) : mc * Kq + k0)) = c;
-  // both lanes of the pair store the same byte (no divergent branch in the loop)
-  s[blocked_offset(m, k0 >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
-}
-
 // Grid (ceil(Tpad / 128), column groups): wave w of workgroup b owns the 32-row block 4b + w and walks every
 // 32-column tile of the group, loading tile t + 1 while it computes tile t; the four waves of a workgroup
 // walk the same tiles, so they share the LoRA weight rows in L1.  A wave sums its own xS_down partial over the

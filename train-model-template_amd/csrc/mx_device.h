@@ -166,6 +166,46 @@ __device__ __forceinline__ void load16_rc(const uint16_t* base, int64_t r, int64
   w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
 }
 
+// MX-quantize the 16 contiguous values w (8 packed pairs) of row mc, columns k0..k0+15, which with the partner
+// lane's 16 form one 32-block: one 16-byte code store (row-major with Kq codes per row, or MX-tiled), scale
+// byte of row m (0 for padded rows).
+__device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
+                                        int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
+  u16x2 mm = {0, 0};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
+  uint32_t am = amax_bits(mm);
+  am = max(am, (uint32_t)__shfl_xor((int)am, 32));
+  const uint32_t e = e8m0_from_amax_bits(am);
+  const uint4 c = make_uint4(encode4_bf16(w[0], w[1], e), encode4_bf16(w[2], w[3], e), encode4_bf16(w[4], w[5], e),
+                             encode4_bf16(w[6], w[7], e));
+  *reinterpret_cast<uint4*>(q + (tiled ? tiled_offset(mc, k0, Kq) : mc * Kq + k0)) = c;
+  // both lanes of the pair store the same byte (no divergent branch in the loop)
+  s[blocked_offset(m, k0 >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
+}
+
+// ---- LDS DMA (global_load_lds_dwordx4) and explicit memory-counter waits
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr_t)p; }
+
+// global_load_lds_dwordx4: lane i's 16 bytes land at LDS address m0 + 16 i.  Issued from inline assembly so
+// the compiler does not treat every later LDS read as dependent on every outstanding DMA (it cannot tell ring
+// stages apart and would drain a ring with vmcnt(0)); the kernels order them with explicit vmcnt waits and
+// barriers.  m0 is written here and nowhere else in this library's kernels.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N) leaving the other counters unconstrained (gfx9 encoding: vmcnt[3:0] at bits 3:0,
+// vmcnt[5:4] at bits 15:14, expcnt at 6:4, lgkmcnt at 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ---- transposes through LDS with ds_read_b64_tr_b16 (gfx950)
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s16 __attribute__((ext_vector_type(8)));

@@ -78,27 +78,6 @@ struct Shape {
   static constexpr int64_t kPartBytes = (int64_t)kBM * kBN * 4;  // fp32 partial tile
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// global_load_lds_dwordx4: lane i's 16 bytes land at LDS address m0 + 16 i.  Issued from inline assembly so
-// the compiler does not treat every later LDS read as dependent on every outstanding DMA (it cannot tell the
-// ring stages apart and would drain the ring with vmcnt(0)); the kernel orders them itself with explicit
-// vmcnt waits and barriers.  m0 is written here and nowhere else in the kernels of this file.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr_t)p; }
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// s_waitcnt vmcnt(N) leaving the other counters unconstrained (gfx9 encoding: vmcnt[3:0] at bits 3:0,
-// vmcnt[5:4] at bits 15:14, expcnt at 6:4, lgkmcnt at 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 struct Lora {
   const uint16_t* p;  // [M, r] bf16
   int64_t ld_p;

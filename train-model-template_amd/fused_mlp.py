@@ -186,13 +186,17 @@ class _MLP(torch.autograd.Function):
         lw = _prep(Ag, Bg, Au, Bu, Ad, Bd, dt)  # every bf16 form of the LoRA weights, one kernel per step
         S, bg, bu, ad, bd = lw.S, lw.bg, lw.bu, lw.ad, lw.bd
         T, R = x2.shape[0], Ad.shape[0]
-        # xs = bf16(x2 · Sᵀ) [T, 2R] = xa_gate | xa_up, and its zero-padded transpose for the backward kernel
-        xs = torch.empty((T, 2 * R), dtype=dt, device=x2.device)
-        xsT = torch.empty((2 * R, _cdiv(T, 128) * 128), dtype=dt, device=x2.device)
-        _native.lora_nt(x2, S, xs, outT=xsT)
-        # GEMM operands in the MX-tiled layout (same codes and scales as mx_quant; the GEMM streams 1 KB blocks)
+        # one read of x2: its MX operand (MX-tiled codes, the GEMM's operand layout; same codes and scales as
+        # mx_quant) and xs = bf16(x2 · Sᵀ) [T, 2R] = xa_gate | xa_up, with the zero-padded transpose the backward
+        # kernel reads
+        if 2 * R <= 32:
+            q, sc, xs, xsT = mxfp8.mx_quant_lora(x2, S)
+        else:
+            xs = torch.empty((T, 2 * R), dtype=dt, device=x2.device)
+            xsT = torch.empty((2 * R, _cdiv(T, 128) * 128), dtype=dt, device=x2.device)
+            _native.lora_nt(x2, S, xs, outT=xsT)
+            q, sc = mxfp8.mx_quant_tiled(x2)
         # gu = gate | up [T, 2N] in the fused-tile layout the fused kernels read (32 x 32 blocks of 2 KB)
-        q, sc = mxfp8.mx_quant_tiled(x2)
         gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=_LAYOUT_FT, m=T)
         del q, sc
         if need_out:
@@ -222,13 +226,10 @@ class _MLP(torch.autograd.Function):
             dy2 = dy2.contiguous()
         T, N = dy2.shape[0], hold.n
         lw, xsT = ctx.lw, ctx.xsT
-        qd, sd = mxfp8.mx_quant_tiled(dy2)
+        # one read of dy2: its MX operand and dxd = bf16(bf16(dy2 · bd) · s_d) [T, R] with its zero-padded transpose
+        qd, sd, dxd, dxdT = mxfp8.mx_quant_lora(dy2, lw.bdT, scale=s_d)
         dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)  # MX(dy) · W_down, FT
         del qd, sd
-        # dxd = bf16(bf16(dy2 · bd) · s_d) [T, R], and its zero-padded transpose
-        dxd = torch.empty((T, R), dtype=dt, device=dy2.device)
-        dxdT = torch.empty((R, xsT.shape[1]), dtype=dt, device=dy2.device)
-        _native.lora_nt(dy2, lw.bdT, dxd, scale=s_d, outT=dxdT)
         qg, sg, parts = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, lw.bgT, lw.buT, ad, lw.adT, s_g, s_u,
                                     need_x, None, True, gu_ft=True)
         del dhm

@@ -72,6 +72,21 @@ def mx_quant_tiled(x2d):
     return q, s.view(E8)
 
 
+def mx_quant_lora(x2d, w, scale=1.0, out_t=True):
+    """mx_quant_tiled(x2d) and bf16(x2d · wᵀ) (then bf16(· scale)) from one read of x2d, w [rp, K] bf16 with
+    rp in {16, 32}: -> (q, s, out [R, rp], outT [rp, ceil(R/128)*128] zero-padded, or None)."""
+    R, K = x2d.shape
+    assert x2d.dtype == torch.bfloat16 and x2d.stride(1) == 1 and K % 128 == 0 and R > 0, (x2d.dtype, x2d.shape)
+    rp = w.shape[0]
+    dev = x2d.device
+    q = torch.empty((tiled_rows(R), K), dtype=F8, device=dev)
+    s = torch.empty(scale_numel(R, K), dtype=torch.uint8, device=dev)
+    out = torch.empty((R, rp), dtype=torch.bfloat16, device=dev)
+    outT = torch.empty((rp, _cdiv(R, 128) * 128), dtype=torch.bfloat16, device=dev) if out_t else None
+    _native.quant_lora(x2d, q, s, w, out, scale=scale, outT=outT)
+    return q, s.view(E8), out, outT
+
+
 def tile_codes(q):
     """Row-major codes [R, K] (any row stride) -> the MX-tiled layout ([ceil(R/16)*16, K] bytes)."""
     R, K = q.shape
