@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 4
+#define MXFP8_MLP_ABI_VERSION 5
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -204,6 +204,33 @@ int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void*
  */
 int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w, int64_t rp,
                      float scale, void* out, void* outT, int64_t Tpad, void* stream);
+
+/*
+ * out = bf16(x + bf16(y + scale * xa · Bᵀ)): x, y, out [T, N] bf16 (row stride N), xa [T, r] bf16 (row stride
+ * ld_xa), B [N, r] bf16.  The LoRA-B addmm_ and the residual add of o_proj / out_proj in one pass; replaces res_lora /
+ * _res_lora_kernel (/root/reference/scripts/mxfp8.py:265-293).  N % 128 == 0, r in {16, 32}, T * N < 2^31; x, y,
+ * B, out 16-byte aligned, xa at any element offset and row stride.
+ */
+int mxfp8_res_lora(const void* x, const void* y, const void* xa, int64_t ld_xa, const void* b, int64_t T, int64_t N,
+                   int64_t r, float scale, void* out, void* stream);
+
+/* Row chunks mxfp8_lora_bwd uses for dy [T, N] (part_db holds chunks * N * r floats); 0 for invalid sizes. */
+int64_t mxfp8_lora_bwd_chunks(int64_t T, int64_t N);
+
+/*
+ * One read of dy [T, N] bf16 (row stride ld_dy) for the backward of a LoRA-carrying MX linear; replaces lora_bwd /
+ * _lora_bwd_kernel / _sum_parts (/root/reference/scripts/mxfp8.py:202-262).
+ *  - q != NULL: MX-quantize dy into columns col_tile_off*128 .. + N of the row-major code buffer q (row stride
+ *    ld_q) and its blocked scales s (s_col_tiles 128-column tiles per row, ceil(T/128) row tiles; padded rows
+ *    scale 0): byte for byte mxfp8_quant_rows(dy) placed at that column offset.
+ *  - xa != NULL: dxa [T, r] bf16 (row stride ld_dxa) = bf16(scale * dy · B) and db [N, r] fp32 = scale * dyᵀ · xa,
+ *    xa [T, r] bf16 (row stride ld_xa, 16-byte aligned), B [N, r] bf16.  part_dxa: (N/128) * T * r floats,
+ *    part_db: mxfp8_lora_bwd_chunks(T, N) * N * r floats of scratch, added in a fixed order (deterministic).
+ * N % 128 == 0, r in {16, 32}; at least one of q, xa.
+ */
+int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q, int64_t ld_q, void* s,
+                   int64_t s_col_tiles, int64_t col_tile_off, const void* xa, int64_t ld_xa, const void* b, int64_t r,
+                   float scale, void* dxa, int64_t ld_dxa, float* db, float* part_dxa, float* part_db, void* stream);
 
 /* Token chunks mxfp8_lora_tn uses for [T, K] (its partial buffer holds chunks * rp * K floats). */
 int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);

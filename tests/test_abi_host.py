@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 19, names
+    assert len(names) == 22, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -80,6 +80,19 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.mxfp8_lora_tn(p, 4, 96, 96, p, 16, 1, ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), 1.0, 0, 0, p,
                              None) == -1
     assert lib.mxfp8_lora_tn_chunks(10752, 2048) > 0 and lib.mxfp8_lora_tn_chunks(10752, 100) == 0
+    # residual LoRA epilogue: N % 128, r in {16, 32}
+    assert lib.mxfp8_res_lora(p, p, p, 16, p, 4, 100, 16, 1.0, p, None) == -1
+    assert lib.mxfp8_res_lora(p, p, p, 16, p, 4, 128, 8, 1.0, p, None) == -1
+    # LoRA backward: N % 128, something to do, rank, code columns inside q and its scale tiles
+    lb = lambda T, N, q, ld_q, s_tiles, off, xa, r: lib.mxfp8_lora_bwd(  # noqa: E731
+        p, T, N, N, q, ld_q, p if q else None, s_tiles, off, xa, 48, p, r, 1.0, p, 48, p, p, p, None)
+    assert lb(4, 100, p, 128, 1, 0, None, 16) == -1
+    assert lb(4, 128, None, 0, 0, 0, None, 16) == -1
+    assert lb(4, 128, None, 0, 0, 0, p, 8) == -1
+    assert lb(4, 256, p, 384, 3, 2, None, 16) == -1   # columns 256..511 past ld_q = 384
+    assert lb(4, 256, p, 512, 3, 2, None, 16) == -1   # scale tiles 2..3 past s_col_tiles = 3
+    assert b"destination" in lib.mxfp8_last_error()
+    assert lib.mxfp8_lora_bwd_chunks(10752, 4096) > 0 and lib.mxfp8_lora_bwd_chunks(10752, 100) == 0
     # tiled quantizer / tile_codes shape checks
     assert lib.mxfp8_quant_tiled(p, 4, 100, 100, p, p, None) == -1
     assert lib.mxfp8_tile_codes(p, 4, 96, 96, p, None) == -1

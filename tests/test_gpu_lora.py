@@ -139,3 +139,87 @@ def test_quant_lora_matches_quantizer_and_product(T, K, rp, scale, gpu):
     tpad = -(-T // 128) * 128
     assert outT.shape == (rp, tpad) and torch.equal(outT[:, :T].t().cpu(), out.cpu())
     assert int(torch.count_nonzero(outT[:, T:])) == 0
+
+
+@pytest.mark.parametrize("T,N,r,scale", [(300, 2048, 16, 2.0), (4096, 1024, 32, 0.5), (1, 128, 16, 1.0),
+                                         (10752, 2048, 16, 2.0)])
+def test_res_lora_matches_oracle(T, N, r, scale, gpu):
+    # out = bf16(x + bf16(y + scale · xa·Bᵀ)) (mxfp8.py:265-293): the GPU sums the r products in the MFMA's order,
+    # so an element may sit one bf16 step from the oracle where y + scale·p lies near a rounding boundary
+    import mxfp8
+    from oracle import lora
+    g = torch.Generator().manual_seed(T + N + r)
+    x = torch.randn(T, N, generator=g).to(torch.bfloat16)
+    y = torch.randn(T, N, generator=g).to(torch.bfloat16)
+    xa_full = torch.randn(T, r + 8, generator=g).to(torch.bfloat16)  # a column slice: row stride r + 8
+    xa = xa_full[:, 4:4 + r]
+    B = (torch.randn(N, r, generator=g) * 0.1).to(torch.bfloat16)
+    want = lora.res_lora(x, y, xa, B, scale)
+    xa_d = xa_full.to(gpu)[:, 4:4 + r]
+    got = mxfp8.res_lora(x.to(gpu), y.to(gpu), xa_d, B.to(gpu), scale).cpu()
+    # the intermediate t = bf16(y + scale·p) may land on a bf16 neighbour of the oracle's; the result must be the
+    # second rounding bf16(x + t) of one of those three values (under cancellation one step of t can exceed one
+    # step of the output), and equal the oracle's almost everywhere
+    t = (y.float() + scale * (xa.double() @ B.double().t()).float()).to(torch.bfloat16)
+    bits = t.view(torch.int16)
+    cands = [(x.float() + (bits + k).view(torch.bfloat16).float()).to(torch.bfloat16) for k in (-1, 0, 1)]
+    ok = (got == cands[0]) | (got == cands[1]) | (got == cands[2])
+    assert bool(ok.all()), (got[~ok][:4], want[~ok][:4])
+    assert torch.equal(cands[1], want)
+    assert (got == want).double().mean().item() >= 0.99
+
+
+@pytest.mark.parametrize("T,N,r,off,mode", [(300, 1024, 16, 1, "both"), (1, 128, 16, 0, "both"),
+                                            (4096, 2048, 32, 2, "both"), (777, 384, 16, 0, "quant"),
+                                            (2000, 512, 32, 0, "lora"), (10752, 4096, 16, 0, "both")])
+def test_lora_bwd_matches_oracle(T, N, r, off, mode, gpu):
+    # one read of dy (mxfp8.py:202-262): codes and scales at column tile `off` of a wider q, byte for byte the
+    # oracle quantizer's; d(xa) within one bf16 step of the oracle (the GPU adds the N products in another fp32
+    # order); dB within fp32 summation slack; other columns of q / s / the d(xa) destination untouched
+    import mxfp8
+    from oracle import lora, mx
+    g = torch.Generator().manual_seed(T + N + r + off)
+    dy = torch.randn(T, N, generator=g).to(torch.bfloat16)
+    xS = torch.randn(T, 3 * r, generator=g).to(torch.bfloat16)  # xa = the middle r columns (row stride 3r)
+    B = (torch.randn(N, r, generator=g) * 0.05).to(torch.bfloat16)
+    scale = 0.5
+    do_q, has_lora = mode != "lora", mode != "quant"
+    width = (off + N // 128 + 1) * 128
+    q = torch.zeros(T, width, dtype=torch.uint8, device=gpu) if do_q else None
+    s = torch.zeros(mxfp8.scale_numel(T, width), dtype=torch.uint8, device=gpu) if do_q else None
+    xS_d = xS.to(gpu)
+    dS = torch.zeros(T, 2 * r, dtype=torch.bfloat16, device=gpu)
+    db = mxfp8.lora_bwd(dy.to(gpu), xS_d[:, r:2 * r] if has_lora else None, B.to(gpu) if has_lora else None,
+                        scale, q, s, off, dS[:, r:] if has_lora else None)
+    if do_q:
+        qr = torch.zeros(T, width, dtype=torch.uint8)
+        sr = torch.zeros(mx.scale_bytes(T, width), dtype=torch.uint8)
+        mx.quant_into(dy, qr, sr, off * 128, width // 128)
+        assert torch.equal(q.cpu(), qr) and torch.equal(s.cpu(), sr)
+    if not has_lora:
+        assert db is None
+        return
+    want_dxa, want_db = lora.lora_bwd(dy, xS[:, r:2 * r], B, scale)
+    got = dS.cpu()
+    assert int(torch.count_nonzero(got[:, :r])) == 0
+    exact = scale * (dy.double() @ B.double())
+    absum = scale * (dy.double().abs() @ B.double().abs())
+    _bf16_step_ok(got[:, r:], exact, absum)
+    assert (got[:, r:] == want_dxa).double().mean().item() >= 0.99
+    absum_b = scale * (dy.double().abs().t() @ xS[:, r:2 * r].double().abs())
+    d = (db.cpu().double() - want_db.double()).abs()
+    assert bool((d <= 2.0 ** -16 * absum_b + 1e-30).all()), (d / absum_b.clamp_min(1e-30)).max().item()
+    db2 = mxfp8.lora_bwd(dy.to(gpu), xS_d[:, r:2 * r], B.to(gpu), scale, None, None, 0, dS[:, r:])
+    assert torch.equal(db2, db)  # deterministic: fixed-order partial sums
+
+
+def test_lora_bwd_quant_matches_mx_quant(gpu):
+    # quantization alone into a q of the same width: the bytes of mxfp8.mx_quant(dy)
+    import mxfp8
+    g = torch.Generator().manual_seed(9)
+    dy = (torch.randn(1000, 768, generator=g) * 3).to(torch.bfloat16).to(gpu)
+    q = torch.empty(1000, 768, dtype=mxfp8.F8, device=gpu)
+    s = torch.empty(mxfp8.scale_numel(1000, 768), dtype=torch.uint8, device=gpu)
+    assert mxfp8.lora_bwd(dy, q=q, s=s) is None
+    qr, sr = mxfp8.mx_quant(dy)
+    assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr.view(torch.uint8))

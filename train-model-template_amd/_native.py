@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT = 1, 2, 4, 8  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -37,14 +37,18 @@ SIGNATURES = {
     "mxfp8_lora_prep": [_ptr] * 6 + [_i64, _i64, _i64] + [_ptr] * 10 + [_ptr],
     "mxfp8_lora_nt": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
+    "mxfp8_res_lora": [_ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _f32, _ptr, _ptr],
     "mxfp8_lora_tn_chunks": [_i64, _i64],
+    "mxfp8_lora_bwd_chunks": [_i64, _i64],
+    "mxfp8_lora_bwd": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _i64,
+                       _ptr, _ptr, _ptr],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
                              _ptr, _ptr],
 }
 
 _RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64, "mxfp8_mlp_fwd_groups": _i64,
-             "mxfp8_lora_tn_chunks": _i64}
+             "mxfp8_lora_tn_chunks": _i64, "mxfp8_lora_bwd_chunks": _i64}
 
 _lib = None
 _WORKSPACE = {}  # (device index, stream) -> zero-initialised uint8 workspace of the MX GEMM
@@ -200,6 +204,27 @@ def quant_lora(x, q, s, w, out, scale=1.0, outT=None):
     T, K = x.shape
     call("mxfp8_quant_lora", _p(x), T, K, x.stride(0), _p(q), _p(s), _p(w), w.shape[0], float(scale), _p(out),
          _p(outT), -(-T // 128) * 128, like=x)
+
+
+def res_lora(x, y, xa, b, out, scale):
+    """out = bf16(x + bf16(y + scale · xa · bᵀ)); x, y, out [T, N], xa [T, r] (row stride any), b [N, r]."""
+    T, N = x.shape
+    call("mxfp8_res_lora", _p(x), _p(y), _p(xa), xa.stride(0), _p(b), T, N, b.shape[1], float(scale), _p(out),
+         like=x)
+
+
+def lora_bwd_chunks(T, N):
+    return int(load().mxfp8_lora_bwd_chunks(T, N))
+
+
+def lora_bwd(dy, q, s, s_col_tiles, col_tile_off, xa, b, scale, dxa, db, part_dxa, part_db):
+    """One read of dy [T, N]: MX codes/scales into q/s at column tile col_tile_off (q None: skipped) and, with xa,
+    dxa = bf16(scale · dy·b), db = scale · dyᵀ·xa (fp32) through the partial buffers."""
+    T, N = dy.shape
+    lora = xa is not None
+    call("mxfp8_lora_bwd", _p(dy), T, N, dy.stride(0), _p(q), q.stride(0) if q is not None else 0, _p(s),
+         s_col_tiles, col_tile_off, _p(xa), xa.stride(0) if lora else 0, _p(b), b.shape[1] if lora else 0,
+         float(scale), _p(dxa), dxa.stride(0) if lora else 0, _p(db), _p(part_dxa), _p(part_db), like=dy)
 
 
 def lora_tn(x, p, out, part, scale=1.0, transpose=False):

@@ -13,6 +13,8 @@
 // the row).  Products that reduce over the tokens split the tokens into chunks whose fp32 partials are added
 // in chunk order by a second kernel (deterministic); inside a chunk both operands are transposed through LDS
 // with ds_read_b64_tr_b16 so that k runs along the tokens.
+#include <algorithm>
+
 #include "abi_common.h"
 #include "mx_device.h"
 
@@ -229,6 +231,220 @@ __global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restr
     if (r < T) out[(int64_t)r * RP + rho] = bf(v);
     if (outT) outT[(int64_t)rho * Tpad + r] = r < T ? bf(v) : (uint16_t)0;
   }
+}
+
+// ------------------------------------------------------------------ residual + rank-r epilogue
+// out = bf16(x + bf16(y + scale * xa · Bᵀ)) for x, y [T, N] bf16 (row stride N), xa [T, R] (row stride ld_xa),
+// B [N, R] bf16: the addmm_ of the LoRA-B product followed by the residual add, in one pass
+// (/root/reference/scripts/mxfp8.py:265-293).  Grid (ceil(T / 32), N / 128), 4 waves: wave w owns the 32 x 32
+// tile (rows 32b.., columns 128c + 32w..).  The rank-r product runs on the 32x32x16 MFMA with weight rows in the
+// pi_col order, so each lane holds 16 contiguous columns of its row and moves x, y and out as 16-byte pieces.
+template <int R, bool kVecXa>
+__global__ __launch_bounds__(256) void res_lora_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ y,
+                                                       const uint16_t* __restrict__ xa, int64_t ld_xa,
+                                                       const uint16_t* __restrict__ B, int T, int N, float scale,
+                                                       uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
+  const int m = blockIdx.x * 32 + (lane & 31);
+  const bool live = m < T;
+  const int mc = live ? m : T - 1;
+  const int jb = blockIdx.y * 128 + w * 32;
+  const int64_t e0 = (int64_t)mc * N + jb + lg * 16;  // this lane's 16 contiguous elements
+  uint32_t xv[8], yv[8];
+  load16(x + e0, xv);
+  load16(y + e0, yv);
+  v8bf xf[R / 16], wf[R / 16];
+  const int64_t wr = (int64_t)(jb + pi_col(lane & 31)) * R + lg * 8;
+#pragma unroll
+  for (int h = 0; h < R / 16; ++h) {
+    const uint16_t* px = xa + (int64_t)mc * ld_xa + h * 16 + lg * 8;
+    if constexpr (kVecXa) {
+      xf[h] = load_bf8(px);
+    } else {  // xa at any element offset and row stride: eight 2-byte loads
+      v8s16 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (short)px[e];
+      xf[h] = __builtin_bit_cast(v8bf, v);
+    }
+    wf[h] = load_bf8(B + wr + h * 16);
+  }
+  const v16f d = lora_pi<R>(wf, xf);
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    float t0 = bf16_lo(yv[i / 2]) + scale * d[i], t1 = bf16_hi(yv[i / 2]) + scale * d[i + 1];
+    rnd2(t0, t1);  // t = bf16(y + scale * xa·Bᵀ)
+    float o0 = bf16_lo(xv[i / 2]) + t0, o1 = bf16_hi(xv[i / 2]) + t1;
+    o[i / 2] = rnd2(o0, o1);
+  }
+  if (live) {
+    uint4* po = reinterpret_cast<uint4*>(out + e0);
+    po[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    po[1] = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+}
+
+// --------------------------------------------------------------- LoRA backward of a linear: one read of dy
+// For dy [T, N] bf16 (row stride ld_dy), from ONE read (/root/reference/scripts/mxfp8.py:89-262, lora_bwd):
+//   kQuant: MX(dy) into columns col_tile_off*128 .. of a wider code buffer q (row stride ld_q) and its blocked
+//           scales s (s_col_tiles 128-column tiles per row), byte for byte mx_quant(dy) (rows past T: scale 0);
+//   kLora:  d(xa) = scale · dy · B  (B [N, R] bf16) and dB = scale · dyᵀ · xa (xa [T, R] bf16, row stride ld_xa),
+//           as fp32 partial sums: part_dxa [N / 128, T, R] over each 128-column chunk, part_db [rs, N, R] over each
+//           row chunk (added in order by lora_bwd_sum_kernel).
+// Grid (rs, N / 128), 4 waves: the workgroup owns rows [blockIdx.x * chunk, + chunk) (clipped at Tpad, a multiple
+// of 128, so the padded rows of the last scale tiles get scale 0) and 128 columns, and streams 32-row blocks of dy
+// (32 x 256 B, the same chunk swizzle as quant_lora_kernel) and of xa (32 rows x 2R B) through a 4-stage LDS ring.
+// Wave w takes columns 32w..32w+31: lane l reads 16 contiguous values of row l%32, quantizes them with lane l^32,
+// and feeds them to the d(xa) MFMA (its B operand fragments gathered once per workgroup); the 4 waves' d(xa)
+// products are added in LDS in a fixed order.  For dB the wave writes its 32 x 32 dy tile to LDS (zero past T) and
+// reads it back transposed (ds_read_b64_tr_b16), with xa read transposed from the ring: 16x16x32 MFMAs over the
+// block's 32 rows, accumulated in registers over the row chunk.
+template <int R, bool kQuant, bool kLora>
+__global__ __launch_bounds__(256) void lora_bwd_kernel(const uint16_t* __restrict__ dy, int64_t ld_dy, int T, int N,
+                                                       int Tpad, int chunk, uint8_t* __restrict__ q, int64_t ld_q,
+                                                       uint8_t* __restrict__ s, int64_t s_col_tiles, int col_tile_off,
+                                                       const uint16_t* __restrict__ xa, int64_t ld_xa,
+                                                       const uint16_t* __restrict__ B, float* __restrict__ part_dxa,
+                                                       float* __restrict__ part_db) {
+  constexpr int kStages = 4, kTileB = 32 * 256, kXaB = 32 * R * 2, kStageB = kTileB + kXaB;
+  constexpr int kXaDma = kXaB / 1024;  // 1 or 2 distinct 1 KB pieces; every wave issues one (copies repeat)
+  constexpr int kDma = 2 + (kLora ? 1 : 0);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
+  __shared__ __attribute__((aligned(16))) uint16_t trt[4][32 * kTrLd];  // per-wave dy tile for dB
+  __shared__ float red[4][32][R + 1];                                     // per-wave d(xa) products
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
+  const int r0 = blockIdx.x * chunk, r1 = min(r0 + chunk, Tpad);
+  const int c0 = blockIdx.y * 128;
+  const int row = lane & 31;
+  // DMA sources for the block at rows rb: dy rows 4j + lane/16 (j = 2w, 2w + 1), logical chunk (lane%16)^(row%16)
+  const int pc = lane & 15;
+  int xr[2], xc[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    xr[jj] = 4 * (2 * w + jj) + (lane >> 4);
+    xc[jj] = c0 + (pc ^ (xr[jj] & 15)) * 8;
+  }
+  // xa piece of this wave: piece w % kXaDma, lane i -> row (1024 / (2R)) * piece + i / (2R / 16), 16-B part
+  const int xpiece = w % kXaDma, xper = 2 * R / 16;  // 16-byte parts per xa row
+  const int xar = xpiece * (64 / xper) + lane / xper, xac = (lane % xper) * 8;
+  const uint32_t lds0 = lds_addr(lds);
+  auto issue = [&](int rb, int slot) {
+    const uint32_t st = lds0 + slot * kStageB;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      dma16(dy + (int64_t)min(rb + xr[jj], T - 1) * ld_dy + xc[jj], st + (2 * w + jj) * 1024);
+    if constexpr (kLora) dma16(xa + (int64_t)min(rb + xar, T - 1) * ld_xa + xac, st + kTileB + xpiece * 1024);
+  };
+  // d(xa) A operand: lane l holds B[n, ρ] (ρ = l % 32 < R, else 0) at the lane's columns n (both MFMA k steps)
+  v8bf bt[2];
+  if constexpr (kLora) {
+    const int rho = row;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      v8s16 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int n = c0 + 32 * w + 16 * lg + 8 * ks + e;
+        v[e] = rho < R ? (short)B[(int64_t)n * R + rho] : (short)0;
+      }
+      bt[ks] = __builtin_bit_cast(v8bf, v);
+    }
+    wait_vmcnt<0>();  // so that no wait for these loads lands inside the DMA loop
+  }
+  const int cx = 4 * w + 2 * lg;  // the lane's first logical 16-byte chunk of a block row
+  const int sx0 = (cx ^ (row & 15)) << 4, sx1 = ((cx + 1) ^ (row & 15)) << 4;
+  v4f db[2][R / 16];
+#pragma unroll
+  for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+    for (int h = 0; h < R / 16; ++h) db[jh][h] = v4f{};
+  const int nblk = (r1 - r0) / 32;
+#pragma unroll
+  for (int j = 0; j < kStages - 1; ++j) issue(r0 + 32 * min(j, nblk - 1), j);
+  int slot = 0;
+  for (int b = 0; b < nblk; ++b) {
+    const int rb = r0 + 32 * b;
+    wait_vmcnt<(kStages - 2) * kDma>();
+    lds_barrier();  // block b landed for every wave; every wave is done with block b - 1's slot and red[]
+    issue(r0 + 32 * min(b + kStages - 1, nblk - 1), slot == 0 ? kStages - 1 : slot - 1);
+    const uint8_t* st = lds + slot * kStageB;
+    const uint4 a = *reinterpret_cast<const uint4*>(st + row * 256 + sx0);
+    const uint4 c = *reinterpret_cast<const uint4*>(st + row * 256 + sx1);
+    uint32_t v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+    const int m = rb + row;
+    const bool live = m < T;
+    const int mc = live ? m : T - 1;
+    if constexpr (kQuant)
+      quant16(v, lane, m, live, q, mc, ld_q, false, (int64_t)col_tile_off * 128 + c0 + 32 * w + 16 * lg, s,
+              s_col_tiles);
+    if constexpr (kLora) {
+      // d(xa) partial over this wave's 32 columns: D[ρ][t] (lane: t = l % 32, ρ = tile_col(i, l))
+      v16f p = v16f{};
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bt[0], as_bf8(a), p, 0, 0, 0);
+      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bt[1], as_bf8(c), p, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rr = (i >> 2) * 8 + lg * 4 + (i & 3);
+        if (rr < R) red[w][row][rr] = p[i];
+      }
+      // dB: D[n][ρ] += Σ_t dy[t, n] xa[t, ρ] over the block's rows (rows past T add nothing)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = live ? v[k] : 0u;
+      tr_store(trt[w], lane, v);
+      const uint16_t* xt = reinterpret_cast<const uint16_t*>(st + kTileB);
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh) {
+        const v8bf ad = tr_operand(trt[w], jh * 16, lane);
+#pragma unroll
+        for (int h = 0; h < R / 16; ++h) {
+          // rows past T hold row T - 1's xa: their dy is zero, so they add nothing
+          const v8bf xb = tr_operand_ld(xt, R, h * 16, lane);
+          db[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, xb, db[jh][h], 0, 0, 0);
+        }
+      }
+      lds_barrier();
+      float* dst = part_dxa + ((int64_t)blockIdx.y * T + rb) * R;
+      for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
+        const int tt = idx / R, rr = idx % R;
+        if (rb + tt < T) dst[idx] = ((red[0][tt][rr] + red[1][tt][rr]) + red[2][tt][rr]) + red[3][tt][rr];
+      }
+    }
+    slot = slot + 1 == kStages ? 0 : slot + 1;
+  }
+  wait_vmcnt<0>();
+  if constexpr (kLora) {
+    // lane l: ρ = 16 h + l % 16, n = c0 + 32 w + 16 jh + (l / 16) * 4 + i
+#pragma unroll
+    for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+      for (int h = 0; h < R / 16; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = c0 + 32 * w + 16 * jh + (lane >> 4) * 4 + i;
+          part_db[((int64_t)blockIdx.x * N + n) * R + h * 16 + (lane & 15)] = db[jh][h][i];
+        }
+  }
+}
+
+// dxa[t, ρ] (row stride ld_dxa) = bf16(scale · Σ_p part_dxa[p, t, ρ]) and dB[n, ρ] = scale · Σ_p part_db[p, n, ρ]
+// (fp32), partials added in ascending p (mxfp8.py:180-216, _sum_rows / _sum_parts).  One thread per output element.
+__global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restrict__ part_dxa, int ncs,
+                                                           const float* __restrict__ part_db, int nrs, int T, int N,
+                                                           int R, float scale, uint16_t* __restrict__ dxa,
+                                                           int64_t ld_dxa, float* __restrict__ dB) {
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nx = (int64_t)T * R, nb = (int64_t)N * R;
+  if (i < nx) {
+    float v = part_dxa[i];
+    for (int p = 1; p < ncs; ++p) v += part_dxa[(int64_t)p * nx + i];
+    dxa[(i / R) * ld_dxa + i % R] = bf(v * scale);
+    return;
+  }
+  i -= nx;
+  if (i >= nb) return;
+  float v = part_db[i];
+  for (int p = 1; p < nrs; ++p) v += part_db[(int64_t)p * nb + i];
+  dB[i] = v * scale;
 }
 
 // ------------------------------------------------------------------------------------- Pᵀ · X (tn)
@@ -501,5 +717,81 @@ extern "C" int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_
   else quant_lora_kernel<32><<<grid, 256, 0, stm>>>(QL_ARGS);
 #undef QL_ARGS
   MX_CHECK_LAUNCH("mxfp8_quant_lora");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_res_lora(const void* x, const void* y, const void* xa, int64_t ld_xa, const void* b, int64_t T,
+                              int64_t N, int64_t r, float scale, void* out, void* stream) {
+  MX_CHECK_ARG(x && y && xa && b && out, "mxfp8_res_lora: null pointer");
+  MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && (r == 16 || r == 32) && ld_xa >= r,
+               "mxfp8_res_lora: need N %% 128 == 0, r in {16, 32}");
+  MX_CHECK_ARG(T * N < (1LL << 31), "mxfp8_res_lora: T * N must stay below 2^31");
+  MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(y, 16) && mx_aligned(b, 16) && mx_aligned(out, 16) &&
+                   mx_aligned(xa, 2),
+               "mxfp8_res_lora: misaligned buffer");
+  const bool vec = mx_aligned(xa, 16) && ld_xa % 8 == 0;
+  dim3 grid((unsigned)((T + 31) / 32), (unsigned)(N / 128));
+  hipStream_t stm = (hipStream_t)stream;
+#define RL_ARGS (const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)xa, ld_xa, (const uint16_t*)b, (int)T, (int)N, \
+                scale, (uint16_t*)out
+  if (r == 16) {
+    if (vec) res_lora_kernel<16, true><<<grid, 256, 0, stm>>>(RL_ARGS);
+    else res_lora_kernel<16, false><<<grid, 256, 0, stm>>>(RL_ARGS);
+  } else {
+    if (vec) res_lora_kernel<32, true><<<grid, 256, 0, stm>>>(RL_ARGS);
+    else res_lora_kernel<32, false><<<grid, 256, 0, stm>>>(RL_ARGS);
+  }
+#undef RL_ARGS
+  MX_CHECK_LAUNCH("mxfp8_res_lora");
+  return MXFP8_OK;
+}
+
+extern "C" int64_t mxfp8_lora_bwd_chunks(int64_t T, int64_t N) {
+  if (T <= 0 || N <= 0 || N % 128) return 0;
+  const int64_t blocks = (T + 127) / 128 * 4;  // 32-row blocks up to the padded end of the last 128-row tile
+  const int64_t cs = N / 128, want = (512 + cs - 1) / cs;
+  const int64_t per = (blocks + std::min(want, blocks) - 1) / std::min(want, blocks);
+  return (blocks + per - 1) / per;
+}
+
+extern "C" int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q, int64_t ld_q, void* s,
+                              int64_t s_col_tiles, int64_t col_tile_off, const void* xa, int64_t ld_xa, const void* b,
+                              int64_t r, float scale, void* dxa, int64_t ld_dxa, float* db, float* part_dxa,
+                              float* part_db, void* stream) {
+  const bool quant = q != nullptr, lora = xa != nullptr;
+  MX_CHECK_ARG(dy && (quant || lora), "mxfp8_lora_bwd: need dy and q/s or xa");
+  MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && ld_dy >= N && ld_dy % 8 == 0 && T * ld_dy < (1LL << 40),
+               "mxfp8_lora_bwd: need N %% 128 == 0");
+  MX_CHECK_ARG(!quant || (s && ld_q % 16 == 0 && col_tile_off >= 0 && col_tile_off * 128 + N <= ld_q &&
+                          col_tile_off * 128 + N <= s_col_tiles * 128 && mx_aligned(q, 16)),
+               "mxfp8_lora_bwd: bad code / scale destination");
+  MX_CHECK_ARG(!lora || (b && dxa && db && part_dxa && part_db && (r == 16 || r == 32) && ld_xa >= r &&
+                         ld_xa % 8 == 0 && ld_dxa >= r && mx_aligned(xa, 16) && mx_aligned(b, 2)),
+               "mxfp8_lora_bwd: LoRA needs xa, B, dxa, dB and partial buffers, r in {16, 32}");
+  MX_CHECK_ARG(mx_aligned(dy, 16), "mxfp8_lora_bwd: misaligned dy");
+  const int64_t rs = mxfp8_lora_bwd_chunks(T, N);
+  const int64_t Tpad = (T + 127) / 128 * 128, blocks = Tpad / 32;
+  const int64_t chunk = (blocks + rs - 1) / rs * 32;
+  const int64_t used = (Tpad + chunk - 1) / chunk;
+  hipStream_t stm = (hipStream_t)stream;
+  dim3 grid((unsigned)used, (unsigned)(N / 128));
+#define LB_ARGS (const uint16_t*)dy, ld_dy, (int)T, (int)N, (int)Tpad, (int)chunk, (uint8_t*)q, ld_q, (uint8_t*)s, \
+                s_col_tiles, (int)col_tile_off, (const uint16_t*)xa, ld_xa, (const uint16_t*)b, part_dxa, part_db
+  if (!lora) lora_bwd_kernel<16, true, false><<<grid, 256, 0, stm>>>(LB_ARGS);
+  else if (r == 16) {
+    if (quant) lora_bwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(LB_ARGS);
+    else lora_bwd_kernel<16, false, true><<<grid, 256, 0, stm>>>(LB_ARGS);
+  } else {
+    if (quant) lora_bwd_kernel<32, true, true><<<grid, 256, 0, stm>>>(LB_ARGS);
+    else lora_bwd_kernel<32, false, true><<<grid, 256, 0, stm>>>(LB_ARGS);
+  }
+#undef LB_ARGS
+  MX_CHECK_LAUNCH("mxfp8_lora_bwd");
+  if (lora) {
+    const int64_t total = T * r + N * r;
+    lora_bwd_sum_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stm>>>(
+        part_dxa, (int)(N / 128), part_db, (int)used, (int)T, (int)N, (int)r, scale, (uint16_t*)dxa, ld_dxa, db);
+    MX_CHECK_LAUNCH("mxfp8_lora_bwd");
+  }
   return MXFP8_OK;
 }

@@ -32,19 +32,6 @@ namespace {
 
 __device__ __forceinline__ int tile_col(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
-typedef float v2f __attribute__((ext_vector_type(2)));
-
-// Round a pair to bf16 with v_cvt_pk_bf16_f32 (round to nearest even, verified bit-exact against a software
-// RNE on the device); returns the packed pair and leaves the bf16-valued floats in a, b.
-__device__ __forceinline__ uint32_t rnd2(float& a, float& b) {
-  const v2f f = {a, b};
-  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
-  a = __uint_as_float(w << 16);
-  b = __uint_as_float(w & 0xffff0000u);
-  return w;
-}
-
 // sigmoid(g) = 1 / (1 + exp(-g)) with the hardware exp2 and reciprocal (about 1 ulp each; the reference's
 // Triton fp32 division is approximate as well); silu(g) = g * sigmoid(g).  exp(-g) overflowing to +inf
 // gives sigmoid 0 and silu -0, as g / (exp(-g) + 1) does.
@@ -127,18 +114,6 @@ __device__ __forceinline__ v8bf words_bf8(const uint32_t* w) { return as_bf8(mak
 // pieces, quantizes 16 adjacent codes of one 32-block with its partner lane l ^ 32, and stores them as one
 // 16-byte word (the accumulator order of the previous tile layout needed four 8-byte loads and four 4-byte
 // stores per 16 values).
-__device__ __forceinline__ int pi_col(int a) { return ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3); }
-
-// D[a][m] = Σ_ρ W[jb + pi_col(a), ρ] · X[m, ρ] from the lane's weight-row fragments wf (lane l holds weight row
-// jb + pi_col(l % 32), k = h*16 + (l/32)*8 .. +7 in wf[h])
-template <int R>
-__device__ __forceinline__ v16f lora_pi(const v8bf* wf, const v8bf* xf) {
-  v16f d = v16f{};
-#pragma unroll
-  for (int h = 0; h < R / 16; ++h) d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[h], xf[h], d, 0, 0, 0);
-  return d;
-}
-
 // Grid (ceil(Tpad / 128), column groups): wave w of workgroup b owns the 32-row block 4b + w and walks every
 // 32-column tile of the group, loading tile t + 1 while it computes tile t; the four waves of a workgroup
 // walk the same tiles, so they share the LoRA weight rows in L1.  A wave sums its own xS_down partial over the

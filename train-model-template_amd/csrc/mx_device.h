@@ -184,6 +184,34 @@ __device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool
   s[blocked_offset(m, k0 >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
 }
 
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// Round a pair to bf16 with v_cvt_pk_bf16_f32 (round to nearest even, verified bit-exact against a software
+// RNE on the device); returns the packed pair and leaves the bf16-valued floats in a, b.
+__device__ __forceinline__ uint32_t rnd2(float& a, float& b) {
+  const v2f f = {a, b};
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));
+  a = __uint_as_float(w << 16);
+  b = __uint_as_float(w & 0xffff0000u);
+  return w;
+}
+
+// ---- rank-r products in the fused kernels' column order
+// The LoRA-B product D[a][m] = Σ_ρ W[j(a), ρ] X[m, ρ] may take any weight row for MFMA row a; with j(a) = pi_col(a)
+// lane l holds, for row m = l % 32, the 16 CONTIGUOUS columns (l/32)*16 + i in its 16 accumulator registers i.
+__device__ __forceinline__ int pi_col(int a) { return ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3); }
+
+// D[a][m] = Σ_ρ W[jb + pi_col(a), ρ] · X[m, ρ] from the lane's weight-row fragments wf (lane l holds weight row
+// jb + pi_col(l % 32), k = h*16 + (l/32)*8 .. +7 in wf[h])
+template <int R>
+__device__ __forceinline__ v16f lora_pi(const v8bf* wf, const v8bf* xf) {
+  v16f d = v16f{};
+#pragma unroll
+  for (int h = 0; h < R / 16; ++h) d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[h], xf[h], d, 0, 0, 0);
+  return d;
+}
+
 // ---- LDS DMA (global_load_lds_dwordx4) and explicit memory-counter waits
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr_t)p; }
@@ -206,6 +234,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Workgroup barrier ordering LDS accesses only: waits for this wave's LDS operations (lgkmcnt), not for its
+// outstanding global loads, stores or LDS DMAs, which a __syncthreads() fence would drain.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---- transposes through LDS with ds_read_b64_tr_b16 (gfx950)
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef short v8s16 __attribute__((ext_vector_type(8)));
@@ -218,6 +254,19 @@ __device__ __forceinline__ v4s tr4(const uint16_t* tile, int r0, int c0, int lan
   const int sl = lane & 15;
   const uint16_t* p = tile + (r0 + (sl >> 2)) * kTrLd + c0 + 4 * (sl & 3);
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+}
+
+// tr4 / tr_operand over a [32][ld] bf16 tile of another row stride (ld % 4 == 0)
+__device__ __forceinline__ v4s tr4_ld(const uint16_t* tile, int ld, int r0, int c0, int lane) {
+  const int sl = lane & 15;
+  const uint16_t* p = tile + (r0 + (sl >> 2)) * ld + c0 + 4 * (sl & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+}
+__device__ __forceinline__ v8bf tr_operand_ld(const uint16_t* tile, int ld, int c0, int lane) {
+  const int g8 = (lane >> 4) * 8;
+  const v4s lo = tr4_ld(tile, ld, g8, c0, lane), hi = tr4_ld(tile, ld, g8 + 4, c0, lane);
+  const v8s16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(v8bf, v);
 }
 
 // 16x16x32 A operand of the transposed tile: lane l holds column c0 + l % 16, rows 8 (l / 16) + 0..7

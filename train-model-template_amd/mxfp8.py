@@ -87,6 +87,53 @@ def mx_quant_lora(x2d, w, scale=1.0, out_t=True):
     return q, s.view(E8), out, outT
 
 
+def res_lora(x, y, xa, B, scale):
+    """x + (y + scale * xa @ Bᵀ) for x, y [T, N] bf16 contiguous, xa [T, r] (any row stride), B [N, r] contiguous:
+    out = bf16(x + bf16(y + scale · xa·Bᵀ)), the LoRA-B addmm_ and the residual add in one pass
+    (mxfp8.py:285-293).  r in {16, 32} (the LoRA ranks this build supports)."""
+    T, N = x.shape
+    assert T * N < 2 ** 31 and N % 128 == 0, (x.shape,)
+    assert x.dtype == y.dtype == xa.dtype == B.dtype == torch.bfloat16 and x.is_contiguous() and y.is_contiguous()
+    assert B.is_contiguous() and xa.stride(1) == 1 and B.shape == (N, xa.shape[1]) and xa.shape[0] == T
+    assert xa.shape[1] in (16, 32), "res_lora: LoRA rank must be 16 or 32"
+    out = torch.empty_like(x)
+    if T:
+        _native.res_lora(x, y, xa, B, out, scale)
+    return out
+
+
+def lora_bwd(dy, xa=None, B=None, scale=1.0, q=None, s=None, col_tile_off=0, dxa_out=None):
+    """One read of dy [T, N] bf16 (unit column stride) for the backward of a LoRA-carrying MX linear
+    (mxfp8.py:202-262, same arguments and result):
+    - q/s given: MX codes of dy into columns col_tile_off*128 .. of q [T, ΣN] (row-major) and its scales into the
+      blocked layout of q (q.shape[1] / 128 column tiles), byte for byte mx_quant(dy);
+    - xa [T, r] (unit column stride, any row stride), B [N, r] contiguous given: writes bf16(scale · dy @ B) into
+      dxa_out [T, r] (any row stride) and returns dB = scale · dyᵀ @ xa in fp32; otherwise returns None.
+    r in {16, 32} (the LoRA ranks this build supports)."""
+    T, N = dy.shape
+    assert dy.dtype == torch.bfloat16 and dy.stride(1) == 1 and N % 128 == 0, (dy.dtype, dy.shape, dy.stride())
+    has_lora, do_q = xa is not None, q is not None
+    if not (has_lora or do_q) or T == 0:
+        return None if not has_lora else torch.zeros((N, xa.shape[1]), dtype=torch.float32, device=dy.device)
+    dev = dy.device
+    db = part_dxa = part_db = None
+    if do_q:
+        assert q.is_contiguous() and q.dim() == 2 and q.shape[0] == T and s is not None
+        assert s.numel() >= scale_numel(T, q.shape[1]) and (col_tile_off * 128 + N) <= q.shape[1]
+    if has_lora:
+        R = xa.shape[1]
+        assert R in (16, 32), "lora_bwd: LoRA rank must be 16 or 32"
+        assert xa.dtype == B.dtype == torch.bfloat16 and xa.stride(1) == 1 and B.is_contiguous()
+        assert B.shape == (N, R) and xa.shape[0] == T and dxa_out is not None and dxa_out.shape == (T, R)
+        assert dxa_out.stride(1) == 1 and dxa_out.dtype == torch.bfloat16
+        db = torch.empty((N, R), dtype=torch.float32, device=dev)
+        part_dxa = torch.empty((N // 128, T, R), dtype=torch.float32, device=dev)
+        part_db = torch.empty((_native.lora_bwd_chunks(T, N), N, R), dtype=torch.float32, device=dev)
+    _native.lora_bwd(dy, q.view(torch.uint8) if do_q else None, s.view(torch.uint8) if do_q else None,
+                     q.shape[1] // 128 if do_q else 0, col_tile_off, xa, B, scale, dxa_out, db, part_dxa, part_db)
+    return db
+
+
 def tile_codes(q):
     """Row-major codes [R, K] (any row stride) -> the MX-tiled layout ([ceil(R/16)*16, K] bytes)."""
     R, K = q.shape
