@@ -131,6 +131,38 @@ def _quantizer(T, K, N, dev):
     return out, wq_ms
 
 
+def _lora_epilogues(T, K, N, r, dev):
+    """The LoRA epilogues beside the MLP (mxfp8.lora_bwd, mxfp8.res_lora) at the workload's token count, timed with
+    events around back-to-back launches on the current stream; algorithmic bytes over the mean call time."""
+    import torch
+
+    import mxfp8
+    import workloads
+    g = torch.Generator(device=dev).manual_seed(7)
+    out = {}
+
+    def rec(name, ms, by):
+        out[name] = {"GB/s": round(by / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 2), "bytes": by,
+                     "frac": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+    for cols in (K, N):
+        dy = torch.randn(T, cols, device=dev, generator=g).to(torch.bfloat16)
+        xS = torch.randn(T, 2 * r, device=dev, generator=g).to(torch.bfloat16)
+        B = (torch.randn(cols, r, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        q = torch.empty(T, cols, dtype=mxfp8.F8, device=dev)
+        s = torch.empty(mxfp8.scale_numel(T, cols), dtype=torch.uint8, device=dev)
+        dS = torch.empty(T, 2 * r, dtype=torch.bfloat16, device=dev)
+        ms = _time_launches(lambda: mxfp8.lora_bwd(dy, xS[:, :r], B, 2.0, q, s, 0, dS[:, :r]), 50)
+        rec(f"lora_bwd+q dy[T,{cols}] r{r}", ms, workloads.lora_bwd_bytes(T, cols, r))
+        del dy, q, s
+    x = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16)
+    y = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16)
+    B = (torch.randn(K, r, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    ms = _time_launches(lambda: mxfp8.res_lora(x, y, xS[:, :r], B, 2.0), 50)
+    rec(f"res_lora [T,{K}] r{r}", ms, workloads.res_lora_bytes(T, K, r))
+    return out
+
+
 def _copy_calib(dev):
     import torch
     src = torch.ones(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev)
@@ -333,6 +365,7 @@ def main():
     if not args.no_quant:
         quant, wq_ms = _quantizer(T, K, N, dev)
         line["quantizer"] = quant
+        line["lora_epilogues"] = _lora_epilogues(T, K, N, c["r"], dev)
         tot = ms + wq_ms * c["layers"]
         line["with_requant"] = {"ms_per_step": round(tot, 4), "TFLOP/s": round(fl / (tot * 1e-3) / 1e12, 2),
                                 "weight_prep_ms_per_layer": round(wq_ms, 4)}

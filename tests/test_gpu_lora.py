@@ -171,7 +171,8 @@ def test_res_lora_matches_oracle(T, N, r, scale, gpu):
 
 @pytest.mark.parametrize("T,N,r,off,mode", [(300, 1024, 16, 1, "both"), (1, 128, 16, 0, "both"),
                                             (4096, 2048, 32, 2, "both"), (777, 384, 16, 0, "quant"),
-                                            (2000, 512, 32, 0, "lora"), (10752, 4096, 16, 0, "both")])
+                                            (2000, 512, 32, 0, "lora"), (10752, 4096, 16, 0, "both"),
+                                            (1500, 128, 32, 3, "both")])
 def test_lora_bwd_matches_oracle(T, N, r, off, mode, gpu):
     # one read of dy (mxfp8.py:202-262): codes and scales at column tile `off` of a wider q, byte for byte the
     # oracle quantizer's; d(xa) within one bf16 step of the oracle (the GPU adds the N products in another fp32

@@ -289,11 +289,11 @@ __global__ __launch_bounds__(256) void res_lora_kernel(const uint16_t* __restric
 //   kQuant: MX(dy) into columns col_tile_off*128 .. of a wider code buffer q (row stride ld_q) and its blocked
 //           scales s (s_col_tiles 128-column tiles per row), byte for byte mx_quant(dy) (rows past T: scale 0);
 //   kLora:  d(xa) = scale · dy · B  (B [N, R] bf16) and dB = scale · dyᵀ · xa (xa [T, R] bf16, row stride ld_xa),
-//           as fp32 partial sums: part_dxa [N / 128, T, R] over each 128-column chunk, part_db [rs, N, R] over each
-//           row chunk (added in order by lora_bwd_sum_kernel).
+//           as fp32 partial sums: part_dxa [N / 128, T, R] over each 128-column chunk (or d(xa) itself when N is
+//           one chunk), part_db [rs, N, R] over each row chunk (added in order by lora_bwd_sum_kernel).
 // Grid (rs, N / 128), 4 waves: the workgroup owns rows [blockIdx.x * chunk, + chunk) (clipped at Tpad, a multiple
 // of 128, so the padded rows of the last scale tiles get scale 0) and 128 columns, and streams 32-row blocks of dy
-// (32 x 256 B, the same chunk swizzle as quant_lora_kernel) and of xa (32 rows x 2R B) through a 4-stage LDS ring.
+// (32 x 256 B, the same chunk swizzle as quant_lora_kernel) and of xa (32 rows x 2R B) through an LDS ring.
 // Wave w takes columns 32w..32w+31: lane l reads 16 contiguous values of row l%32, quantizes them with lane l^32,
 // and feeds them to the d(xa) MFMA (its B operand fragments gathered once per workgroup); the 4 waves' d(xa)
 // products are added in LDS in a fixed order.  For dB the wave writes its 32 x 32 dy tile to LDS (zero past T) and
@@ -305,9 +305,13 @@ __global__ __launch_bounds__(256) void lora_bwd_kernel(const uint16_t* __restric
                                                        uint8_t* __restrict__ s, int64_t s_col_tiles, int col_tile_off,
                                                        const uint16_t* __restrict__ xa, int64_t ld_xa,
                                                        const uint16_t* __restrict__ B, float* __restrict__ part_dxa,
-                                                       float* __restrict__ part_db) {
-  constexpr int kStages = 4, kTileB = 32 * 256, kXaB = 32 * R * 2, kStageB = kTileB + kXaB;
-  constexpr int kXaDma = kXaB / 1024;  // 1 or 2 distinct 1 KB pieces; every wave issues one (copies repeat)
+                                                       float* __restrict__ part_db, uint16_t* __restrict__ dxa,
+                                                       int64_t ld_dxa, float scale) {
+  // Ring depth: stores issued inside the loop count in the same in-order vmcnt as the DMAs, so the wait for block b
+  // also covers the DMAs issued before the last stores; a deeper ring keeps about two blocks in flight regardless.
+  constexpr int kStages = R == 16 ? 6 : 5, kTileB = 32 * 256, kXaB = kLora ? 32 * R * 2 : 0;
+  constexpr int kStageB = kTileB + kXaB;
+  constexpr int kXaDma = kLora ? R / 16 : 1;  // 1 or 2 distinct 1 KB pieces; every wave issues one (copies repeat)
   constexpr int kDma = 2 + (kLora ? 1 : 0);
   __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
   __shared__ __attribute__((aligned(16))) uint16_t trt[4][32 * kTrLd];  // per-wave dy tile for dB
@@ -345,8 +349,9 @@ __global__ __launch_bounds__(256) void lora_bwd_kernel(const uint16_t* __restric
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int n = c0 + 32 * w + 16 * lg + 8 * ks + e;
-        v[e] = rho < R ? (short)B[(int64_t)n * R + rho] : (short)0;
+        v[e] = (short)B[(int64_t)n * R + (rho < R ? rho : 0)];
       }
+      if (rho >= R) v = v8s16{};
       bt[ks] = __builtin_bit_cast(v8bf, v);
     }
     wait_vmcnt<0>();  // so that no wait for these loads lands inside the DMA loop
@@ -403,10 +408,18 @@ __global__ __launch_bounds__(256) void lora_bwd_kernel(const uint16_t* __restric
         }
       }
       lds_barrier();
-      float* dst = part_dxa + ((int64_t)blockIdx.y * T + rb) * R;
-      for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
-        const int tt = idx / R, rr = idx % R;
-        if (rb + tt < T) dst[idx] = ((red[0][tt][rr] + red[1][tt][rr]) + red[2][tt][rr]) + red[3][tt][rr];
+      if (gridDim.y == 1) {  // one column chunk: the sum is final (mxfp8.py:168-172, DXA_DIRECT)
+        for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
+          const int tt = idx / R, rr = idx % R;
+          const float sum = ((red[0][tt][rr] + red[1][tt][rr]) + red[2][tt][rr]) + red[3][tt][rr];
+          if (rb + tt < T) dxa[(int64_t)(rb + tt) * ld_dxa + rr] = bf(sum * scale);
+        }
+      } else {
+        float* dst = part_dxa + ((int64_t)blockIdx.y * T + rb) * R;
+        for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
+          const int tt = idx / R, rr = idx % R;
+          if (rb + tt < T) dst[idx] = ((red[0][tt][rr] + red[1][tt][rr]) + red[2][tt][rr]) + red[3][tt][rr];
+        }
       }
     }
     slot = slot + 1 == kStages ? 0 : slot + 1;
@@ -426,25 +439,40 @@ __global__ __launch_bounds__(256) void lora_bwd_kernel(const uint16_t* __restric
   }
 }
 
-// dxa[t, ρ] (row stride ld_dxa) = bf16(scale · Σ_p part_dxa[p, t, ρ]) and dB[n, ρ] = scale · Σ_p part_db[p, n, ρ]
-// (fp32), partials added in ascending p (mxfp8.py:180-216, _sum_rows / _sum_parts).  One thread per output element.
-__global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restrict__ part_dxa, int ncs,
-                                                           const float* __restrict__ part_db, int nrs, int T, int N,
+// 16-byte vectors of fp32 partial sums added in ascending partial order, four loads in flight at a time
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 sum_ordered(const float4* __restrict__ p, int64_t stride, int n) {
+  float4 v = p[0];
+  int c = 1;
+  for (; c + 3 < n; c += 4) {
+    const float4 x0 = p[c * stride], x1 = p[(c + 1) * stride], x2 = p[(c + 2) * stride], x3 = p[(c + 3) * stride];
+    v = add4(add4(add4(add4(v, x0), x1), x2), x3);
+  }
+  for (; c < n; ++c) v = add4(v, p[c * stride]);
+  return v;
+}
+
+
+__global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restrict__ part_dxa, int ncs, int64_t nx,
+                                                           const float* __restrict__ part_db, int nrs, int64_t nb,
                                                            int R, float scale, uint16_t* __restrict__ dxa,
                                                            int64_t ld_dxa, float* __restrict__ dB) {
-  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t nx = (int64_t)T * R, nb = (int64_t)N * R;
+  int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i < nx) {
-    float v = part_dxa[i];
-    for (int p = 1; p < ncs; ++p) v += part_dxa[(int64_t)p * nx + i];
-    dxa[(i / R) * ld_dxa + i % R] = bf(v * scale);
+    const float4 v = sum_ordered(reinterpret_cast<const float4*>(part_dxa + i), nx / 4, ncs);
+    uint16_t* o = dxa + (i / R) * ld_dxa + i % R;  // R % 4 == 0: the four share a row
+    o[0] = bf(v.x * scale);
+    o[1] = bf(v.y * scale);
+    o[2] = bf(v.z * scale);
+    o[3] = bf(v.w * scale);
     return;
   }
   i -= nx;
   if (i >= nb) return;
-  float v = part_db[i];
-  for (int p = 1; p < nrs; ++p) v += part_db[(int64_t)p * nb + i];
-  dB[i] = v * scale;
+  const float4 v = sum_ordered(reinterpret_cast<const float4*>(part_db + i), nb / 4, nrs);
+  *reinterpret_cast<float4*>(dB + i) = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
 }
 
 // ------------------------------------------------------------------------------------- Pᵀ · X (tn)
@@ -562,21 +590,7 @@ struct FinishArgs {
 };
 
 // Four consecutive output elements per thread (16-byte loads) of dxa | xsd, dB_g, dB_u, dA_d; the partials
-// are added in ascending order, four loads in flight at a time (fused_mlp.py:258, :319-326).
-__device__ __forceinline__ float4 add4(float4 a, float4 b) {
-  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
-__device__ __forceinline__ float4 sum_ordered(const float4* __restrict__ p, int64_t stride, int n) {
-  float4 v = p[0];
-  int c = 1;
-  for (; c + 3 < n; c += 4) {
-    const float4 x0 = p[c * stride], x1 = p[(c + 1) * stride], x2 = p[(c + 2) * stride], x3 = p[(c + 3) * stride];
-    v = add4(add4(add4(add4(v, x0), x1), x2), x3);
-  }
-  for (; c < n; ++c) v = add4(v, p[c * stride]);
-  return v;
-}
-
+// are added in ascending order (fused_mlp.py:258, :319-326).
 __global__ __launch_bounds__(256) void finish_kernel(FinishArgs a, int64_t total4) {
   int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= total4) return;
@@ -776,7 +790,8 @@ extern "C" int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_d
   hipStream_t stm = (hipStream_t)stream;
   dim3 grid((unsigned)used, (unsigned)(N / 128));
 #define LB_ARGS (const uint16_t*)dy, ld_dy, (int)T, (int)N, (int)Tpad, (int)chunk, (uint8_t*)q, ld_q, (uint8_t*)s, \
-                s_col_tiles, (int)col_tile_off, (const uint16_t*)xa, ld_xa, (const uint16_t*)b, part_dxa, part_db
+                s_col_tiles, (int)col_tile_off, (const uint16_t*)xa, ld_xa, (const uint16_t*)b, part_dxa, part_db,     \
+                (uint16_t*)dxa, ld_dxa, scale
   if (!lora) lora_bwd_kernel<16, true, false><<<grid, 256, 0, stm>>>(LB_ARGS);
   else if (r == 16) {
     if (quant) lora_bwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(LB_ARGS);
@@ -788,9 +803,9 @@ extern "C" int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_d
 #undef LB_ARGS
   MX_CHECK_LAUNCH("mxfp8_lora_bwd");
   if (lora) {
-    const int64_t total = T * r + N * r;
-    lora_bwd_sum_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stm>>>(
-        part_dxa, (int)(N / 128), part_db, (int)used, (int)T, (int)N, (int)r, scale, (uint16_t*)dxa, ld_dxa, db);
+    const int64_t nx = N == 128 ? 0 : T * r, total = nx + N * r;  // one column chunk: d(xa) already written
+    lora_bwd_sum_kernel<<<(unsigned)((total / 4 + 255) / 256), 256, 0, stm>>>(
+        part_dxa, (int)(N / 128), nx, part_db, (int)used, N * r, (int)r, scale, (uint16_t*)dxa, ld_dxa, db);
     MX_CHECK_LAUNCH("mxfp8_lora_bwd");
   }
   return MXFP8_OK;

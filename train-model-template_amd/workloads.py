@@ -56,6 +56,19 @@ def quant_bytes(rows, cols, dual=False):
     return rows * cols * 4 + s + st
 
 
+def lora_bwd_bytes(T, N, r, quant=True):
+    """Algorithmic HBM bytes of one lora_bwd over dy [T, N] bf16: read dy, xa [T, r], B [N, r]; write d(xa) [T, r]
+    bf16 and dB [N, r] fp32; with quantization also the codes and blocked scales of dy (the partial sums are
+    implementation traffic, not counted)."""
+    by = T * N * 2 + T * r * 2 * 2 + N * r * (2 + 4)
+    return by + (quant_bytes(T, N) - T * N * 2 if quant else 0)
+
+
+def res_lora_bytes(T, N, r):
+    """Algorithmic HBM bytes of one res_lora: read x, y [T, N] and xa [T, r], B [N, r]; write out [T, N] (bf16)."""
+    return T * N * 2 * 3 + (T + N) * r * 2
+
+
 def _outlier_blocks(x, rng):
     """Inject MX edge cases into a bf16-valued fp32 [T, C] tensor in place (config 5)."""
     T, C = x.shape
