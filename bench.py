@@ -163,6 +163,56 @@ def _lora_epilogues(T, K, N, r, dev):
     return out
 
 
+def _grouped_linears(T, K, r, alpha, dev, steps=10):
+    """Attention projections through fused_linear (q|k|v grouped with the concatenated Wᵀ, o_proj deferred into the
+    residual add), forward + backward per step.  q 2048 and k, v 512 outputs for d_model 2048 (GQA shape).  FLOPs
+    counted: the MX GEMMs only (forward x·Wᵀ and backward dx, 2·T·K·N each)."""
+    import torch
+
+    import fused_linear
+    import mxfp8
+    import workloads
+    nq, nkv = K, K // 4
+    m = workloads.build_attn(K, nq, nkv, r, alpha, device=dev, seed=17)
+    mxfp8.enable_mxfp8(m)
+    a = m.model.layers[0].self_attn
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    resid = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    dy = (torch.randn(T, K, device=dev, generator=g) * 1e-2).to(torch.bfloat16)
+    params = [p for p in m.parameters() if p.requires_grad]
+
+    def step():
+        fused_linear.new_step()
+        q, k, v = fused_linear.group_linear(x, [a.q_proj, a.k_proj, a.v_proj])
+        h = q + 0.5 * (k.repeat(1, 4) + v.repeat(1, 4))  # stands in for attention: mixes q, k, v into [T, nq]
+        (o,) = fused_linear.group_linear(h, [a.o_proj], defer=True)
+        out = fused_linear.residual_add(resid, o)
+        out.backward(dy)
+        for p in params:
+            p.grad = None
+        x.grad = resid.grad = None
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    before = fused_linear.STATS.get("lan ngược gộp", 0)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert fused_linear.STATS.get("lan ngược gộp", 0) - before == 2 * steps  # both groups took the fused backward
+    fl = 2 * 2 * T * K * (nq + 2 * nkv) + 2 * 2 * T * nq * K
+    del m, x, resid, dy
+    return {"ms_per_step": round(ms, 4), "MX_GEMM_TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 1),
+            "shape": f"T={T} d_model={K} q={nq} k=v={nkv} o={nq}->{K} r={r}",
+            "note": "fwd+bwd of q|k|v (one group) and o_proj (deferred, residual_add); the q/k/v mix between them is"
+                    " plain torch"}
+
+
 def _copy_calib(dev):
     import torch
     src = torch.ones(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev)
@@ -366,6 +416,7 @@ def main():
         quant, wq_ms = _quantizer(T, K, N, dev)
         line["quantizer"] = quant
         line["lora_epilogues"] = _lora_epilogues(T, K, N, c["r"], dev)
+        line["grouped_linears"] = _grouped_linears(T, K, c["r"], c["alpha"], dev)
         tot = ms + wq_ms * c["layers"]
         line["with_requant"] = {"ms_per_step": round(tot, 4), "TFLOP/s": round(fl / (tot * 1e-3) / 1e12, 2),
                                 "weight_prep_ms_per_layer": round(wq_ms, 4)}

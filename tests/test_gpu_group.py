@@ -1,0 +1,187 @@
+"""Grouped MX linears (fused_linear._Group with mxfp8.lora_bwd and the concatenated Wᵀ GEMM, after
+/root/reference/scripts/fused_linear.py:79-330 and mxfp8.py:360-439) against the CPU oracle: the MX operands are the
+oracle quantizer's codes, dequantized exactly, and every product is taken in float64.  Bar: normwise relative error
+<= 1e-2 and elementwise within 2e-2 of (|value| + the tensor's rms), under the 2e-2 output/gradient tolerance."""
+import pytest
+import torch
+from torch import nn
+
+import fused_linear
+import workloads
+
+pytestmark = pytest.mark.gpu
+
+T, K, NQ, NKV, R, ALPHA, NTHIN = 300, 1024, 1024, 256, 16, 32.0, 16
+
+
+class _Attn(nn.Module):
+    def __init__(self, g):
+        super().__init__()
+
+        def lin(n_out, n_in):
+            m = nn.Linear(n_in, n_out, bias=False)
+            with torch.no_grad():
+                m.weight.copy_(torch.randn(n_out, n_in, generator=g) * 0.03)
+            m.weight.requires_grad_(False)
+            return m
+
+        def lora(n_out, n_in):
+            return workloads.LoraLinear(lin(n_out, n_in), torch.randn(R, n_in, generator=g) * 0.03,
+                                        torch.randn(n_out, R, generator=g) * 0.03, ALPHA)
+
+        self.q_proj, self.k_proj, self.v_proj = lora(NQ, K), lora(NKV, K), lora(NKV, K)
+        self.o_proj = lora(K, NQ)
+        self.thin = lin(NTHIN, K)  # not an MX name: a thin plain linear that joins the S GEMM
+
+
+class _Model(nn.Module):
+    def __init__(self, g):
+        super().__init__()
+        self.model = nn.Module()
+        layer = nn.Module()
+        layer.self_attn = _Attn(g)
+        self.model.layers = nn.ModuleList([layer])
+
+    @property
+    def attn(self):
+        return self.model.layers[0].self_attn
+
+
+def _build(gpu, seed=0):
+    import mxfp8
+    g = torch.Generator().manual_seed(seed)
+    m = _Model(g)
+    for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        getattr(m.attn, name).base_layer.to(dtype=torch.bfloat16)
+    m.attn.thin.to(dtype=torch.bfloat16)
+    m = m.to(gpu)
+    w_cpu = {n: getattr(m.attn, n).base_layer.weight.detach().cpu().clone() for n in ("q_proj", "k_proj", "v_proj",
+                                                                                      "o_proj")}
+    mxfp8.enable_mxfp8(m)
+    fused_linear.new_step()
+    return m, w_cpu
+
+
+def _close(got, want, what):
+    got, want = got.detach().double().cpu(), want.double()
+    rms = want.pow(2).mean().sqrt().item()
+    nrm = ((got - want).norm() / want.norm().clamp_min(1e-30)).item()
+    assert nrm <= 1e-2, (what, nrm)
+    bad = (got - want).abs() > 2e-2 * (want.abs() + rms)
+    assert not bool(bad.any()), (what, int(bad.sum()), (got - want).abs().max().item())
+
+
+def _deq(x2d):
+    from oracle import mx
+    q, s = mx.quant(x2d)
+    return mx.dequant(q, s, x2d.shape[0], x2d.shape[1]).double()
+
+
+def _deq_t(w):
+    """Wᵀ quantized along N (the dx operand), dequantized, as [K, N]."""
+    return _deq(w.t().contiguous())
+
+
+def _bf(t):
+    return t.to(torch.bfloat16).double()
+
+
+def _oracle(m, w_cpu, x, dys, names):
+    """Outputs, dx, dB, dA of the group in float64 from the oracle's MX codes (bf16 rounding of xa = x·Aᵀ and of
+    d(xa) kept, as the path stores them in bf16)."""
+    xd = x.double()
+    xq = _deq(x)
+    outs, dx, grads = [], 0.0, {}
+    dS, Srows = [], []
+    for n, dy in zip(names, dys):
+        mod = getattr(m.attn, n)
+        if n == "thin":
+            W = mod.weight.detach().cpu().double()
+            outs.append(_bf(xd @ W.t()))
+            dS.append(dy.double())
+            Srows.append(W)
+            continue
+        A = mod.lora_A["default"].weight.detach().cpu().to(torch.bfloat16).double()
+        B = mod.lora_B["default"].weight.detach().cpu().to(torch.bfloat16).double()
+        s = mod.scaling["default"]
+        xa = _bf(xd @ A.t())
+        y0 = _bf(xq @ _deq(w_cpu[n]).t())
+        outs.append(y0 + s * xa @ B.t())
+        dyd = dy.double()
+        dx = dx + _deq(dy) @ _deq_t(w_cpu[n]).t()
+        dxa = _bf(s * dyd @ B)
+        grads[n] = (s * dyd.t() @ xa, dxa.t() @ xd)  # dB, dA
+        dS.append(dxa)
+        Srows.append(A)
+    dx = dx + torch.cat(dS, 1) @ torch.cat(Srows, 0)
+    return outs, dx, grads
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_group_qkv_thin_matches_oracle(fused, gpu):
+    import mxfp8
+    m, w_cpu = _build(gpu)
+    a = m.attn
+    names = ["q_proj", "k_proj", "v_proj", "thin"]
+    assert a.q_proj.base_layer.__dict__.get("_mx_cat") is not None and a.q_proj.base_layer._mx_fbwd
+    if not fused:
+        for n in names[:3]:
+            getattr(a, n).base_layer._mx_fbwd = False  # the plain path: one MX GEMM per layer, bf16 adds
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    dys = [(torch.randn(T, n, generator=g) * 0.1).to(torch.bfloat16) for n in (NQ, NKV, NKV, NTHIN)]
+    xg = x.to(gpu).requires_grad_(True)
+    before = fused_linear.STATS.get("lan ngược gộp", 0)
+    outs = fused_linear.group_linear(xg, [getattr(a, n) for n in names])
+    torch.autograd.backward(outs, [d.to(gpu) for d in dys])
+    assert fused_linear.STATS.get("lan ngược gộp", 0) == before + (1 if fused else 0)
+    w_outs, w_dx, w_grads = _oracle(m, w_cpu, x, dys, names)
+    for n, o, w in zip(names, outs, w_outs):
+        _close(o, w, n)
+    _close(xg.grad, w_dx, "dx")
+    for n in names[:3]:
+        mod = getattr(a, n)
+        dB, dA = w_grads[n]
+        assert mod.lora_B["default"].weight.grad.dtype == torch.float32
+        _close(mod.lora_B["default"].weight.grad, dB, n + ".dB")
+        _close(mod.lora_A["default"].weight.grad, dA, n + ".dA")
+    assert mxfp8.group_wt([a.q_proj.base_layer, a.k_proj.base_layer]) is not None
+    assert mxfp8.group_wt([a.k_proj.base_layer, a.q_proj.base_layer]) is None
+
+
+def test_cat_ranges_are_the_layers_own_quantization(gpu):
+    # a column range of the concatenated Wᵀ (codes and cut-out scales) equals quantizing that layer's Wᵀ alone
+    import mxfp8
+    from oracle import mx
+    m, w_cpu = _build(gpu, seed=3)
+    for k, n in enumerate(("q_proj", "k_proj", "v_proj")):
+        base = getattr(m.attn, n).base_layer
+        mat2, sc = mxfp8.wt_of(base)
+        qr, sr = mx.quant_t(w_cpu[n])
+        assert torch.equal(mat2.t().contiguous().view(torch.uint8).cpu(), qr)
+        assert torch.equal(sc.view(torch.uint8).cpu(), sr)
+        qf, sf = mx.quant(w_cpu[n])  # forward codes: rows of the concatenated quantization
+        assert torch.equal(base._mx_w.view(torch.uint8).cpu(), qf) and torch.equal(base._mx_ws.view(torch.uint8).cpu(),
+                                                                                  sf)
+
+
+def test_residual_add_deferred_matches_plain(gpu):
+    # o_proj's output with LoRA added in the residual kernel == the grouped output added to the residual
+    m, _ = _build(gpu, seed=5)
+    o = m.attn.o_proj
+    g = torch.Generator().manual_seed(12)
+    h = torch.randn(T, NQ, generator=g).to(torch.bfloat16).to(gpu)
+    resid = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    (d,) = fused_linear.group_linear(h, [o], defer=True)
+    assert isinstance(d, fused_linear.Deferred)
+    before = fused_linear.STATS.get("residual LoRA", 0)
+    got = fused_linear.residual_add(resid, d)
+    assert fused_linear.STATS.get("residual LoRA", 0) == before + 1
+    (y,) = fused_linear.group_linear(h, [o])
+    want = resid + y
+    # both round y + s·xa·Bᵀ to bf16, then x + that; the r products are summed in another order, so an element may
+    # differ by one step of the intermediate
+    d_ = (got.float() - want.float()).abs()
+    t = torch.maximum(y.float().abs(), got.float().abs())
+    assert bool((d_ <= torch.exp2(torch.floor(torch.log2(t.clamp_min(1e-30)))) * 2 ** -7 * 1.0001 + 1e-30).all())
+    assert (got == want).double().mean().item() >= 0.99

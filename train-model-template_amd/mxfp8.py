@@ -277,6 +277,43 @@ def _leaf_parent(name):
     return parts[-1], ".".join(parts[:-1])
 
 
+# Groups whose Wᵀ is kept once, concatenated along N, so that dx of the whole group is one GEMM over the
+# concatenated dy codes (mxfp8.py:360-366).  Every N is a multiple of 128, so no 32-block straddles two layers and
+# each layer's codes and scales equal its own quantization.  gate/up/down go through fused_mlp instead.
+_CATS = (("in_proj_qkv", "in_proj_z"), ("q_proj", "k_proj", "v_proj"))
+# Linears whose backward takes the grouped path of fused_linear._Group (one read of dy through lora_bwd)
+FUSED_BWD = {"in_proj_qkv", "in_proj_z", "q_proj", "k_proj", "v_proj", "o_proj", "out_proj"}
+
+
+class _Cat:
+    """Wᵀ of a group concatenated along N: codes [K, ΣN] quantized along ΣN with their blocked scales, and the
+    MX-tiled copy the whole-group GEMM reads (mxfp8.py:369-395)."""
+
+    def __init__(self, qt, st, ns):
+        self.qt, self.st = qt, st
+        self.qt_tl = tile_codes(qt)
+        self.offs = [0]
+        for n in ns:
+            self.offs.append(self.offs[-1] + n)
+        self.n = len(ns)
+        self._sub = {}
+
+    def range(self, a, b):
+        """(mat2 [N_a+..+N_{b-1}, K] column-major view, scales) of layers a..b-1, the torch._scaled_mm form.  The
+        scales of a column range are its 128x4 tiles of every 128-row block, cut out contiguously on first use:
+        byte for byte the quantization of that range alone."""
+        c0, c1 = self.offs[a], self.offs[b]
+        mat2 = self.qt[:, c0:c1].t()
+        if (a, b) == (0, self.n):
+            return mat2, self.st
+        sc = self._sub.get((a, b))
+        if sc is None:
+            K, ntot = self.qt.shape
+            blk = self.st.view(torch.uint8).view(_cdiv(K, 128), ntot // 128, 512)
+            sc = self._sub[(a, b)] = blk[:, c0 // 128:c1 // 128].contiguous().view(-1).view(E8)
+        return mat2, sc
+
+
 def is_mx(lin):
     return getattr(lin, "_mx_w", None) is not None
 
@@ -284,9 +321,12 @@ def is_mx(lin):
 def mx_wt(lin):
     """(fp8 Wᵀ [K, N] as the B operand of dx = dy @ W, scales).  For a gate/up pair: a column view of W_guᵀ
     (row stride 2N) plus that half's scale tiles cut out contiguously, made on first use and kept
-    (mxfp8.py:402-415)."""
+    (mxfp8.py:402-415); for a layer of a concatenated group, its column range of the group's Wᵀ."""
     gu = lin.__dict__.get("_mx_gu")
     if gu is None:
+        if "_mx_cat" in lin.__dict__:
+            m, sc = wt_of(lin)
+            return m.t(), sc
         return lin._mx_wt, lin._mx_wts
     hold, i = gu
     if hold.half_t[i] is None:
@@ -300,8 +340,39 @@ def mx_wt(lin):
 def wt_of(lin):
     """(mat2, scale) of dy @ W in torch._scaled_mm form: mat2 = Wᵀ codes as an [N, K] column-major view
     (mxfp8.py:418-426)."""
+    c = lin.__dict__.get("_mx_cat")
+    if c is not None:
+        return c[0].range(c[1], c[1] + 1)
     wt, s = mx_wt(lin)
     return wt.t(), s
+
+
+def group_wt(lins):
+    """(mat2 [ΣN, K], scale) of dx = [dy_1|dy_2|..] @ [W_1; W_2; ..] for consecutive layers of one concatenated
+    group (or a single layer); None when no concatenated copy fits (mxfp8.py:429-439)."""
+    c = lins[0].__dict__.get("_mx_cat")
+    if c is None:
+        return wt_of(lins[0]) if len(lins) == 1 else None
+    cat, k = c
+    for d, lin in enumerate(lins):
+        if lin.__dict__.get("_mx_cat") != (cat, k + d):
+            return None
+    return cat.range(k, k + len(lins))
+
+
+def group_operand(lins):
+    """(B operand [K, ΣN] of mx_mm, scales, layout bit) for dx of `lins` (group_wt): the MX-tiled copy when the
+    range is a whole concatenated group, else the row-major column view (row stride = the group's ΣN)."""
+    g = group_wt(lins)
+    if g is None:
+        return None
+    mat2, sc = g
+    c = lins[0].__dict__.get("_mx_cat")
+    if c is not None and c[1] == 0 and len(lins) == c[0].n:
+        return c[0].qt_tl, sc, 2
+    if c is None and "_mx_wt_tl" in lins[0].__dict__:
+        return lins[0]._mx_wt_tl, sc, 2
+    return mat2.t(), sc, 0
 
 
 FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
@@ -319,8 +390,24 @@ def enable_mxfp8(model):
         assert w.is_cuda and w.shape[0] % 128 == 0 and w.shape[1] % 128 == 0, w.shape
         leaf, parent = _leaf_parent(name)
         fam.setdefault(parent, {})[leaf] = lin
-    paired = set()
+    in_cat, paired = set(), set()
     for d in fam.values():
+        for names in _CATS:
+            if all(k in d for k in names):
+                # one read of the concatenated weight gives every layer's forward codes (rows of q) and the
+                # group's Wᵀ along ΣN
+                grp = [d[k] for k in names]
+                w = torch.cat([lin.weight.data for lin in grp]).to(torch.bfloat16)  # [ΣN, K]
+                q, sq, qt, st = quant_both(w)
+                del w
+                cat = _Cat(qt, st, [lin.weight.shape[0] for lin in grp])
+                tile_b = (q.shape[1] // 128) * 512  # scale bytes of one 128-row tile row
+                for k, lin in enumerate(grp):
+                    c0, c1 = cat.offs[k], cat.offs[k + 1]
+                    lin._mx_w, lin._mx_ws = q[c0:c1], sq[c0 // 128 * tile_b:c1 // 128 * tile_b]
+                    lin._mx_w_tl = tile_codes(lin._mx_w)
+                    lin._mx_cat = (cat, k)
+                    in_cat.add(id(lin))
         gb, ub = d.get("gate_proj"), d.get("up_proj")
         if FUSE_GU and gb is not None and ub is not None and gb.weight.shape == ub.weight.shape:
             w = torch.cat([gb.weight.data, ub.weight.data]).to(torch.bfloat16)  # [2N, K]
@@ -336,16 +423,16 @@ def enable_mxfp8(model):
                 paired.add(id(lin))
     for name, lin in lins:
         w = lin.weight.data
-        if id(lin) not in paired:
+        if id(lin) not in paired and id(lin) not in in_cat:
             lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(w.to(torch.bfloat16))
             lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
-        lin._mx_fbwd = False  # the grouped LoRA backward of the non-MLP linears is not part of this library
+        lin._mx_fbwd = _leaf_parent(name)[0] in FUSED_BWD
         lin._bf16_cpu = w.to("cpu", copy=True)
         lin.weight.data = torch.empty((0,), dtype=w.dtype, device=w.device)
         lin.forward = types.MethodType(_forward, lin)
     torch.cuda.empty_cache()
     print(f"MXFP8: {len(lins)} frozen linears on MX GEMMs (bf16 weights moved to host memory;"
-          f" {len(paired) // 2} gate/up pairs shared)", flush=True)
+          f" {len(in_cat)} with a concatenated group Wᵀ, {len(paired) // 2} gate/up pairs shared)", flush=True)
     return len(lins)
 
 

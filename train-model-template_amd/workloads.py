@@ -231,6 +231,38 @@ class MLPStack(torch.nn.Module):
         return self.model.layers
 
 
+class AttnProjections(torch.nn.Module):
+    """q_proj / k_proj / v_proj / o_proj of an attention block as PEFT-shaped LoRA linears (frozen bf16 base
+    weights N(0, 0.02), fp32 LoRA A/B N(0, 0.02)), the grouped MX linears of fused_linear.  Seeded from `seed`."""
+
+    def __init__(self, K, nq, nkv, r, alpha, seed=0):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+
+        def lora(n_out, n_in):
+            base = torch.nn.Linear(n_in, n_out, bias=False)
+            with torch.no_grad():
+                base.weight.copy_(torch.randn(n_out, n_in, generator=g) * 0.02)
+            base.weight.requires_grad_(False)
+            base.to(torch.bfloat16)
+            return LoraLinear(base, torch.randn(r, n_in, generator=g) * 0.02, torch.randn(n_out, r, generator=g) * 0.02,
+                              alpha)
+
+        self.q_proj, self.k_proj, self.v_proj = lora(nq, K), lora(nkv, K), lora(nkv, K)
+        self.o_proj = lora(K, nq)
+
+
+def build_attn(K, nq, nkv, r, alpha, device="cuda", seed=0):
+    """A one-layer decoder-shaped module ('model.layers.0.self_attn.q_proj...') holding AttnProjections, the path
+    mxfp8.enable_mxfp8 walks."""
+    m = torch.nn.Module()
+    m.model = torch.nn.Module()
+    layer = torch.nn.Module()
+    layer.self_attn = AttnProjections(K, nq, nkv, r, alpha, seed)
+    m.model.layers = torch.nn.ModuleList([layer])
+    return m.to(device)
+
+
 def build_model(cfg, T=None, layers=1, device="cuda"):
     """(model, inputs) for `layers` independent seeded layers of configuration cfg, bf16 frozen weights and
     fp32 LoRA parameters on `device`; inputs of layer 0 (x, dy) are returned on the CPU (the other layers'
