@@ -214,6 +214,16 @@ int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q,
 int mxfp8_res_lora(const void* x, const void* y, const void* xa, int64_t ld_xa, const void* b, int64_t T, int64_t N,
                    int64_t r, float scale, void* out, void* stream);
 
+/*
+ * h[i] = bf16(silu(g[i]) * u[i]) over n bf16 values (n % 8 == 0, 16-byte aligned), silu(g) = g * sigmoid(g) with the
+ * sigmoid of the fused MLP kernels.  Replaces _SWIGLU, the compiled silu(g) * u of the unfused MLP path
+ * (/root/reference/scripts/shared_prefix.py:172-197).
+ */
+int mxfp8_swiglu(const void* g, const void* u, int64_t n, void* h, void* stream);
+
+/* Backward of mxfp8_swiglu: du = bf16(dh * silu(g)), dg = bf16(dh * u * sig * (g * (1 - sig) + 1)). */
+int mxfp8_swiglu_bwd(const void* g, const void* u, const void* dh, int64_t n, void* dg, void* du, void* stream);
+
 /* Row chunks mxfp8_lora_bwd uses for dy [T, N] (part_db holds chunks * N * r floats); 0 for invalid sizes. */
 int64_t mxfp8_lora_bwd_chunks(int64_t T, int64_t N);
 

@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 22, names
+    assert len(names) == 24, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -80,6 +80,9 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.mxfp8_lora_tn(p, 4, 96, 96, p, 16, 1, ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), 1.0, 0, 0, p,
                              None) == -1
     assert lib.mxfp8_lora_tn_chunks(10752, 2048) > 0 and lib.mxfp8_lora_tn_chunks(10752, 100) == 0
+    # SwiGLU: n % 8, aligned
+    assert lib.mxfp8_swiglu(p, p, 12, p, None) == -1
+    assert lib.mxfp8_swiglu_bwd(p, p, p, 16, p, ctypes.c_void_p(18), None) == -1
     # residual LoRA epilogue: N % 128, r in {16, 32}
     assert lib.mxfp8_res_lora(p, p, p, 16, p, 4, 100, 16, 1.0, p, None) == -1
     assert lib.mxfp8_res_lora(p, p, p, 16, p, 4, 128, 8, 1.0, p, None) == -1

@@ -39,6 +39,8 @@ SIGNATURES = {
     "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_res_lora": [_ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _f32, _ptr, _ptr],
     "mxfp8_lora_tn_chunks": [_i64, _i64],
+    "mxfp8_swiglu": [_ptr, _ptr, _i64, _ptr, _ptr],
+    "mxfp8_swiglu_bwd": [_ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr],
     "mxfp8_lora_bwd_chunks": [_i64, _i64],
     "mxfp8_lora_bwd": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _i64,
                        _ptr, _ptr, _ptr],
@@ -211,6 +213,15 @@ def res_lora(x, y, xa, b, out, scale):
     T, N = x.shape
     call("mxfp8_res_lora", _p(x), _p(y), _p(xa), xa.stride(0), _p(b), T, N, b.shape[1], float(scale), _p(out),
          like=x)
+
+
+def swiglu(g, u, h):
+    """h = bf16(silu(g) · u) elementwise (bf16, contiguous, numel % 8 == 0)."""
+    call("mxfp8_swiglu", _p(g), _p(u), g.numel(), _p(h), like=g)
+
+
+def swiglu_bwd(g, u, dh, dg, du):
+    call("mxfp8_swiglu_bwd", _p(g), _p(u), _p(dh), g.numel(), _p(dg), _p(du), like=g)
 
 
 def lora_bwd_chunks(T, N):

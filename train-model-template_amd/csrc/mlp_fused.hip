@@ -32,12 +32,6 @@ namespace {
 
 __device__ __forceinline__ int tile_col(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
-// sigmoid(g) = 1 / (1 + exp(-g)) with the hardware exp2 and reciprocal (about 1 ulp each; the reference's
-// Triton fp32 division is approximate as well); silu(g) = g * sigmoid(g).  exp(-g) overflowing to +inf
-// gives sigmoid 0 and silu -0, as g / (exp(-g) + 1) does.
-__device__ __forceinline__ float fast_sigmoid(float g) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
-}
 
 
 // 8 bf16 of row `p` at columns base + {lg*4 + 0..3} and base + 8 + {lg*4 + 0..3} (one k-step of the permuted

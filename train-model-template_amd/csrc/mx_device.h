@@ -212,6 +212,13 @@ __device__ __forceinline__ v16f lora_pi(const v8bf* wf, const v8bf* xf) {
   return d;
 }
 
+// sigmoid(g) = 1 / (1 + exp(-g)) with the hardware exp2 and reciprocal (about 1 ulp each; the reference's
+// Triton fp32 division is approximate as well); silu(g) = g * sigmoid(g).  exp(-g) overflowing to +inf
+// gives sigmoid 0 and silu -0, as g / (exp(-g) + 1) does.
+__device__ __forceinline__ float fast_sigmoid(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
 // ---- LDS DMA (global_load_lds_dwordx4) and explicit memory-counter waits
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(lds_ptr_t)p; }

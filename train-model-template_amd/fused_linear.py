@@ -65,6 +65,26 @@ def _vec_ok(t):
     return t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
 
 
+def _rp(n):
+    """Padded row count of S / column count of dS for the native rank-r kernels (16, 32 or 64), None above 64."""
+    for rp in (16, 32, 64):
+        if n <= rp:
+            return rp
+    return None
+
+
+def _native_ok(x2, dt, n):
+    """The thin GEMMs x·Sᵀ, dSᵀ·x and dS·S run on the library's kernels (mxfp8_lora_nt / mxfp8_lora_tn / the MX
+    GEMM epilogue) when the math is bf16 on the GPU, S has at most 64 rows and d_model % 256 == 0."""
+    return (x2.is_cuda and dt == torch.bfloat16 and _rp(n) is not None and x2.shape[0] > 0 and x2.shape[1] % 256 == 0
+            and _vec_ok(x2))
+
+
+def _s_pad(S, key, rp):
+    """S zero-padded to rp rows (cached per step with the S it pads)."""
+    return _cast(key + ("pad", rp), lambda: torch.cat([S, S.new_zeros(rp - S.shape[0], S.shape[1])]))
+
+
 def _base_mm(base, x2, dt, q, T):
     """x2 @ Wᵀ of a base weight: the MX GEMM when enable_mxfp8 covers the layer (q = the group's tiled MX codes of
     x2), else a bf16 GEMM (fused_linear.py:72-76)."""
@@ -103,9 +123,17 @@ class _Group(torch.autograd.Function):
                 rows.append(base.weight)
                 thin.append((i, off, base.weight.shape[0]))
                 off += base.weight.shape[0]
-        S = _cast((tuple(id(r) for r in rows), dt),
-                  lambda: torch.cat([r.detach().to(dt) for r in rows])) if rows else None
-        xS = x2 @ S.t() if rows else None
+        skey = (tuple(id(r) for r in rows), dt)
+        S = _cast(skey, lambda: torch.cat([r.detach().to(dt) for r in rows])) if rows else None
+        xS = None
+        if rows and _native_ok(x2, dt, off):
+            # bf16(x·Sᵀ) from one read of x (the extra columns of the padded product are zero)
+            import _native
+            rp = _rp(off)
+            xS = torch.empty((T, rp), dtype=dt, device=x2.device)
+            _native.lora_nt(x2, _s_pad(S, skey, rp), xS)
+        elif rows:
+            xS = x2 @ S.t()
         outs = [None] * len(parts)
         thin_ids = {i for i, _, _ in thin}
         lora_of = {i: (j, o, r, s) for j, (i, o, r, s) in enumerate(lora)}
@@ -142,6 +170,7 @@ class _Group(torch.autograd.Function):
             outs[i] = xS[:, o:o + n].contiguous()
         ctx.save_for_backward(x2, xS, S, *Bs)
         ctx.meta = (parts, lora, thin, lead, K, dt, x.dtype)
+        ctx.skey = skey
         return tuple(y.view(*lead, y.shape[-1]) for y in outs)
 
     @staticmethod
@@ -247,7 +276,14 @@ def _fused_backward(ctx, x2, xS, S, Bs, flat, plan, need_x):
     lora_of = {i: (j, o, r, s) for j, (i, o, r, s) in enumerate(lora)}
     n_act = sum(r for _, _, r, _ in lora)
     n_cols = n_act + (sum(n for _, _, n in thin) if need_x else 0)
-    dS = torch.empty((T, n_cols), dtype=dt, device=dev) if n_cols else None
+    plain = [i for i, p in enumerate(parts) if not _mx(p[0]) and i not in {t[0] for t in thin}]
+    # dS·S rides in the dx GEMM's epilogue and dA = dSᵀ·x2 runs on the token-reduction kernel when dS fits a
+    # padded width of 16/32/64 (zero columns) and no plain bf16 linear has to be added into dx first
+    native = n_cols > 0 and _native_ok(x2, dt, n_cols) and not plain
+    width = _rp(n_cols) if native else n_cols
+    dS = torch.empty((T, width), dtype=dt, device=dev) if n_cols else None
+    if native and width > n_cols:
+        dS[:, n_cols:].zero_()
     grads = [None] * (2 * len(lora))
     q = s_buf = None
     if need_x:
@@ -284,18 +320,27 @@ def _fused_backward(ctx, x2, xS, S, Bs, flat, plan, need_x):
     dx = None
     if need_x:
         wq, ws, lay = wt
-        dx = mxfp8.mx_mm(q, s_buf.view(mxfp8.E8), wq, ws, layout=lay)
-        del q, s_buf
-        thin_ids = {i for i, _, _ in thin}
-        for i, (base, A, B, s) in enumerate(parts):  # plain bf16 linears (neither MX nor thin)
-            if i not in thin_ids and not _mx(base):
-                dx.addmm_(flat[i], base.weight.to(dt))
         for i, o, n in thin:
             dS[:, o:o + n].copy_(flat[i])
-        if dS is not None:
-            dx.addmm_(dS, S)
+        if native:
+            # bf16(bf16(MX GEMM) + dS·S): the dx.addmm_(dS, S) of the reference in the GEMM epilogue
+            St = _cast(ctx.skey + ("padT", width), lambda: _s_pad(S, ctx.skey, width).t().contiguous())
+            dx = mxfp8.mx_mm(q, s_buf.view(mxfp8.E8), wq, ws, layout=lay, lora=(dS, St), alpha=1.0)
+        else:
+            dx = mxfp8.mx_mm(q, s_buf.view(mxfp8.E8), wq, ws, layout=lay)
+            for i in plain:  # plain bf16 linears (neither MX nor thin)
+                dx.addmm_(flat[i], parts[i][0].weight.to(dt))
+            if dS is not None:
+                dx.addmm_(dS, S)
+        del q, s_buf
     if lora:
-        dA = dS[:, :n_act].t() @ x2
+        if native:
+            import _native
+            dA = torch.empty((width, K), dtype=dt, device=dev)
+            part = torch.empty(_native.lora_tn_chunks(T, K) * width * K, dtype=torch.float32, device=dev)
+            _native.lora_tn(x2, dS, dA, part)  # bf16(dSᵀ·x2)
+        else:
+            dA = dS[:, :n_act].t() @ x2
         for j, (i, o, r, s) in enumerate(lora):
             grads[2 * j] = dA[o:o + r]
     STATS["lan ngược gộp"] = STATS.get("lan ngược gộp", 0) + 1
