@@ -292,152 +292,217 @@ __global__ __launch_bounds__(256) void res_lora_kernel(const uint16_t* __restric
 //           as fp32 partial sums: part_dxa [N / 128, T, R] over each 128-column chunk (or d(xa) itself when N is
 //           one chunk), part_db [rs, N, R] over each row chunk (added in order by lora_bwd_sum_kernel).
 // Grid (rs, N / 128), 4 waves: the workgroup owns rows [blockIdx.x * chunk, + chunk) (clipped at Tpad, a multiple
-// of 128, so the padded rows of the last scale tiles get scale 0) and 128 columns, and streams 32-row blocks of dy
-// (32 x 256 B, the same chunk swizzle as quant_lora_kernel) and of xa (32 rows x 2R B) through an LDS ring.
-// Wave w takes columns 32w..32w+31: lane l reads 16 contiguous values of row l%32, quantizes them with lane l^32,
-// and feeds them to the d(xa) MFMA (its B operand fragments gathered once per workgroup); the 4 waves' d(xa)
-// products are added in LDS in a fixed order.  For dB the wave writes its 32 x 32 dy tile to LDS (zero past T) and
-// reads it back transposed (ds_read_b64_tr_b16), with xa read transposed from the ring: 16x16x32 MFMAs over the
-// block's 32 rows, accumulated in registers over the row chunk.
+// of 128, so the padded rows of the last scale tiles get scale 0) and 128 columns.  Each wave works alone on the
+// 32-row blocks w, w + 4, ... of that range, all 128 columns: no barrier inside the loop, and d(xa) of a block is
+// complete in one wave.  A block is loaded row-contiguously (16 lanes per 256-byte row piece, the next block's
+// loads in flight during this one's work), stored into the wave's own LDS tile with the 16-byte chunk swizzle
+// c ^ (row % 16) and read back with lane l holding 16 contiguous values of row l % 32 per 32-column group g: the
+// quantizer takes them with partner lane l ^ 32, the d(xa) MFMA takes them as its B operand (A = B's rows, gathered
+// once).  For dB each group's 32 x 32 tile goes through a second per-wave tile and is read back transposed
+// (ds_read_b64_tr_b16), with xa, also staged per wave, read transposed: 16x16x32 MFMAs accumulate dB in registers
+// over the wave's blocks; the four waves' dB are added in LDS in a fixed order at the end.
 template <int R, bool kQuant, bool kLora>
-__global__ __launch_bounds__(256) void lora_bwd_kernel(const uint16_t* __restrict__ dy, int64_t ld_dy, int T, int N,
-                                                       int Tpad, int chunk, uint8_t* __restrict__ q, int64_t ld_q,
-                                                       uint8_t* __restrict__ s, int64_t s_col_tiles, int col_tile_off,
-                                                       const uint16_t* __restrict__ xa, int64_t ld_xa,
-                                                       const uint16_t* __restrict__ B, float* __restrict__ part_dxa,
-                                                       float* __restrict__ part_db, uint16_t* __restrict__ dxa,
-                                                       int64_t ld_dxa, float scale) {
-  // Ring depth: stores issued inside the loop count in the same in-order vmcnt as the DMAs, so the wait for block b
-  // also covers the DMAs issued before the last stores; a deeper ring keeps about two blocks in flight regardless.
-  constexpr int kStages = R == 16 ? 6 : 5, kTileB = 32 * 256, kXaB = kLora ? 32 * R * 2 : 0;
-  constexpr int kStageB = kTileB + kXaB;
-  constexpr int kXaDma = kLora ? R / 16 : 1;  // 1 or 2 distinct 1 KB pieces; every wave issues one (copies repeat)
-  constexpr int kDma = 2 + (kLora ? 1 : 0);
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
-  __shared__ __attribute__((aligned(16))) uint16_t trt[4][32 * kTrLd];  // per-wave dy tile for dB
-  __shared__ float red[4][32][R + 1];                                     // per-wave d(xa) products
+__global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __restrict__ dy, int64_t ld_dy, int T,
+                                                          int N, int Tpad, int chunk, uint8_t* __restrict__ q,
+                                                          int64_t ld_q, uint8_t* __restrict__ s, int64_t s_col_tiles,
+                                                          int col_tile_off, const uint16_t* __restrict__ xa,
+                                                          int64_t ld_xa, const uint16_t* __restrict__ B,
+                                                          float* __restrict__ part_dxa, float* __restrict__ part_db,
+                                                          uint16_t* __restrict__ dxa, int64_t ld_dxa, float scale) {
+  constexpr int kTileB = 32 * 256;         // one block of one wave: 32 rows x 128 bf16
+  constexpr int kRedB = kLora ? 4 * 128 * 17 * 4 : 0;  // end-of-kernel dB exchange: [wave][column][16 ρ + 1]
+  constexpr int kXaL = kLora ? R / 16 : 0;  // 16-byte xa pieces per lane per block
+  __shared__ __attribute__((aligned(16))) uint8_t tiles[(4 * kTileB > kRedB) ? 4 * kTileB : kRedB];
+  __shared__ __attribute__((aligned(16))) uint16_t trt[4][32 * kTrLd];        // per-wave dy tile for dB
+  __shared__ __attribute__((aligned(16))) uint16_t xat[4][kLora ? 32 * R : 8];  // per-wave xa tile
+  __shared__ __attribute__((aligned(16))) uint8_t qtile[4][kQuant ? 32 * 128 : 16];  // per-wave block of codes
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int r0 = blockIdx.x * chunk, r1 = min(r0 + chunk, Tpad);
   const int c0 = blockIdx.y * 128;
   const int row = lane & 31;
-  // DMA sources for the block at rows rb: dy rows 4j + lane/16 (j = 2w, 2w + 1), logical chunk (lane%16)^(row%16)
-  const int pc = lane & 15;
-  int xr[2], xc[2];
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    xr[jj] = 4 * (2 * w + jj) + (lane >> 4);
-    xc[jj] = c0 + (pc ^ (xr[jj] & 15)) * 8;
+  const int nblk = (r1 - r0) / 32;
+  uint8_t* tile = tiles + w * kTileB;
+  // loads of a block: piece j covers rows 4j + lane/16, 16-byte chunk lane%16 of the row's 256 bytes
+  const int pc = lane & 15, prow = lane >> 4;
+  // the wave's next two blocks, in flight (register sets ca and cb): dy pieces 0..7 and the xa pieces
+  uint4 ca0, ca1, ca2, ca3, ca4, ca5, ca6, ca7, cax0, cax1;
+  uint4 cb0, cb1, cb2, cb3, cb4, cb5, cb6, cb7, cbx0, cbx1;
+  constexpr int xper = R / 8;  // 16-byte parts per xa row
+  const uint16_t* dyc = dy + c0 + pc * 8;
+  const uint16_t* xac = xa + (lane % xper) * 8;
+#define LB_FETCH(b, P)                                                                                    \
+  {                                                                                                       \
+    const int rb_ = r0 + 32 * (b);                                                                        \
+    P##0 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 0 + prow, T - 1) * ld_dy);            \
+    P##1 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 4 + prow, T - 1) * ld_dy);            \
+    P##2 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 8 + prow, T - 1) * ld_dy);            \
+    P##3 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 12 + prow, T - 1) * ld_dy);           \
+    P##4 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 16 + prow, T - 1) * ld_dy);           \
+    P##5 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 20 + prow, T - 1) * ld_dy);           \
+    P##6 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 24 + prow, T - 1) * ld_dy);           \
+    P##7 = *reinterpret_cast<const uint4*>(dyc + (int64_t)min(rb_ + 28 + prow, T - 1) * ld_dy);           \
+    if constexpr (kXaL >= 1)                                                                              \
+      P##x0 = *reinterpret_cast<const uint4*>(xac + (int64_t)min(rb_ + lane / xper, T - 1) * ld_xa);     \
+    if constexpr (kXaL >= 2)                                                                              \
+      P##x1 = *reinterpret_cast<const uint4*>(xac + (int64_t)min(rb_ + 64 / xper + lane / xper, T - 1) * ld_xa); \
   }
-  // xa piece of this wave: piece w % kXaDma, lane i -> row (1024 / (2R)) * piece + i / (2R / 16), 16-B part
-  const int xpiece = w % kXaDma, xper = 2 * R / 16;  // 16-byte parts per xa row
-  const int xar = xpiece * (64 / xper) + lane / xper, xac = (lane % xper) * 8;
-  const uint32_t lds0 = lds_addr(lds);
-  auto issue = [&](int rb, int slot) {
-    const uint32_t st = lds0 + slot * kStageB;
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-      dma16(dy + (int64_t)min(rb + xr[jj], T - 1) * ld_dy + xc[jj], st + (2 * w + jj) * 1024);
-    if constexpr (kLora) dma16(xa + (int64_t)min(rb + xar, T - 1) * ld_xa + xac, st + kTileB + xpiece * 1024);
-  };
-  // d(xa) A operand: lane l holds B[n, ρ] (ρ = l % 32 < R, else 0) at the lane's columns n (both MFMA k steps)
-  v8bf bt[2];
+  // d(xa) A operand: lane l holds B[n, ρ] (ρ = l % 32 < R, else 0) at the lane's columns n of group g, k step ks
+  v8bf bt[4][2];
   if constexpr (kLora) {
     const int rho = row;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      v8s16 v;
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int n = c0 + 32 * w + 16 * lg + 8 * ks + e;
-        v[e] = (short)B[(int64_t)n * R + (rho < R ? rho : 0)];
+      for (int ks = 0; ks < 2; ++ks) {
+        v8s16 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int n = c0 + 32 * g + 16 * lg + 8 * ks + e;
+          v[e] = (short)B[(int64_t)n * R + (rho < R ? rho : 0)];
+        }
+        if (rho >= R) v = v8s16{};
+        bt[g][ks] = __builtin_bit_cast(v8bf, v);
       }
-      if (rho >= R) v = v8s16{};
-      bt[ks] = __builtin_bit_cast(v8bf, v);
-    }
-    wait_vmcnt<0>();  // so that no wait for these loads lands inside the DMA loop
   }
-  const int cx = 4 * w + 2 * lg;  // the lane's first logical 16-byte chunk of a block row
-  const int sx0 = (cx ^ (row & 15)) << 4, sx1 = ((cx + 1) ^ (row & 15)) << 4;
-  v4f db[2][R / 16];
+  v4f db[4][2][R / 16];
 #pragma unroll
-  for (int jh = 0; jh < 2; ++jh)
-#pragma unroll
-    for (int h = 0; h < R / 16; ++h) db[jh][h] = v4f{};
-  const int nblk = (r1 - r0) / 32;
-#pragma unroll
-  for (int j = 0; j < kStages - 1; ++j) issue(r0 + 32 * min(j, nblk - 1), j);
-  int slot = 0;
-  for (int b = 0; b < nblk; ++b) {
-    const int rb = r0 + 32 * b;
-    wait_vmcnt<(kStages - 2) * kDma>();
-    lds_barrier();  // block b landed for every wave; every wave is done with block b - 1's slot and red[]
-    issue(r0 + 32 * min(b + kStages - 1, nblk - 1), slot == 0 ? kStages - 1 : slot - 1);
-    const uint8_t* st = lds + slot * kStageB;
-    const uint4 a = *reinterpret_cast<const uint4*>(st + row * 256 + sx0);
-    const uint4 c = *reinterpret_cast<const uint4*>(st + row * 256 + sx1);
-    uint32_t v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-    const int m = rb + row;
-    const bool live = m < T;
-    const int mc = live ? m : T - 1;
-    if constexpr (kQuant)
-      quant16(v, lane, m, live, q, mc, ld_q, false, (int64_t)col_tile_off * 128 + c0 + 32 * w + 16 * lg, s,
-              s_col_tiles);
-    if constexpr (kLora) {
-      // d(xa) partial over this wave's 32 columns: D[ρ][t] (lane: t = l % 32, ρ = tile_col(i, l))
-      v16f p = v16f{};
-      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bt[0], as_bf8(a), p, 0, 0, 0);
-      p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bt[1], as_bf8(c), p, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int rr = (i >> 2) * 8 + lg * 4 + (i & 3);
-        if (rr < R) red[w][row][rr] = p[i];
-      }
-      // dB: D[n][ρ] += Σ_t dy[t, n] xa[t, ρ] over the block's rows (rows past T add nothing)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = live ? v[k] : 0u;
-      tr_store(trt[w], lane, v);
-      const uint16_t* xt = reinterpret_cast<const uint16_t*>(st + kTileB);
-#pragma unroll
-      for (int jh = 0; jh < 2; ++jh) {
-        const v8bf ad = tr_operand(trt[w], jh * 16, lane);
-#pragma unroll
-        for (int h = 0; h < R / 16; ++h) {
-          // rows past T hold row T - 1's xa: their dy is zero, so they add nothing
-          const v8bf xb = tr_operand_ld(xt, R, h * 16, lane);
-          db[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, xb, db[jh][h], 0, 0, 0);
-        }
-      }
-      lds_barrier();
-      if (gridDim.y == 1) {  // one column chunk: the sum is final (mxfp8.py:168-172, DXA_DIRECT)
-        for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
-          const int tt = idx / R, rr = idx % R;
-          const float sum = ((red[0][tt][rr] + red[1][tt][rr]) + red[2][tt][rr]) + red[3][tt][rr];
-          if (rb + tt < T) dxa[(int64_t)(rb + tt) * ld_dxa + rr] = bf(sum * scale);
-        }
-      } else {
-        float* dst = part_dxa + ((int64_t)blockIdx.y * T + rb) * R;
-        for (int idx = threadIdx.x; idx < 32 * R; idx += 256) {
-          const int tt = idx / R, rr = idx % R;
-          if (rb + tt < T) dst[idx] = ((red[0][tt][rr] + red[1][tt][rr]) + red[2][tt][rr]) + red[3][tt][rr];
-        }
-      }
-    }
-    slot = slot + 1 == kStages ? 0 : slot + 1;
-  }
-  wait_vmcnt<0>();
-  if constexpr (kLora) {
-    // lane l: ρ = 16 h + l % 16, n = c0 + 32 w + 16 jh + (l / 16) * 4 + i
+  for (int g = 0; g < 4; ++g)
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
-      for (int h = 0; h < R / 16; ++h)
+      for (int h = 0; h < R / 16; ++h) db[g][jh][h] = v4f{};
+  const bool direct = gridDim.y == 1;
+  auto lb_block = [&](const int rb) __attribute__((always_inline)) {
+    const int m = rb + row;
+    const bool live = m < T;
+    const int mc = live ? m : T - 1;
+    v16f p = v16f{};
+    uint32_t epack = 0;  // the row's four scale bytes (groups 0..3), 0 past T
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = c0 + 32 * w + 16 * jh + (lane >> 4) * 4 + i;
-          part_db[((int64_t)blockIdx.x * N + n) * R + h * 16 + (lane & 15)] = db[jh][h][i];
+    for (int g = 0; g < 4; ++g) {
+      const int cx = 4 * g + 2 * lg;  // the lane's first logical 16-byte chunk of the row
+      const uint4 a = *reinterpret_cast<const uint4*>(tile + row * 256 + ((cx ^ (row & 15)) << 4));
+      const uint4 c = *reinterpret_cast<const uint4*>(tile + row * 256 + (((cx + 1) ^ (row & 15)) << 4));
+      uint32_t v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+      if constexpr (kQuant) {
+        // codes into the wave's code tile (row stride 128 B, 16-byte chunk k at k ^ (row % 8)); scales by row
+        uint4 cw;
+        const uint32_t e = quant16_codes(v, cw);
+        epack |= (live ? e : 0u) << (8 * g);
+        *reinterpret_cast<uint4*>(qtile[w] + row * 128 + (((2 * g + lg) ^ (row & 7)) << 4)) = cw;
+      }
+      if constexpr (kLora) {
+        // d(xa) over the group's 32 columns, into D[ρ][t] (lane: t = l % 32, ρ = 8 (i / 4) + 4 (l / 32) + i % 4)
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bt[g][0], as_bf8(a), p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bt[g][1], as_bf8(c), p, 0, 0, 0);
+        // dB: D[n][ρ] += Σ_t dy[t, n] xa[t, ρ] over the block's rows (rows past T add nothing)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = live ? v[k] : 0u;
+        tr_store(trt[w], lane, v);
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh) {
+          const v8bf ad = tr_operand(trt[w], jh * 16, lane);
+#pragma unroll
+          for (int h = 0; h < R / 16; ++h) {
+            // rows past T hold row T - 1's xa: their dy is zero, so they add nothing
+            const v8bf xb = tr_operand_ld(xat[w], R, h * 16, lane);
+            db[g][jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, xb, db[g][jh][h], 0, 0, 0);
+          }
         }
+      }
+    }
+    if constexpr (kQuant) {
+      // the block's codes as whole 128-byte row pieces: lane l takes row 8 j + l / 8, chunk l % 8 (rows past T hold
+      // row T - 1's codes and store them again); the four scale bytes of a row are one word of the 128 x 4 tile
+      // (lanes l and l + 32 store the same word)
+      uint8_t* qrow = q + (int64_t)col_tile_off * 128 + c0 + (lane & 7) * 16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int rr = 8 * j + (lane >> 3);
+        const uint4 cw = *reinterpret_cast<const uint4*>(qtile[w] + rr * 128 + (((lane & 7) ^ (rr & 7)) << 4));
+        *reinterpret_cast<uint4*>(qrow + (int64_t)min(rb + rr, T - 1) * ld_q) = cw;
+      }
+      *reinterpret_cast<uint32_t*>(s + (((int64_t)(m >> 7) * s_col_tiles + col_tile_off + (c0 >> 7)) << 9) +
+                                   (m & 31) * 16 + ((m & 127) >> 5) * 4) = epack;
+    }
+    if constexpr (kLora) {
+      // rows past T computed row T - 1's values again (same inputs, same order): storing them to row T - 1
+      // writes the same bytes, so every store is unconditional
+      if (direct) {  // one column chunk: the sum is final (mxfp8.py:168-172, DXA_DIRECT)
+        uint16_t* o = dxa + (int64_t)mc * ld_dxa;
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i) o[(i >> 2) * 8 + lg * 4 + (i & 3)] = bf(p[i] * scale);
+      } else {
+        float* o = part_dxa + ((int64_t)blockIdx.y * T + mc) * R;
+#pragma unroll
+        for (int i4 = 0; i4 < R / 8; ++i4)
+          *reinterpret_cast<float4*>(o + i4 * 8 + lg * 4) =
+              make_float4(p[4 * i4], p[4 * i4 + 1], p[4 * i4 + 2], p[4 * i4 + 3]);
+      }
+    }
+  };
+  // LDS slot of piece j: row 4j + lane/16, physical chunk (lane%16) ^ (row%16); (4j + prow) % 16 = 4 (j % 4) + prow
+  uint8_t* st0 = tile + prow * 256 + ((pc ^ prow) << 4);
+  uint8_t* st1 = tile + prow * 256 + ((pc ^ (prow + 4)) << 4);
+  uint8_t* st2 = tile + prow * 256 + ((pc ^ (prow + 8)) << 4);
+  uint8_t* st3 = tile + prow * 256 + ((pc ^ (prow + 12)) << 4);
+  // One block: stage register set P into the wave's LDS tiles, start the loads of the wave's block kAhead blocks
+  // on into P (none past its last), then quantize and multiply.  Two blocks stay in flight per wave (one for
+  // r = 32 with both outputs, whose accumulators leave no room for a second set).
+  constexpr int kAhead = (R == 32 && kQuant && kLora) ? 4 : 8;
+#define LB_BODY(b, P)                                                                                       \
+  {                                                                                                         \
+    *reinterpret_cast<uint4*>(st0) = P##0;                                                                  \
+    *reinterpret_cast<uint4*>(st1 + 1024) = P##1;                                                           \
+    *reinterpret_cast<uint4*>(st2 + 2048) = P##2;                                                           \
+    *reinterpret_cast<uint4*>(st3 + 3072) = P##3;                                                           \
+    *reinterpret_cast<uint4*>(st0 + 4096) = P##4;                                                           \
+    *reinterpret_cast<uint4*>(st1 + 5120) = P##5;                                                           \
+    *reinterpret_cast<uint4*>(st2 + 6144) = P##6;                                                           \
+    *reinterpret_cast<uint4*>(st3 + 7168) = P##7;                                                           \
+    if constexpr (kXaL >= 1) *reinterpret_cast<uint4*>(xat[w] + lane * 8) = P##x0;                          \
+    if constexpr (kXaL >= 2) *reinterpret_cast<uint4*>(xat[w] + 512 + lane * 8) = P##x1;                    \
+    if ((b) + kAhead < nblk) LB_FETCH((b) + kAhead, P)                                                      \
+    lb_block(r0 + 32 * (b));                                                                                \
+  }
+  if constexpr (kAhead == 8) {
+    if (w < nblk) LB_FETCH(w, ca)
+    if (w + 4 < nblk) LB_FETCH(w + 4, cb)
+    for (int b = w; b < nblk; b += 8) {
+      LB_BODY(b, ca)
+      if (b + 4 < nblk) LB_BODY(b + 4, cb)
+    }
+  } else {
+    if (w < nblk) {  // the first block outside the loop: the same memory operations in flight on every entry
+      LB_FETCH(w, ca)
+      LB_BODY(w, ca)
+    }
+    for (int b = w + 4; b < nblk; b += 4) LB_BODY(b, ca)
+  }
+#undef LB_BODY
+  if constexpr (kLora) {
+    // the four waves' dB, added in wave order, 16 ρ at a time (the dy tiles are free now)
+    float(*red)[128][17] = reinterpret_cast<float(*)[128][17]>(tiles);
+#pragma unroll
+    for (int h = 0; h < R / 16; ++h) {
+      __syncthreads();
+      // lane l: ρ = 16 h + l % 16, column 32 g + 16 jh + (l / 16) * 4 + i
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) red[w][32 * g + 16 * jh + (lane >> 4) * 4 + i][lane & 15] = db[g][jh][h][i];
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < 128 * 16; idx += 256) {
+        const int n = idx >> 4, rr = idx & 15;
+        part_db[((int64_t)blockIdx.x * N + c0 + n) * R + h * 16 + rr] =
+            ((red[0][n][rr] + red[1][n][rr]) + red[2][n][rr]) + red[3][n][rr];
+      }
+    }
   }
 }
+#undef LB_FETCH
 
 // 16-byte vectors of fp32 partial sums added in ascending partial order, four loads in flight at a time
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
@@ -454,7 +519,9 @@ __device__ __forceinline__ float4 sum_ordered(const float4* __restrict__ p, int6
   return v;
 }
 
-
+// dxa[t, ρ] (row stride ld_dxa) = bf16(scale · Σ_p part_dxa[p, t, ρ]) over the first nx = T·R elements (none when
+// the main kernel wrote d(xa) itself) and dB[n, ρ] = scale · Σ_p part_db[p, n, ρ] (fp32) over the next N·R, partials
+// added in ascending p (mxfp8.py:180-216, _sum_rows / _sum_parts).  Four consecutive elements per thread.
 __global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restrict__ part_dxa, int ncs, int64_t nx,
                                                            const float* __restrict__ part_db, int nrs, int64_t nb,
                                                            int R, float scale, uint16_t* __restrict__ dxa,
@@ -760,13 +827,17 @@ extern "C" int mxfp8_res_lora(const void* x, const void* y, const void* xa, int6
   return MXFP8_OK;
 }
 
-extern "C" int64_t mxfp8_lora_bwd_chunks(int64_t T, int64_t N) {
+// Row chunks for about `target` workgroups over (chunks, N / 128): two per CU with the LoRA products (their dB
+// partials grow with the chunk count), three for the codes alone.
+static int64_t lora_bwd_rows(int64_t T, int64_t N, int64_t target) {
   if (T <= 0 || N <= 0 || N % 128) return 0;
   const int64_t blocks = (T + 127) / 128 * 4;  // 32-row blocks up to the padded end of the last 128-row tile
-  const int64_t cs = N / 128, want = (512 + cs - 1) / cs;
+  const int64_t cs = N / 128, want = (target + cs - 1) / cs;
   const int64_t per = (blocks + std::min(want, blocks) - 1) / std::min(want, blocks);
   return (blocks + per - 1) / per;
 }
+
+extern "C" int64_t mxfp8_lora_bwd_chunks(int64_t T, int64_t N) { return lora_bwd_rows(T, N, 512); }
 
 extern "C" int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q, int64_t ld_q, void* s,
                               int64_t s_col_tiles, int64_t col_tile_off, const void* xa, int64_t ld_xa, const void* b,
@@ -777,13 +848,13 @@ extern "C" int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_d
   MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && ld_dy >= N && ld_dy % 8 == 0 && T * ld_dy < (1LL << 40),
                "mxfp8_lora_bwd: need N %% 128 == 0");
   MX_CHECK_ARG(!quant || (s && ld_q % 16 == 0 && col_tile_off >= 0 && col_tile_off * 128 + N <= ld_q &&
-                          col_tile_off * 128 + N <= s_col_tiles * 128 && mx_aligned(q, 16)),
+                          col_tile_off * 128 + N <= s_col_tiles * 128 && mx_aligned(q, 16) && mx_aligned(s, 4)),
                "mxfp8_lora_bwd: bad code / scale destination");
   MX_CHECK_ARG(!lora || (b && dxa && db && part_dxa && part_db && (r == 16 || r == 32) && ld_xa >= r &&
                          ld_xa % 8 == 0 && ld_dxa >= r && mx_aligned(xa, 16) && mx_aligned(b, 2)),
                "mxfp8_lora_bwd: LoRA needs xa, B, dxa, dB and partial buffers, r in {16, 32}");
   MX_CHECK_ARG(mx_aligned(dy, 16), "mxfp8_lora_bwd: misaligned dy");
-  const int64_t rs = mxfp8_lora_bwd_chunks(T, N);
+  const int64_t rs = lora ? mxfp8_lora_bwd_chunks(T, N) : lora_bwd_rows(T, N, 768);
   const int64_t Tpad = (T + 127) / 128 * 128, blocks = Tpad / 32;
   const int64_t chunk = (blocks + rs - 1) / rs * 32;
   const int64_t used = (Tpad + chunk - 1) / chunk;

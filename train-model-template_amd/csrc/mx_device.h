@@ -169,16 +169,23 @@ __device__ __forceinline__ void load16_rc(const uint16_t* base, int64_t r, int64
 // MX-quantize the 16 contiguous values w (8 packed pairs) of row mc, columns k0..k0+15, which with the partner
 // lane's 16 form one 32-block: one 16-byte code store (row-major with Kq codes per row, or MX-tiled), scale
 // byte of row m (0 for padded rows).
-__device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
-                                        int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
+// The 16 codes of w (with the partner lane's 16 forming the 32-block) into c; returns the block's E8M0 scale.
+__device__ __forceinline__ uint32_t quant16_codes(const uint32_t* w, uint4& c) {
   u16x2 mm = {0, 0};
 #pragma unroll
   for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
   uint32_t am = amax_bits(mm);
   am = max(am, (uint32_t)__shfl_xor((int)am, 32));
   const uint32_t e = e8m0_from_amax_bits(am);
-  const uint4 c = make_uint4(encode4_bf16(w[0], w[1], e), encode4_bf16(w[2], w[3], e), encode4_bf16(w[4], w[5], e),
-                             encode4_bf16(w[6], w[7], e));
+  c = make_uint4(encode4_bf16(w[0], w[1], e), encode4_bf16(w[2], w[3], e), encode4_bf16(w[4], w[5], e),
+                 encode4_bf16(w[6], w[7], e));
+  return e;
+}
+
+__device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
+                                        int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
+  uint4 c;
+  const uint32_t e = quant16_codes(w, c);
   *reinterpret_cast<uint4*>(q + (tiled ? tiled_offset(mc, k0, Kq) : mc * Kq + k0)) = c;
   // both lanes of the pair store the same byte (no divergent branch in the loop)
   s[blocked_offset(m, k0 >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
