@@ -131,9 +131,25 @@ def _quantizer(T, K, N, dev):
     return out, wq_ms
 
 
+def _time_calls_gpu(fn, n):
+    """Mean GPU time of fn() in ms: an event pair around each call, so host-side gaps between calls (the Python
+    wrapper of a ~20 us kernel pair takes about as long) are not counted."""
+    import torch
+    for _ in range(3):
+        fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / n
+
+
 def _lora_epilogues(T, K, N, r, dev):
-    """The LoRA epilogues beside the MLP (mxfp8.lora_bwd, mxfp8.res_lora) at the workload's token count, timed with
-    events around back-to-back launches on the current stream; algorithmic bytes over the mean call time."""
+    """The LoRA epilogues beside the MLP (mxfp8.lora_bwd, mxfp8.res_lora) at the workload's token count: GPU time
+    per call (events around each call), algorithmic bytes over it."""
     import torch
 
     import mxfp8
@@ -152,13 +168,13 @@ def _lora_epilogues(T, K, N, r, dev):
         q = torch.empty(T, cols, dtype=mxfp8.F8, device=dev)
         s = torch.empty(mxfp8.scale_numel(T, cols), dtype=torch.uint8, device=dev)
         dS = torch.empty(T, 2 * r, dtype=torch.bfloat16, device=dev)
-        ms = _time_launches(lambda: mxfp8.lora_bwd(dy, xS[:, :r], B, 2.0, q, s, 0, dS[:, :r]), 50)
+        ms = _time_calls_gpu(lambda: mxfp8.lora_bwd(dy, xS[:, :r], B, 2.0, q, s, 0, dS[:, :r]), 50)
         rec(f"lora_bwd+q dy[T,{cols}] r{r}", ms, workloads.lora_bwd_bytes(T, cols, r))
         del dy, q, s
     x = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16)
     y = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16)
     B = (torch.randn(K, r, device=dev, generator=g) * 0.02).to(torch.bfloat16)
-    ms = _time_launches(lambda: mxfp8.res_lora(x, y, xS[:, :r], B, 2.0), 50)
+    ms = _time_calls_gpu(lambda: mxfp8.res_lora(x, y, xS[:, :r], B, 2.0), 50)
     rec(f"res_lora [T,{K}] r{r}", ms, workloads.res_lora_bytes(T, K, r))
     return out
 
@@ -326,6 +342,8 @@ def main():
     ap.add_argument("--no-quant", action="store_true", help="skip the standalone quantizer timings")
     ap.add_argument("--cpu-tokens", type=int, default=1024)
     ap.add_argument("--copy-calib", action="store_true")
+    ap.add_argument("--only", choices=("epilogues",), help="time only the LoRA epilogues and the grouped linears "
+                    "(one JSON line of those figures, not the MLP metric line): the profiling command of that section")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--traffic-commands", nargs=2, default=("", ""), metavar=("CMD_FETCH", "CMD_WRITE"))
     args = ap.parse_args()
@@ -348,6 +366,12 @@ def main():
     torch.cuda.set_device(dev)
     cfg = args.config
     c = workloads.CONFIGS[cfg]
+    if args.only == "epilogues":
+        T, K, N = c["T"], c["K"], c["N"]
+        print(json.dumps({"config": workloads.DESCRIPTIONS[cfg],
+                          "lora_epilogues": _lora_epilogues(T, K, N, c["r"], dev),
+                          "grouped_linears": _grouped_linears(T, K, c["r"], c["alpha"], dev)}), flush=True)
+        return
     model, inps = workloads.build_model(cfg, layers=c["layers"], device=dev)
     mxfp8.enable_mxfp8(model)
     mods = [layer.mlp for layer in model.layers]
