@@ -224,3 +224,31 @@ def test_lora_bwd_quant_matches_mx_quant(gpu):
     assert mxfp8.lora_bwd(dy, q=q, s=s) is None
     qr, sr = mxfp8.mx_quant(dy)
     assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr.view(torch.uint8))
+
+
+@pytest.mark.parametrize("mode", ["both", "quant"])
+def test_lora_bwd_codes_on_edge_blocks(mode, gpu):
+    # configuration 5's upstream gradient (Student-t with x100 channels, +-0 blocks, 448·2^k maxima, RNE ties)
+    # plus NaN and inf blocks: codes and scale words byte for byte the oracle's, at a column-tile offset
+    import mxfp8
+    import workloads
+    from oracle import mx
+    dy = workloads.make_inputs(5, T=700, x=False)["dy"].clone()  # [700, 2048]
+    dy[5, 64:96] = float("nan")
+    dy[6, 128:160] = float("inf")
+    dy[7, 0:32] = -float("inf")
+    dy[699, 2016:2048] = float("nan")
+    T, N, off = dy.shape[0], dy.shape[1], 1
+    width = (off + N // 128) * 128
+    q = torch.zeros(T, width, dtype=torch.uint8, device=gpu)
+    s = torch.zeros(mxfp8.scale_numel(T, width), dtype=torch.uint8, device=gpu)
+    g = torch.Generator().manual_seed(3)
+    xa = torch.randn(T, 16, generator=g).to(torch.bfloat16).to(gpu) if mode == "both" else None
+    B = (torch.randn(N, 16, generator=g) * 0.05).to(torch.bfloat16).to(gpu) if mode == "both" else None
+    dxa = torch.empty(T, 16, dtype=torch.bfloat16, device=gpu) if mode == "both" else None
+    mxfp8.lora_bwd(dy.to(gpu), xa, B, 1.0, q, s, off, dxa)
+    qr = torch.zeros(T, width, dtype=torch.uint8)
+    sr = torch.zeros(mx.scale_bytes(T, width), dtype=torch.uint8)
+    mx.quant_into(dy, qr, sr, off * 128, width // 128)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu(), qr)
