@@ -420,10 +420,11 @@ __global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __rest
       for (int j = 0; j < 4; ++j) {
         const int rr = 8 * j + (lane >> 3);
         const uint4 cw = *reinterpret_cast<const uint4*>(qtile[w] + rr * 128 + (((lane & 7) ^ (rr & 7)) << 4));
-        *reinterpret_cast<uint4*>(qrow + (int64_t)min(rb + rr, T - 1) * ld_q) = cw;
+        store_codes<MX_NT_FUSED>(qrow + (int64_t)min(rb + rr, T - 1) * ld_q, cw);
       }
-      *reinterpret_cast<uint32_t*>(s + (((int64_t)(m >> 7) * s_col_tiles + col_tile_off + (c0 >> 7)) << 9) +
-                                   (m & 31) * 16 + ((m & 127) >> 5) * 4) = epack;
+      store_codes<MX_NT_FUSED>(s + (((int64_t)(m >> 7) * s_col_tiles + col_tile_off + (c0 >> 7)) << 9) +
+                                   (m & 31) * 16 + ((m & 127) >> 5) * 4,
+                               epack);
     }
     if constexpr (kLora) {
       // rows past T computed row T - 1's values again (same inputs, same order): storing them to row T - 1

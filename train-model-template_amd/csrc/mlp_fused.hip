@@ -92,10 +92,10 @@ __device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, b
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int64_t k = jb + g * 8 + (lane >> 5) * 4;
-      *reinterpret_cast<uint32_t*>(q + (tiled ? tiled_offset(mc, k, Kq) : mc * Kq + k)) = c[g];
+      store_codes<MX_NT_FUSED>(q + (tiled ? tiled_offset(mc, k, Kq) : mc * Kq + k), c[g]);
     }
   }
-  if (lane < 32) s[blocked_offset(m, jb >> 5, s_col_tiles)] = live ? (uint8_t)e : (uint8_t)0;
+  if (lane < 32) store_scale<MX_NT_FUSED>(s + blocked_offset(m, jb >> 5, s_col_tiles), live ? (uint8_t)e : (uint8_t)0);
 }
 
 // registers 8s..8s+7 of an element tile held as packed words w[4s..4s+3], as an MFMA operand

@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
       uint2 codes = quant8(v[it], e);
       if (r < rows) {
         // row-major (row stride ld_q), or the MX-tiled layout with tk codes per row
-        *reinterpret_cast<uint2*>(q + (tk ? tiled_offset(r, col, tk) : r * ld_q + col)) = codes;
+        store_codes<MX_NT_QUANT>(q + (tk ? tiled_offset(r, col, tk) : r * ld_q + col), codes);
         if ((tid & 3) == 0) sb[(rl & 31) * 16 + (rl >> 5) * 4 + (c8 >> 5)] = (uint8_t)e;
       }
     }
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
   }
   __syncthreads();
   if (kRows && tid < 32)
-    reinterpret_cast<uint4*>(s + (rt * s_col_tiles + s_tile0 + ct) * 512)[tid] =
-        reinterpret_cast<const uint4*>(stile)[tid];
+    store_codes<MX_NT_QUANT>(s + (rt * s_col_tiles + s_tile0 + ct) * 512 + tid * 16,
+                             reinterpret_cast<const uint4*>(stile)[tid]);
   if (kCols && tid >= 64 && tid < 96) {
     // tile (row tile ct, column tile rt) of xᵀ's blocked scales, rows/128 tiles per tile row
     const int64_t n_tiles_t = rows / kTile;
