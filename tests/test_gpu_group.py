@@ -185,3 +185,78 @@ def test_residual_add_deferred_matches_plain(gpu):
     t = torch.maximum(y.float().abs(), got.float().abs())
     assert bool((d_ <= torch.exp2(torch.floor(torch.log2(t.clamp_min(1e-30)))) * 2 ** -7 * 1.0001 + 1e-30).all())
     assert (got == want).double().mean().item() >= 0.99
+
+
+@pytest.mark.parametrize("r", [32, 8])
+def test_group_other_ranks_match_plain_path(r, gpu):
+    # r = 32 takes the fused kernels with a 64-wide padded S (3 layers x 32 = 96 rows: the torch thin GEMMs);
+    # r = 8 is outside the fused kernels' ranks (codes from lora_bwd, products as plain GEMMs): the grouped
+    # backward must match the plain backward of the same layers within tolerance either way
+    import mxfp8
+    g = torch.Generator().manual_seed(20 + r)
+    m = _Model.__new__(_Model)
+    nn.Module.__init__(m)
+    m.model = nn.Module()
+    layer = nn.Module()
+    attn = nn.Module()
+
+    def lin(n_out, n_in):
+        x = nn.Linear(n_in, n_out, bias=False)
+        with torch.no_grad():
+            x.weight.copy_(torch.randn(n_out, n_in, generator=g) * 0.03)
+        x.weight.requires_grad_(False)
+        return x
+
+    for name, n in (("q_proj", NQ), ("k_proj", NKV), ("v_proj", NKV)):
+        setattr(attn, name, workloads.LoraLinear(lin(n, K), torch.randn(r, K, generator=g) * 0.03,
+                                                 torch.randn(n, r, generator=g) * 0.03, ALPHA))
+        getattr(attn, name).base_layer.to(dtype=torch.bfloat16)
+    layer.self_attn = attn
+    m.model.layers = nn.ModuleList([layer])
+    m = m.to(gpu)
+    mxfp8.enable_mxfp8(m)
+    mods = [attn.q_proj, attn.k_proj, attn.v_proj]
+    x = (torch.randn(T, K, generator=g)).to(torch.bfloat16).to(gpu)
+    dys = [(torch.randn(T, n, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for n in (NQ, NKV, NKV)]
+
+    def run():
+        fused_linear.new_step()
+        for p in m.parameters():
+            p.grad = None
+        xg = x.clone().requires_grad_(True)
+        outs = fused_linear.group_linear(xg, mods)
+        torch.autograd.backward(outs, dys)
+        return [o.detach() for o in outs], xg.grad, [p.grad.clone() for p in m.parameters() if p.requires_grad]
+
+    before = fused_linear.STATS.get("lan ngược gộp", 0)
+    of, dxf, gf = run()
+    assert fused_linear.STATS.get("lan ngược gộp", 0) == before + 1
+    for mod in mods:
+        mod.base_layer._mx_fbwd = False
+    op, dxp, gp = run()
+    for a, b in zip(of, op):
+        assert torch.equal(a, b)  # same forward path
+    _close(dxf, dxp.double().cpu(), "dx")
+    for k, (a, b) in enumerate(zip(gf, gp)):
+        _close(a, b.double().cpu(), f"grad {k}")
+
+
+def test_need_out_false_keeps_gradients(gpu):
+    # the recompute mode builds the same graph without the base GEMM outputs: identical gradients
+    m, _ = _build(gpu, seed=9)
+    a = m.attn
+    mods = [a.q_proj, a.k_proj, a.v_proj]
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    dys = [(torch.randn(T, n, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for n in (NQ, NKV, NKV)]
+    res = []
+    for need_out in (True, False):
+        fused_linear.new_step()
+        for p in m.parameters():
+            p.grad = None
+        xg = x.clone().requires_grad_(True)
+        outs = fused_linear.group_linear(xg, mods, need_out=need_out)
+        torch.autograd.backward(outs, dys)
+        res.append([xg.grad.clone()] + [p.grad.clone() for p in m.parameters() if p.grad is not None])
+    for u, v in zip(*res):
+        assert torch.equal(u, v)
