@@ -120,6 +120,19 @@ int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, con
                   int64_t workspace_bytes, void* stream);
 
 /*
+ * mxfp8_gemm_nt with the output columns in n_seg (1..4) separate row-major matrices: columns
+ * [seg_col0[k], seg_col0[k+1]) (the last up to N) go to seg_c[k] with row stride seg_ldc[k]; seg_col0[0] = 0 and
+ * every boundary a multiple of 128.  seg_col0, seg_c and seg_ldc are host arrays.  The 4-wave shape with row-major
+ * C only (layout bits 0-1), no workspace.  Lets the q|k|v projections of a group run as one GEMM over their
+ * concatenated weight while each returns its own contiguous output (the reference runs one _scaled_mm per layer,
+ * /root/reference/scripts/fused_linear.py:72-76, :106-109).
+ */
+int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
+                      int64_t M, int64_t N, int64_t K, int64_t n_seg, const int64_t* seg_col0, void* const* seg_c,
+                      const int64_t* seg_ldc, const void* lora_p, int64_t ld_p, const void* lora_q, int64_t ld_q,
+                      int64_t r, float alpha, int64_t layout, void* stream);
+
+/*
  * Bytes of workspace mxfp8_gemm_nt uses for this shape with MXFP8_GEMM_WIDE on the current device (0: no
  * split).  No reference counterpart: torch._scaled_mm (fused_mlp.py:279) manages the cuBLAS workspace itself.
  */

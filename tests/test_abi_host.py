@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 24, names
+    assert len(names) == 25, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -80,6 +80,17 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.mxfp8_lora_tn(p, 4, 96, 96, p, 16, 1, ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), 1.0, 0, 0, p,
                              None) == -1
     assert lib.mxfp8_lora_tn_chunks(10752, 2048) > 0 and lib.mxfp8_lora_tn_chunks(10752, 100) == 0
+    # segmented GEMM output: boundaries at multiples of 128 from 0, 4-wave row-major only
+    cols = (ctypes.c_int64 * 2)(0, 100)
+    ptrs = (ctypes.c_void_p * 2)(16, 16)
+    lds = (ctypes.c_int64 * 2)(128, 128)
+    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, None, 0, None, 0, 0, 1.0, 0,
+                                 None) == -1
+    cols = (ctypes.c_int64 * 2)(0, 128)
+    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, None, 0, None, 0, 0, 1.0, 4,
+                                 None) == -1
+    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 5, cols, ptrs, lds, None, 0, None, 0, 0, 1.0, 0,
+                                 None) == -1
     # SwiGLU: n % 8, aligned
     assert lib.mxfp8_swiglu(p, p, 12, p, None) == -1
     assert lib.mxfp8_swiglu_bwd(p, p, p, 16, p, ctypes.c_void_p(18), None) == -1
@@ -141,8 +152,8 @@ def test_bwd_grid_choice():
 
 def test_fwd_groups_choice(lib):
     # one wave per (32-row block, column group); without a GPU the library assumes 256 CUs, and the kernel is
-    # built for 3 waves per SIMD: 3072 waves per round
-    cap = 256 * 4 * 3
+    # built for 2 waves per SIMD (two tiles in flight per wave): 2048 waves per round
+    cap = 256 * 4 * 2
     for T, N in [(10752, 6144), (256, 3584), (4096, 3584), (8896, 6144)]:
         ng = fused_mlp._fwd_groups(T, N)
         nt = N // 32

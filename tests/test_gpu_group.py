@@ -260,3 +260,29 @@ def test_need_out_false_keeps_gradients(gpu):
         res.append([xg.grad.clone()] + [p.grad.clone() for p in m.parameters() if p.grad is not None])
     for u, v in zip(*res):
         assert torch.equal(u, v)
+
+
+def test_merged_forward_gemm_matches_one_gemm_per_layer(gpu):
+    # q|k|v as ONE GEMM over the concatenated forward weight with the block-diagonal LoRA epilogue: the same bits
+    # as one GEMM per layer (the zero blocks add nothing), each output contiguous
+    import mxfp8
+    m, _ = _build(gpu, seed=21)
+    a = m.attn
+    mods = [a.q_proj, a.k_proj, a.v_proj]
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    fused_linear.new_step()
+    merged = fused_linear.group_linear(x, mods)
+    assert all(o.is_contiguous() for o in merged)
+    saved = mxfp8.group_fwd_operand
+    mxfp8.group_fwd_operand = lambda lins: None  # one GEMM per layer
+    try:
+        fused_linear.new_step()
+        single = fused_linear.group_linear(x, mods)
+    finally:
+        mxfp8.group_fwd_operand = saved
+    for u, v in zip(merged, single):
+        assert torch.equal(u, v)
+    # two consecutive layers of the group (k|v) merge too; a non-consecutive pair (q, v) does not
+    assert mxfp8.group_fwd_operand([a.k_proj.base_layer, a.v_proj.base_layer]) is not None
+    assert mxfp8.group_fwd_operand([a.q_proj.base_layer, a.v_proj.base_layer]) is None

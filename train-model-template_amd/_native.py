@@ -28,6 +28,8 @@ SIGNATURES = {
     "mxfp8_gemm_nt": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
                       _i64, _f32, _i64, _ptr, _i64, _ptr],
     "mxfp8_gemm_workspace_size": [_i64, _i64, _i64],
+    "mxfp8_gemm_nt_seg": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64,
+                          _ptr, _i64, _i64, _f32, _i64, _ptr],
     "mxfp8_mlp_fwd_groups": [_i64, _i64, _i64],
     "mxfp8_mlp_fwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _i64, _ptr, _i64,
                       _ptr],
@@ -165,6 +167,28 @@ def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0, split=True
     ws, ws_bytes = gemm_workspace(M, N, K, c.device) if split and layout & GEMM_WIDE else (None, 0)
     call("mxfp8_gemm_nt", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(p), ldp,
          _p(q), ldq, r, float(alpha), layout, _p(ws), ws_bytes, like=c)
+
+
+def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, layout=0):
+    """gemm_nt with the N output columns split over `outs` (1..4 bf16 [M, n_k] matrices, any row stride; the widths
+    sum to N, each a multiple of 128)."""
+    n = len(outs)
+    col0, c0 = [], 0
+    for o in outs:
+        col0.append(c0)
+        c0 += o.shape[1]
+    cols = (ctypes.c_int64 * n)(*col0)
+    ptrs = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    lds = (ctypes.c_int64 * n)(*[o.stride(0) for o in outs])
+    if lora is None:
+        p = q = None
+        ldp = ldq = r = 0
+    else:
+        p, q = lora
+        r = p.shape[1]
+        ldp, ldq = p.stride(0), q.stride(0)
+    call("mxfp8_gemm_nt_seg", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, n, cols, ptrs, lds, _p(p), ldp, _p(q),
+         ldq, r, float(alpha), layout, like=outs[0])
 
 
 def mlp_fwd(gu, xs, bg, bu, ad, T, N, r, s_g, s_u, q, s, part, n_groups, h_out=None, q_layout=0):

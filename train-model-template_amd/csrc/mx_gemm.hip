@@ -86,6 +86,16 @@ struct Lora {
   float alpha;
 };
 
+// Output columns in up to four segments, each its own row-major matrix: columns [col0[k], col0[k + 1]) of the
+// product go to ptr[k] with row stride ld[k] (segment boundaries are multiples of the tile width, so a tile
+// writes into one segment).  One segment = the plain C, ldc.
+struct CSeg {
+  int n;
+  int col0[4];
+  int64_t ld[4];
+  uint16_t* ptr[4];
+};
+
 // Launch plan (computed on the host, see make_plan).
 struct Plan {
   int tm, tn;        // tiles along M and N
@@ -119,8 +129,7 @@ __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw
 template <int kR, int kNW>
 __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, int64_t lda, const uint8_t* __restrict__ B,
-    const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, uint16_t* __restrict__ C, int64_t ldc,
-    Lora lora, Plan plan, int tiled) {
+    const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, CSeg cseg, Lora lora, Plan plan, int tiled) {
   using S = Shape<kNW>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[S::kStages * S::kStageBytes];
   __shared__ int arrived;
@@ -315,6 +324,14 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
     if (tid == 0) __hip_atomic_store(plan.cnt + st_, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  // the output segment of this tile (wave-uniform)
+  int sg = 0;
+#pragma unroll
+  for (int k = 1; k < 4; ++k)
+    if (k < cseg.n && n0 >= cseg.col0[k]) sg = k;
+  uint16_t* const C = cseg.ptr[sg];
+  const int64_t ldc = cseg.ld[sg];
+  const int ncol0 = cseg.col0[sg];
   // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
   // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]
 #pragma unroll
@@ -348,7 +365,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
           const int n = nb + g * 8 + (lane >> 5) * 4;
           if (n < N) {
             uint2 w = make_uint2(pack_bf16x2(o[4 * g], o[4 * g + 1]), pack_bf16x2(o[4 * g + 2], o[4 * g + 3]));
-            *reinterpret_cast<uint2*>(C + (c_ft ? ft_offset(m, n, N) : (int64_t)m * ldc + n)) = w;
+            *reinterpret_cast<uint2*>(C + (c_ft ? ft_offset(m, n, N) : (int64_t)m * ldc + (n - ncol0))) = w;
           }
         }
       }
@@ -404,11 +421,11 @@ int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
 
 template <int kNW>
 void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, const uint8_t* SB, int64_t ldb,
-            int M, int N, int K, uint16_t* C, int64_t ldc, const Lora& lo, int r, const Plan& plan, int layout,
+            int M, int N, int K, const CSeg& cseg, const Lora& lo, int r, const Plan& plan, int layout,
             hipStream_t stm) {
   using S = Shape<kNW>;
   dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
-#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, C, ldc, lo, plan, layout
+#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout
   if (!lo.p) gemm_kernel<0, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 16) gemm_kernel<16, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 32) gemm_kernel<32, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
@@ -424,10 +441,13 @@ extern "C" int64_t mxfp8_gemm_workspace_size(int64_t M, int64_t N, int64_t K) {
   return make_plan<2>(M, N, K, cached_cus(), p);  // only the 8-wave shape splits
 }
 
-extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
-                             int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
-                             const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
-                             void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb, int64_t M,
+              int64_t N, int64_t K, CSeg cseg, const void* lora_p, int64_t ld_p, const void* lora_q, int64_t ld_q,
+              int64_t r, float alpha, int64_t layout, void* workspace, int64_t workspace_bytes, void* stream) {
+  void* const c = cseg.ptr[0];
+  int64_t ldc = cseg.ld[0];
   MX_CHECK_ARG(a && sa && b && sb && c, "mxfp8_gemm_nt: null pointer");
   MX_CHECK_ARG(M >= 0 && N > 0 && K > 0 && K % 128 == 0 && N % 128 == 0,
                "mxfp8_gemm_nt: need K %% 128 == 0 and N %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
@@ -439,8 +459,10 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
   if (layout & 1) lda = K;  // the tiled layouts have no row stride
   if (layout & 2) ldb = K;
   if (layout & MXFP8_GEMM_C_FT) ldc = N;
-  MX_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0 && ldc >= N && ldc % 4 == 0,
+  const int64_t seg_w0 = cseg.n > 1 ? cseg.col0[1] : N;  // width of the first segment
+  MX_CHECK_ARG(lda >= K && ldb >= K && lda % 16 == 0 && ldb % 16 == 0 && ldc >= seg_w0 && ldc % 4 == 0,
                "mxfp8_gemm_nt: bad strides");
+  cseg.ld[0] = ldc;
   MX_CHECK_ARG(256LL * lda < (1LL << 32) && 256LL * ldb < (1LL << 32), "mxfp8_gemm_nt: stride too large");
   MX_CHECK_ARG(mx_aligned(a, 16) && mx_aligned(b, 16) && mx_aligned(sa, 16) && mx_aligned(sb, 16) &&
                    mx_aligned(c, 8),
@@ -470,11 +492,47 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   const int tiled = (int)(layout & ~MXFP8_GEMM_WIDE);
   if (wide)
-    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo, (int)r, plan, tiled,
-              (hipStream_t)stream);
+    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, (hipStream_t)stream);
   else
-    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, (uint16_t*)c, ldc, lo, (int)r, plan, tiled,
-              (hipStream_t)stream);
+    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, (hipStream_t)stream);
   MX_CHECK_LAUNCH("mxfp8_gemm_nt");
   return MXFP8_OK;
+}
+
+}  // namespace
+
+extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
+                             int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
+                             const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
+                             void* workspace, int64_t workspace_bytes, void* stream) {
+  CSeg cs{};
+  cs.n = 1;
+  cs.ptr[0] = (uint16_t*)c;
+  cs.ld[0] = ldc;
+  return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, ld_p, lora_q, ld_q, r, alpha, layout, workspace,
+                   workspace_bytes, stream);
+}
+
+extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, const void* b, const void* sb,
+                                 int64_t ldb, int64_t M, int64_t N, int64_t K, int64_t n_seg, const int64_t* seg_col0,
+                                 void* const* seg_c, const int64_t* seg_ldc, const void* lora_p, int64_t ld_p,
+                                 const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
+                                 void* stream) {
+  MX_CHECK_ARG(n_seg >= 1 && n_seg <= 4 && seg_col0 && seg_c && seg_ldc, "mxfp8_gemm_nt_seg: 1 to 4 segments");
+  MX_CHECK_ARG(!(layout & (MXFP8_GEMM_WIDE | MXFP8_GEMM_C_FT)),
+               "mxfp8_gemm_nt_seg: segments take the 4-wave shape and row-major C");
+  CSeg cs{};
+  cs.n = (int)n_seg;
+  for (int64_t k = 0; k < n_seg; ++k) {
+    const int64_t c0 = seg_col0[k], c1 = k + 1 < n_seg ? seg_col0[k + 1] : N;
+    MX_CHECK_ARG(seg_c[k] && c0 % 128 == 0 && c1 > c0 && c1 <= N && (k > 0 || c0 == 0) && seg_ldc[k] >= c1 - c0 &&
+                     seg_ldc[k] % 4 == 0 && mx_aligned(seg_c[k], 8),
+                 "mxfp8_gemm_nt_seg: segment %lld: columns from 0, increasing multiples of 128, ldc >= width",
+                 (long long)k);
+    cs.col0[k] = (int)c0;
+    cs.ptr[k] = (uint16_t*)seg_c[k];
+    cs.ld[k] = seg_ldc[k];
+  }
+  return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, ld_p, lora_q, ld_q, r, alpha, layout, nullptr, 0,
+                   stream);
 }

@@ -97,6 +97,43 @@ def _base_mm(base, x2, dt, q, T):
     return x2 @ base.weight.to(dt).t()
 
 
+def _fwd_merged(parts, lora, Bs, xS, q, T, dt, skey):
+    """Outputs of the group's MX layers from ONE GEMM over their concatenated forward weight (a consecutive range of
+    one mxfp8._CATS group), each written to its own contiguous tensor, with every layer's LoRA-B product in the
+    epilogue: P = xS (the padded x·Sᵀ), Q = the layers' B placed block-diagonally at their S columns (zeros adding
+    nothing), one alpha.  Same bits as one GEMM per layer.  None when the layers do not qualify (not a cat range,
+    LoRA scalings that differ, xS not in the padded native form)."""
+    import mxfp8
+    mxi = [i for i, p in enumerate(parts) if _mx(p[0])]
+    if len(mxi) < 2 or xS is None or not _vec_ok(xS) or xS.shape[1] not in (16, 32, 64):
+        return None
+    op = mxfp8.group_fwd_operand([parts[i][0] for i in mxi])
+    if op is None:
+        return None
+    lora_of = {i: (j, o, r, s) for j, (i, o, r, s) in enumerate(lora)}
+    scales = {lora_of[i][3] for i in mxi if i in lora_of}
+    if len(scales) > 1:
+        return None
+    alpha = scales.pop() if scales else 1.0
+    rp = xS.shape[1]
+    widths = [parts[i][0].out_features for i in mxi]
+
+    def qcat():
+        Q = torch.zeros((sum(widths), rp), dtype=dt, device=xS.device)
+        r0 = 0
+        for i, n in zip(mxi, widths):
+            if i in lora_of:
+                j, o, r, s = lora_of[i]
+                Q[r0:r0 + n, o:o + r] = Bs[j]
+            r0 += n
+        return Q
+
+    Q = _cast(skey + ("qcat", tuple(mxi), rp), qcat)
+    outs = [torch.empty((T, n), dtype=dt, device=xS.device) for n in widths]
+    mxfp8.mx_mm_seg(q[0], q[1], op[0], op[1], outs, lora=(xS, Q), alpha=alpha, layout=3, m=T)
+    return dict(zip(mxi, outs))
+
+
 class _Group(torch.autograd.Function):
     """Forward/backward of a group of linears on one input (fused_linear.py:79-196)."""
 
@@ -142,8 +179,13 @@ class _Group(torch.autograd.Function):
             if any(_mx(p[0]) for p in parts) and T:
                 import mxfp8
                 q = mxfp8.mx_quant_tiled(x2)  # once for the whole group
+            merged = _fwd_merged(parts, lora, Bs, xS, q, T, dt, skey) if (
+                q is not None and defer is None and dt == torch.bfloat16) else None
+            if merged:
+                for i, y in merged.items():
+                    outs[i] = y
             for i, (base, A, B, s) in enumerate(parts):
-                if i in thin_ids:
+                if i in thin_ids or (merged and i in merged):
                     continue
                 if i in lora_of and _mx(base) and dt == torch.bfloat16 and T:
                     j, o, r, s = lora_of[i]

@@ -179,6 +179,27 @@ def dequant(q, s, shape):
 GEMM_EVENTS = None  # set to a list to record (start event, end event, flops) around every MX GEMM launch
 
 
+def mx_mm_seg(q, s, wq, ws, outs, lora=None, alpha=1.0, layout=0, m=None):
+    """mx_mm whose N output columns go to the separate [M, n_k] tensors `outs` (consecutive column ranges, each a
+    multiple of 128 wide); 4-wave shape, row-major outputs."""
+    M, K = q.shape
+    if m is not None:
+        M = m
+    N = wq.shape[0]
+    assert sum(o.shape[1] for o in outs) == N and all(o.shape[0] == M for o in outs), ([o.shape for o in outs], N)
+    if M:
+        ev = GEMM_EVENTS
+        if ev is not None:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        _native.gemm_nt_seg(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, outs, lora=lora, alpha=alpha,
+                            layout=layout)
+        if ev is not None:
+            e1.record()
+            ev.append((e0, e1, 2 * M * N * K))
+    return outs
+
+
 def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     """bf16 [M, N] = MX(q [M, K]) · MX(wq [N, K])ᵀ, i.e. torch._scaled_mm(q, wq.t(), s, ws, out_dtype=bf16).
     wq may be a row slice/stride view (row stride wq.stride(0)); optional rank-r epilogue
@@ -360,6 +381,21 @@ def group_wt(lins):
     return cat.range(k, k + len(lins))
 
 
+def group_fwd_operand(lins):
+    """(B operand [ΣN, K] of the forward GEMM of consecutive layers of one concatenated group (MX-tiled), scales),
+    or None when the layers are not such a range."""
+    c = lins[0].__dict__.get("_mx_cat")
+    if c is None or getattr(c[0], "w_tl", None) is None:
+        return None
+    cat, k = c
+    for d, lin in enumerate(lins):
+        if lin.__dict__.get("_mx_cat") != (cat, k + d):
+            return None
+    c0, c1 = cat.offs[k], cat.offs[k + len(lins)]
+    tile_b = (cat.w_tl.shape[1] // 128) * 512
+    return cat.w_tl[c0:c1], cat.ws[c0 // 128 * tile_b:c1 // 128 * tile_b]
+
+
 def group_operand(lins):
     """(B operand [K, ΣN] of mx_mm, scales, layout bit) for dx of `lins` (group_wt): the MX-tiled copy when the
     range is a whole concatenated group, else the row-major column view (row stride = the group's ΣN)."""
@@ -401,11 +437,14 @@ def enable_mxfp8(model):
                 q, sq, qt, st = quant_both(w)
                 del w
                 cat = _Cat(qt, st, [lin.weight.shape[0] for lin in grp])
+                # the forward codes of the whole group (MX-tiled) for one GEMM over consecutive layers; each
+                # layer's own codes and scales are row slices of them
+                cat.w_tl, cat.ws = tile_codes(q), sq
                 tile_b = (q.shape[1] // 128) * 512  # scale bytes of one 128-row tile row
                 for k, lin in enumerate(grp):
                     c0, c1 = cat.offs[k], cat.offs[k + 1]
                     lin._mx_w, lin._mx_ws = q[c0:c1], sq[c0 // 128 * tile_b:c1 // 128 * tile_b]
-                    lin._mx_w_tl = tile_codes(lin._mx_w)
+                    lin._mx_w_tl = cat.w_tl[c0:c1]
                     lin._mx_cat = (cat, k)
                     in_cat.add(id(lin))
         gb, ub = d.get("gate_proj"), d.get("up_proj")
