@@ -567,32 +567,29 @@ __global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X,
   struct Step {
     uint32_t x[8];   // X row t + l % 32, columns kb + lg*16 .. + 15
     uint32_t p[PW];  // P row t + l % 32, columns lg * RP/2 .. + RP/2 - 1
+    bool ok;         // row t + l % 32 inside the chunk
   };
   auto fetch = [&](int t, Step& st) {
     const int row = t + (lane & 31);
-    const bool ok = row < t1;
+    st.ok = row < t1;
     const int rc = min(row, T - 1);
     load16(X + (int64_t)rc * ldx + kb + lg * 16, st.x);
-    uint32_t pv[PW];
     const uint16_t* prow = P + (int64_t)rc * RP + lg * (RP / 2);
     if constexpr (RP == 16) {
       const uint4 v = *reinterpret_cast<const uint4*>(prow);
-      pv[0] = v.x; pv[1] = v.y; pv[2] = v.z; pv[3] = v.w;
+      st.p[0] = v.x; st.p[1] = v.y; st.p[2] = v.z; st.p[3] = v.w;
     } else {
 #pragma unroll
-      for (int q = 0; q < PW; q += 8) load16(prow + 2 * q, pv + q);
+      for (int q = 0; q < PW; q += 8) load16(prow + 2 * q, st.p + q);
     }
-    // tokens past the chunk are zero (not 0 * whatever row T - 1 holds)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) st.x[k] = ok ? st.x[k] : 0u;
-#pragma unroll
-    for (int k = 0; k < PW; ++k) st.p[k] = ok ? pv[k] : 0u;
   };
-  Step cur, nxt;
-  fetch(t0, cur);
-  for (int t = t0; t < t1; t += 32) {
-    fetch(min(t + 32, t1 - 1 - ((t1 - 1 - t0) % 32)), nxt);  // the last step reloads itself, unused
-    __builtin_amdgcn_sched_barrier(0);
+  auto consume = [&](Step& cur) {
+    // tokens past the chunk are zero (not 0 * whatever row T - 1 holds); masked here, at the use, so the
+    // loads stay in flight until then
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cur.x[k] = cur.ok ? cur.x[k] : 0u;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) cur.p[k] = cur.ok ? cur.p[k] : 0u;
     tr_store(xt[w], lane, cur.x);
     // P tile row l % 32: the lane's RP/2 columns (RP = 64: lane half lg fills tile lg, columns 0..31)
     {
@@ -608,8 +605,26 @@ __global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X,
       acc[0][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc[0][h], 0, 0, 0);
       acc[1][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc[1][h], 0, 0, 0);
     }
-    cur = nxt;
+  };
+  // Register ring of kD 32-token steps: each round but the last consumes a slot and refills it kD steps ahead,
+  // unconditionally (a conditional load would make the counter waits at the loop header drain the ring); the
+  // refills past the chunk reload its last step, never consumed.
+  constexpr int kD = 2;
+  const int nsteps = (t1 - t0 + 31) / 32;
+  Step ring[kD];
+#pragma unroll
+  for (int j = 0; j < kD; ++j) fetch(t0 + 32 * min(j, nsteps - 1), ring[j]);
+  int s0 = 0;
+  for (; s0 + kD < nsteps; s0 += kD) {
+#pragma unroll
+    for (int j = 0; j < kD; ++j) {
+      consume(ring[j]);
+      fetch(t0 + 32 * min(s0 + j + kD, nsteps - 1), ring[j]);
+    }
   }
+#pragma unroll
+  for (int j = 0; j < kD; ++j)
+    if (s0 + j < nsteps) consume(ring[j]);
   // acc[jh][h] lane l: ρ = 16 h + l % 16, k = kb + 16 jh + (l / 16) * 4 + i
 #pragma unroll
   for (int jh = 0; jh < 2; ++jh)
