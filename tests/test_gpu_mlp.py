@@ -96,6 +96,16 @@ def test_mlp_end_to_end_config2_full(gpu):
     _check_e2e(out, f, b)
 
 
+@pytest.mark.parametrize("cfg", [3, 5])
+def test_mlp_end_to_end_full_size(cfg, gpu):
+    # the headline shape (T=10752, d_model 2048, d_ffn 6144) and its outlier variant at full size: the GPU path
+    # against the oracle (about 20-30 s of CPU and 6 GB of host memory each)
+    print(f"config {cfg} full size", flush=True)
+    _, inp, out = _run_model(cfg, None, gpu)
+    _, _, f, b = _oracle_all(inp)
+    _check_e2e(out, f, b)
+
+
 def _kernel_inputs(cfg, T, gpu):
     inp = workloads.make_inputs(cfg, T=T)
     W, (S, bg, bu, ad, bd), f, b = _oracle_all(inp)
