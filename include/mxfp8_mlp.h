@@ -202,7 +202,7 @@ int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg, const flo
  * out[t, ρ] = bf16(x[t, :] · w[ρ, :]), then bf16(out · scale) when scale != 1; x [T, K] bf16 (row stride ld_x),
  * w [rp, K] bf16, out [T, rp] bf16; outT (optional) [rp, Tpad] bf16, the same values transposed and zero for
  * t >= T.  Replaces xs = x2 @ S.t() and dxd = (dy2 @ bd).mul_(s_d) (/root/reference/scripts/fused_mlp.py:277,
- * :311-313).  K % 256 == 0, rp in {16, 32, 64}.
+ * :311-313).  K % 64 == 0, rp in {16, 32, 64}.
  */
 int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* w, int64_t rp, float scale, void* out,
                   void* outT, int64_t Tpad, void* stream);

@@ -69,7 +69,7 @@ def test_argument_checks_reject_before_launch(lib):
     # backward column group must divide N and be a multiple of 128
     args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, 0, None]
     assert lib.mxfp8_mlp_bwd(*args) == -1
-    # LoRA products: K must be a multiple of 256 (x · Wᵀ) / 128 (token reduction), rp in {16, 32, 64}
+    # LoRA products: K must be a multiple of 64 (x · Wᵀ) / 128 (token reduction), rp in {16, 32, 64}
     assert lib.mxfp8_lora_nt(p, 4, 200, 200, p, 16, 1.0, p, None, 0, None) == -1
     assert lib.mxfp8_lora_nt(p, 4, 256, 256, p, 8, 1.0, p, None, 0, None) == -1
     # fused quantizer + rank-r product: K % 128, rp in {16, 32}, Tpad = ceil(T/128)*128

@@ -46,7 +46,8 @@ def test_prep_casts_and_transposes(R, K, N, gpu):
         assert torch.equal(getattr(lw, k).cpu(), v.contiguous()), k
 
 
-@pytest.mark.parametrize("T,K,rp,scale", [(10752, 2048, 32, 1.0), (300, 1024, 16, 2.0), (77, 2048, 64, 0.75)])
+@pytest.mark.parametrize("T,K,rp,scale", [(10752, 2048, 32, 1.0), (300, 1024, 16, 2.0), (77, 2048, 64, 0.75),
+                                          (45, 384, 64, 1.0), (130, 192, 16, 2.0)])
 def test_lora_nt(T, K, rp, scale, gpu):
     g = torch.Generator().manual_seed(T + rp)
     x = torch.randn(T, K, generator=g).to(torch.bfloat16)

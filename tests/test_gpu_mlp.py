@@ -96,6 +96,24 @@ def test_mlp_end_to_end_config2_full(gpu):
     _check_e2e(out, f, b)
 
 
+_EXTRA = {
+    # rank 32 (the reference's other accepted rank): the fused kernels' R = 32 variants and the 2r = 64 products
+    61: dict(name="r32", T=1000, K=1024, N=3584, r=32, alpha=64, backward=True, layers=1),
+    # d_model and d_ffn odd multiples of 128 (the reference's gate is d_ffn % 128 == 0), at both ranks
+    62: dict(name="odd128", T=700, K=384, N=640, r=16, alpha=32, backward=True, layers=1),
+    63: dict(name="odd128_r32", T=333, K=384, N=640, r=32, alpha=64, backward=True, layers=1),
+}
+
+
+@pytest.mark.parametrize("cfg", sorted(_EXTRA))
+def test_mlp_end_to_end_other_shapes(cfg, gpu, monkeypatch):
+    monkeypatch.setitem(workloads.CONFIGS, cfg, _EXTRA[cfg])
+    print(f"shape {_EXTRA[cfg]}", flush=True)
+    _, inp, out = _run_model(cfg, None, gpu)
+    _, _, f, b = _oracle_all(inp)
+    _check_e2e(out, f, b)
+
+
 @pytest.mark.parametrize("cfg", [3, 5])
 def test_mlp_end_to_end_full_size(cfg, gpu):
     # the headline shape (T=10752, d_model 2048, d_ffn 6144) and its outlier variant at full size: the GPU path

@@ -87,8 +87,9 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
 // ----------------------------------------------------------------------------------------- x · Wᵀ (nt)
 // out[t, ρ] = bf16(X[t, :] · W[ρ, :]) (then bf16(· scale) when scale != 1), X [T, K] bf16 (row stride ldx),
 // W [RP, K] bf16; optionally outT [RP, Tpad] (zero for t >= T).  Grid: Tpad / 32 row blocks, 4 waves, wave w
-// summing a quarter of K for the block's 32 rows with the 32x32x16 MFMA (A = W rows ρ, B = X rows t, k along
-// the row); the 4 quarters are added in LDS in a fixed order.
+// summing a contiguous quarter of the K / 64 steps (w * steps / 4 up to (w + 1) * steps / 4) for the block's 32
+// rows with the 32x32x16 MFMA (A = W rows ρ, B = X rows t, k along the row); the 4 quarters are added in LDS in
+// a fixed order.
 template <int RP>
 __global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W,
                                                  int T, int Tpad, int K, float scale, uint16_t* __restrict__ out,
@@ -98,12 +99,12 @@ __global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X,
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int t = blockIdx.x * 32 + (lane & 31);
   const int tc = min(t, T - 1);
-  const int kq = K / 4, k0 = w * kq;
+  const int ns = K / 64, k0 = (w * ns / 4) * 64, k1 = ((w + 1) * ns / 4) * 64;  // wave w: a contiguous quarter
   const uint16_t* xrow = X + (int64_t)tc * ldx + lg * 8;
   v16f acc[NA];
 #pragma unroll
   for (int a = 0; a < NA; ++a) acc[a] = v16f{};
-  for (int k = k0; k < k0 + kq; k += 64) {
+  for (int k = k0; k < k1; k += 64) {
     v8bf xb[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) xb[u] = load_bf8(xrow + k + 16 * u);
@@ -725,8 +726,8 @@ extern "C" int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg
 extern "C" int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* w, int64_t rp, float scale,
                              void* out, void* outT, int64_t Tpad, void* stream) {
   MX_CHECK_ARG(x && w && out, "mxfp8_lora_nt: null pointer");
-  MX_CHECK_ARG(T > 0 && K > 0 && K % 256 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
-               "mxfp8_lora_nt: need K %% 256 == 0, rp in {16, 32, 64}");
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 64 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
+               "mxfp8_lora_nt: need K %% 64 == 0, rp in {16, 32, 64}");
   MX_CHECK_ARG(!outT || (Tpad >= T && Tpad % 32 == 0), "mxfp8_lora_nt: Tpad must be >= T and a multiple of 32");
   MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(w, 16), "mxfp8_lora_nt: misaligned buffer");
   MX_CHECK_ARG(T < (1LL << 31) && (outT ? Tpad : T) / 32 < (1LL << 31), "mxfp8_lora_nt: too many rows");

@@ -75,8 +75,8 @@ def _rp(n):
 
 def _native_ok(x2, dt, n):
     """The thin GEMMs x·Sᵀ, dSᵀ·x and dS·S run on the library's kernels (mxfp8_lora_nt / mxfp8_lora_tn / the MX
-    GEMM epilogue) when the math is bf16 on the GPU, S has at most 64 rows and d_model % 256 == 0."""
-    return (x2.is_cuda and dt == torch.bfloat16 and _rp(n) is not None and x2.shape[0] > 0 and x2.shape[1] % 256 == 0
+    GEMM epilogue) when the math is bf16 on the GPU, S has at most 64 rows and d_model % 128 == 0."""
+    return (x2.is_cuda and dt == torch.bfloat16 and _rp(n) is not None and x2.shape[0] > 0 and x2.shape[1] % 128 == 0
             and _vec_ok(x2))
 
 

@@ -285,9 +285,9 @@ def mlp(mlp_mod, x, need_out=True):
     r = Ag.shape[0]
     T = x.numel() // x.shape[-1]
     if not (_r_ok(r) and Au.shape[0] == r and Ad.shape[0] == r and x.shape[-1] == hold.w.shape[1]
-            and hold.n % 256 == 0 and x.shape[-1] % 256 == 0 and Ad.shape[1] == hold.n and T > 0
+            and hold.n % 128 == 0 and x.shape[-1] % 128 == 0 and Ad.shape[1] == hold.n and T > 0
             and T * 2 * hold.n < 2 ** 31):
-        return None  # (32-bit element indexing in the kernels; N and K tiled by 256)
+        return None  # (32-bit element indexing in the kernels; N and K in 128-wide MX tiles)
     STATS["mlp gộp"] = STATS.get("mlp gộp", 0) + 1
     ACTIVE[0] = True
     return _MLP.apply(x, (hold, db, (s_g, s_u, s_d), dt), need_out, Ag, Bg, Au, Bu, Ad, Bd)
