@@ -68,7 +68,8 @@ def test_lora_nt(T, K, rp, scale, gpu):
 
 
 @pytest.mark.parametrize("T,K,rp,scale,transpose", [(10752, 2048, 16, 2.0, True), (10752, 2048, 32, 1.0, False),
-                                                    (333, 1024, 64, 1.0, False), (31, 256, 16, 1.0, True)])
+                                                    (333, 1024, 64, 1.0, False), (31, 256, 16, 1.0, True),
+                                                    (49200, 2048, 32, 1.0, False)])  # > 192 MB: one step in flight
 def test_lora_tn(T, K, rp, scale, transpose, gpu):
     g = torch.Generator().manual_seed(T + K + rp)
     x = torch.randn(T, K, generator=g).to(torch.bfloat16)
