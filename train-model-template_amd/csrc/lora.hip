@@ -192,13 +192,19 @@ __global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restr
   const int cx = 4 * w + 2 * lg;  // the lane's first logical 16-byte chunk of a tile row
   const int sx0 = ((cx ^ (row & 15)) << 4), sx1 = (((cx + 1) ^ (row & 15)) << 4);
   v16f acc = v16f{};
-  // Stages past the end re-load the last tile into the slot just consumed (no later step reads it).  The wait
-  // leaves the DMA of the (kStages - 2) later tiles in flight (and, if stores count too, waits a little longer).
+  // Stages past the end re-load the last tile into the slot just consumed (no later step reads it).  The memory
+  // counter also counts this lane's stores (one code store and one scale store per tile), in issue order.  Behind
+  // tile t's DMAs come the (kStages - 2) later tiles' DMAs and, from step kStages - 1 on, the stores of the last
+  // kStages - 1 steps; the wait leaves exactly those in flight.  (Counting the DMAs alone made every step wait
+  // for the previous steps' stores to be acknowledged.)  The first kStages - 1 steps, with fewer stores behind
+  // their tile, wait for the DMAs alone, which covers them.
+  constexpr int kSt = 2;
 #pragma unroll
   for (int j = 0; j < kStages - 1; ++j) issue(min(j, nt - 1), j);
   int slot = 0;
   for (int t = 0; t < nt; ++t) {
-    wait_vmcnt<(kStages - 2) * kDma>();
+    if (t < kStages - 1) wait_vmcnt<(kStages - 2) * kDma>();
+    else wait_vmcnt<(kStages - 2) * kDma + (kStages - 1) * kSt>();
     __builtin_amdgcn_s_barrier();  // every wave's DMA of tile t landed; every wave is done with tile t - 1's slot
     issue(min(t + kStages - 1, nt - 1), slot == 0 ? kStages - 1 : slot - 1);
     const uint8_t* st = lds + slot * kStageB;
