@@ -149,6 +149,16 @@ def test_group_qkv_thin_matches_oracle(fused, gpu):
     assert mxfp8.group_wt([a.k_proj.base_layer, a.q_proj.base_layer]) is None
 
 
+def test_group_odd_multiples_of_128(gpu, monkeypatch):
+    # d_model 384 and a q width of 640 (odd multiples of 128): the thin products (lora_nt / lora_tn), the grouped
+    # GEMMs and their segment boundaries away from multiples of 256
+    import sys
+    here = sys.modules[__name__]
+    monkeypatch.setattr(here, "K", 384)
+    monkeypatch.setattr(here, "NQ", 640)
+    test_group_qkv_thin_matches_oracle(True, gpu)
+
+
 def test_cat_ranges_are_the_layers_own_quantization(gpu):
     # a column range of the concatenated Wᵀ (codes and cut-out scales) equals quantizing that layer's Wᵀ alone
     import mxfp8
