@@ -352,7 +352,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the MLP shards by tokens with "
-              "one LoRA-gradient all-reduce per layer; see DESIGN.md).", file=sys.stderr)
+              "one LoRA-gradient all-reduce per layer).", file=sys.stderr)
         sys.exit(2)
 
     import torch
