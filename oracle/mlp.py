@@ -13,6 +13,11 @@ A PyTorch-CPU restatement of the reference path with every bf16 rounding point o
   - LoRA bf16 products   cuBLAS bf16 GEMMs with fp32 accumulation (train.py:54 disables reduced-precision
                           reduction), restated as fp32 matmul -> bf16
 fp32 summation order and transcendental ulps differ from the GPU; tests state their tolerances.
+
+Pinned by tests/test_oracle_mlp.py without sharing this file's code: lossless MX inputs against an independent
+float64 composition (stage by stage and end to end), torch.autograd and float64 central differences of the exact
+MLP for every gradient, exact-zero reductions (LoRA scalings 0, LoRA B = 0), the bf16 rounding point of every
+rounded backward tensor, and mutants of this file that those checks must reject.
 """
 import torch
 
