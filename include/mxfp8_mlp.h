@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 5
+#define MXFP8_MLP_ABI_VERSION 6
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -254,6 +254,14 @@ int64_t mxfp8_lora_bwd_chunks(int64_t T, int64_t N);
 int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q, int64_t ld_q, void* s,
                    int64_t s_col_tiles, int64_t col_tile_off, const void* xa, int64_t ld_xa, const void* b, int64_t r,
                    float scale, void* dxa, int64_t ld_dxa, float* db, float* part_dxa, float* part_db, void* stream);
+
+/*
+ * out [C, Tpad] bf16 = xᵀ of x [T, C] bf16 (row stride ld_x, 16-byte aligned rows), zero in columns T..Tpad-1.
+ * No counterpart in the reference, which saves xs = x·Sᵀ for the backward (/root/reference/scripts/
+ * fused_mlp.py:291) and reads it row-wise: here the backward kernel takes xsᵀ as a matrix-instruction operand,
+ * so the backward rebuilds it from the saved xs.  C in {16, 32, 64}.
+ */
+int mxfp8_transpose_pad(const void* x, int64_t T, int64_t C, int64_t ld_x, void* out, int64_t Tpad, void* stream);
 
 /* Token chunks mxfp8_lora_tn uses for [T, K] (its partial buffer holds chunks * rp * K floats). */
 int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);

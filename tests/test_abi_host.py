@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 25, names
+    assert len(names) == 26, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -55,6 +55,9 @@ def test_argument_checks_reject_before_launch(lib):
     assert b"cols" in lib.mxfp8_last_error()
     # null pointer
     assert lib.mxfp8_quant_rows(None, 4, 128, 128, p, 128, p, 1, 0, None) == -1
+    # transpose: C outside {16, 32, 64}, padded length below T
+    assert lib.mxfp8_transpose_pad(p, 8, 24, 24, p, 128, None) == -1
+    assert lib.mxfp8_transpose_pad(p, 200, 32, 32, p, 128, None) == -1
     # GEMM K not a multiple of 128
     assert lib.mxfp8_gemm_nt(p, p, 96, p, p, 96, 4, 128, 96, p, 128, None, 0, None, 0, 0, 1.0, 0, None, 0, None) == -1
     # GEMM epilogue rank not supported

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT = 1, 2, 4, 8  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -40,6 +40,7 @@ SIGNATURES = {
     "mxfp8_lora_nt": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_res_lora": [_ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _f32, _ptr, _ptr],
+    "mxfp8_transpose_pad": [_ptr, _i64, _i64, _i64, _ptr, _i64],
     "mxfp8_lora_tn_chunks": [_i64, _i64],
     "mxfp8_swiglu": [_ptr, _ptr, _i64, _ptr, _ptr],
     "mxfp8_swiglu_bwd": [_ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr],
@@ -269,6 +270,12 @@ def lora_tn(x, p, out, part, scale=1.0, transpose=False):
     chunks = part.numel() // (rp * K)
     call("mxfp8_lora_tn", _p(x), T, K, x.stride(0), _p(p), rp, chunks, _p(part), float(scale), int(transpose),
          int(out.dtype == torch.float32), _p(out), like=x)
+
+
+def transpose_pad(x, out):
+    """out [C, Tpad] = xᵀ of x [T, C] bf16, zero past T."""
+    T, C = x.shape
+    call("mxfp8_transpose_pad", _p(x), T, C, x.stride(0), _p(out), out.shape[1], like=x)
 
 
 def lora_tn_chunks(T, K):

@@ -84,6 +84,24 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
   }
 }
 
+// ------------------------------------------------------------------------------------------ transpose
+// out[c, t] = x[t, c] for t < T and 0 for T <= t < Tpad; x [T, C] bf16 (row stride ldx, 16-byte aligned rows),
+// out [C, Tpad].  One thread per token: it reads its row as C / 8 16-byte pieces and writes one element of each
+// output row, so a wave's stores are 64 consecutive tokens (128 B) of one output row.
+template <int C>
+__global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __restrict__ x, int64_t ldx, int T,
+                                                            int Tpad, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= Tpad) return;
+  uint4 v[C / 8];
+  const uint4* row = reinterpret_cast<const uint4*>(x + (int64_t)min(t, T - 1) * ldx);
+#pragma unroll
+  for (int j = 0; j < C / 8; ++j) v[j] = t < T ? row[j] : make_uint4(0, 0, 0, 0);
+  const uint16_t* e = reinterpret_cast<const uint16_t*>(v);
+#pragma unroll
+  for (int c = 0; c < C; ++c) out[(int64_t)c * Tpad + t] = e[c];
+}
+
 // ----------------------------------------------------------------------------------------- x · Wᵀ (nt)
 // out[t, ρ] = bf16(X[t, :] · W[ρ, :]) (then bf16(· scale) when scale != 1), X [T, K] bf16 (row stride ldx),
 // W [RP, K] bf16; optionally outT [RP, Tpad] (zero for t >= T).  Grid: Tpad / 32 row blocks, 4 waves, wave w
@@ -726,6 +744,23 @@ extern "C" int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg
              (uint16_t*)buT, (uint16_t*)ad, (uint16_t*)adT, (uint16_t*)bd, (uint16_t*)bdT, (int)R, (int)K, (int)N};
   prep_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total);
   MX_CHECK_LAUNCH("mxfp8_lora_prep");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_transpose_pad(const void* x, int64_t T, int64_t C, int64_t ld_x, void* out, int64_t Tpad,
+                                   void* stream) {
+  MX_CHECK_ARG(x && out, "mxfp8_transpose_pad: null pointer");
+  MX_CHECK_ARG(T > 0 && Tpad >= T && Tpad < (1LL << 31) && (C == 16 || C == 32 || C == 64) && ld_x >= C &&
+                   ld_x % 8 == 0 && mx_aligned(x, 16) && mx_aligned(out, 2),
+               "mxfp8_transpose_pad: need C in {16, 32, 64}, Tpad >= T, 16-byte aligned rows of x");
+  dim3 grid((unsigned)((Tpad + 255) / 256));
+  hipStream_t stm = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  uint16_t* op = (uint16_t*)out;
+  if (C == 16) transpose_pad_kernel<16><<<grid, 256, 0, stm>>>(xp, ld_x, (int)T, (int)Tpad, op);
+  else if (C == 32) transpose_pad_kernel<32><<<grid, 256, 0, stm>>>(xp, ld_x, (int)T, (int)Tpad, op);
+  else transpose_pad_kernel<64><<<grid, 256, 0, stm>>>(xp, ld_x, (int)T, (int)Tpad, op);
+  MX_CHECK_LAUNCH("mxfp8_transpose_pad");
   return MXFP8_OK;
 }
 

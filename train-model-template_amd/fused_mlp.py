@@ -13,8 +13,9 @@ mlp_fwd, mlp_bwd), same saved-tensor set, same return dtypes and the same None f
             dh += dxd·A_d; SwiGLU backward; MX(dg | du) into one [T, 2N] buffer; dxa, dB, dA_d partials ->
             one K = 2N MX GEMM dx = [dg | du]·W_gu with the LoRA epilogue dx = bf16(dx + dxa·S).
   need_out=False (checkpoint recompute): only xs, MX(x) and the gate|up GEMM run (fused_mlp.py:286-288).
-The heavy kernels are hand-written HIP (libmxfp8_mlp.so, _native.py); the rank-r LoRA products that are plain
-skinny GEMMs (xs, dxd, dB_d, dA) use PyTorch's bf16 GEMM on the same stream.
+Every kernel of the path is hand-written HIP (libmxfp8_mlp.so, _native.py): the rank-r LoRA products come from
+the quantizer (xs with MX(x), dxd with MX(dy)), the GEMM epilogues (y, dx) and the token-reduction kernel
+(dB_d, dA); no BLAS or elementwise torch kernel runs inside a step.
 """
 import types
 
@@ -122,8 +123,9 @@ def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u
 
 
 def _transposed_padded(t, tpad):
-    out = torch.zeros((t.shape[1], tpad), dtype=t.dtype, device=t.device)
-    out[:, :t.shape[0]] = t.t()
+    """[C, tpad] = tᵀ of t [T, C] bf16, zero past T (mxfp8_transpose_pad)."""
+    out = torch.empty((t.shape[1], tpad), dtype=t.dtype, device=t.device)
+    _native.transpose_pad(t, out)
     return out
 
 
@@ -168,6 +170,26 @@ def _prep(Ag, Bg, Au, Bu, Ad, Bd, dt):
     return _cast((("lora_prep", id(Ag), id(Au), id(Bg), id(Bu), id(Ad), id(Bd)), dt), make)
 
 
+def _forms_key(S, bg, bu, ad, bd, dt):
+    return (("lora_forms", id(S), id(bg), id(bu), id(ad), id(bd)), dt)
+
+
+def _forms_of_saved(S, bg, bu, ad, bd, dt):
+    """The step's bf16 weight forms (_prep) looked up from the five tensors _MLP saves.  The forward registers
+    them under the ids of those tensors; when the saved tensors come back as other objects (a saved-tensor
+    hook, e.g. checkpointing) or the cache was cleared, the transposed forms are rebuilt from the saved ones."""
+    def make():
+        R = ad.shape[0]
+        f = lambda t: t.float().contiguous()  # noqa: E731
+        K, N = S.shape[1], bg.shape[0]
+        e = lambda *sh: torch.empty(sh, dtype=torch.bfloat16, device=S.device)  # noqa: E731
+        out = dict(S=e(2 * R, K), ST=e(K, 2 * R), bg=e(N, R), bu=e(N, R), bgT=e(R, N), buT=e(R, N), ad=e(R, N),
+                   adT=e(N, R), bd=e(K, R), bdT=e(R, K))
+        _native.lora_prep(f(S[:R]), f(S[R:]), f(bg), f(bu), f(ad), f(bd), out)
+        return types.SimpleNamespace(**out)
+    return _cast(_forms_key(S, bg, bu, ad, bd, dt), make)
+
+
 # GEMM layout of the MLP's own products: both operands MX-tiled, output in the fused-tile layout
 _LAYOUT_FT = _native.GEMM_A_TILED | _native.GEMM_B_TILED | _native.GEMM_C_FT
 
@@ -190,11 +212,10 @@ class _MLP(torch.autograd.Function):
         # mx_quant) and xs = bf16(x2 · Sᵀ) [T, 2R] = xa_gate | xa_up, with the zero-padded transpose the backward
         # kernel reads
         if 2 * R <= 32:
-            q, sc, xs, xsT = mxfp8.mx_quant_lora(x2, S)
+            q, sc, xs, _ = mxfp8.mx_quant_lora(x2, S, out_t=False)
         else:
             xs = torch.empty((T, 2 * R), dtype=dt, device=x2.device)
-            xsT = torch.empty((2 * R, _cdiv(T, 128) * 128), dtype=dt, device=x2.device)
-            _native.lora_nt(x2, S, xs, outT=xsT)
+            _native.lora_nt(x2, S, xs)
             q, sc = mxfp8.mx_quant_tiled(x2)
         # gu = gate | up [T, 2N] in the fused-tile layout the fused kernels read (32 x 32 blocks of 2 KB)
         gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=_LAYOUT_FT, m=T)
@@ -207,10 +228,11 @@ class _MLP(torch.autograd.Function):
         else:  # graph only (checkpoint recompute / prefix backward): nobody reads y
             STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
             y = x2.new_empty(x2.shape[0], down.out_features)
-        # the same saved set in both modes (non-reentrant checkpointing compares metadata on recompute)
+        # the reference's saved set, the same in both modes (non-reentrant checkpointing compares metadata on
+        # recompute); the transposed weight forms stay in the per-step cast cache, keyed by these tensors
+        _cast(_forms_key(S, bg, bu, ad, bd, dt), lambda: lw)
         ctx.save_for_backward(x2, xs, gu, S, bg, bu, ad, bd)
         ctx.meta = (hold, down, (s_g, s_u, s_d), dt, lead, K, x.dtype)
-        ctx.lw, ctx.xsT = lw, xsT  # the other weight forms and xsᵀ (small; not part of the reference's saved set)
         return y.view(*lead, y.shape[-1])
 
     @staticmethod
@@ -225,7 +247,8 @@ class _MLP(torch.autograd.Function):
         if not dy2.is_contiguous():
             dy2 = dy2.contiguous()
         T, N = dy2.shape[0], hold.n
-        lw, xsT = ctx.lw, ctx.xsT
+        lw = _forms_of_saved(S, bg, bu, ad, bd, dt)
+        xsT = _transposed_padded(xs, _cdiv(T, 128) * 128)  # the backward kernel's operand form of xs
         # one read of dy2: its MX operand and dxd = bf16(bf16(dy2 · bd) · s_d) [T, R] with its zero-padded transpose
         qd, sd, dxd, dxdT = mxfp8.mx_quant_lora(dy2, lw.bdT, scale=s_d)
         dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)  # MX(dy) · W_down, FT
@@ -241,9 +264,9 @@ class _MLP(torch.autograd.Function):
         dA_d = torch.empty((R, N), dtype=torch.float32, device=dy2.device)
         _native.mlp_bwd_finish(*parts, T, N, R, s_g, s_u, dxa, xsd, dB_g, dB_u, dA_d)
         del parts
-        # the token reductions (fp32 tensors holding the bf16 results the reference's bf16 GEMMs return)
+        # the token reductions, bf16 as the reference's bf16 GEMMs return them (fused_mlp.py:316-318, :333)
         part = torch.empty(_native.lora_tn_chunks(T, K) * 2 * R * K, dtype=torch.float32, device=dy2.device)
-        dB_d = torch.empty((K, R), dtype=torch.float32, device=dy2.device)
+        dB_d = torch.empty((K, R), dtype=dt, device=dy2.device)
         _native.lora_tn(dy2, xsd, dB_d, part[:part.numel() // 2], scale=s_d, transpose=True)  # bf16(bf16(dyᵀ xsd) s_d)
         dx = None
         if need_x:
@@ -252,7 +275,7 @@ class _MLP(torch.autograd.Function):
             dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
-        dA = torch.empty((2 * R, K), dtype=torch.float32, device=dy2.device)
+        dA = torch.empty((2 * R, K), dtype=dt, device=dy2.device)
         _native.lora_tn(x2, dxa, dA, part)  # bf16(dxaᵀ · x2)
         grads = [dA[:R], dB_g, dA[R:], dB_u, dA_d, dB_d]
         ws_in = ctx.needs_input_grad[3:]
