@@ -23,3 +23,13 @@ def gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _fresh_cast_cache():
+    """Each test starts a new 'training step': the per-step bf16 cast cache of fused_linear is keyed by id() of the
+    parameters (fused_linear.py:55-69), so entries left by an earlier test could alias a new tensor at a recycled
+    address.  The training loop clears it with new_step() at every step; so do the tests."""
+    import fused_linear
+    fused_linear.new_step()
+    yield

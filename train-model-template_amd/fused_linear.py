@@ -1,26 +1,33 @@
 """Linear layers that share one input (q/k/v; qkv/z/b/a of a DeltaNet block; o_proj / out_proj) computed in ONE
-autograd.Function, after /root/reference/scripts/fused_linear.py.
+autograd.Function: the drop-in for /root/reference/scripts/fused_linear.py (group_linear, residual_add, Deferred,
+_part, _cast, new_step, STATS).
 
-  - x is read once for every LoRA A of the group (and the weights of thin frozen linears, <= _THIN outputs): one
-    GEMM x·Sᵀ with S the concatenated rows;
-  - MX base layers share one quantization of x; the LoRA-B product rides in the MX GEMM's epilogue;
-  - backward over MX layers (mxfp8.FUSED_BWD): each dy is read once by mxfp8.lora_bwd (MX codes into one buffer
-    concatenated along the group's N, d(xa), dB), and dx of the group is ONE MX GEMM against the concatenated Wᵀ;
+A group is described once per call by a _Spec: which layers are MX, which carry a LoRA adapter, which are thin
+frozen linears (<= _THIN outputs), and where each one's columns sit in the thin product xS = x·Sᵀ.  S stacks the
+LoRA A rows of the adapter layers in layer order, then the thin linears' weights; the gradient layout of dS
+follows the same columns.  On that layout:
+  - forward reads x once for every A (and thin weight), quantizes x once for every MX layer, and puts each LoRA-B
+    product in the MX GEMM's epilogue; consecutive layers of a concatenated group (mxfp8._CATS) run as one GEMM;
+  - backward over MX layers (mxfp8.FUSED_BWD) reads each dy once (mxfp8.lora_bwd: MX codes into one buffer
+    concatenated along the group's N, d(xa), dB) and computes dx of the group as ONE MX GEMM against the
+    concatenated Wᵀ, with dS·S in its epilogue; other groups take the per-layer backward;
   - o_proj / out_proj may return a Deferred output (LoRA not yet added) that residual_add adds inside the residual
     kernel (mxfp8.res_lora).
-Layers that cannot take this path (trainable base weights, DoRA, dropout > 0, several adapters) are called one by
-one.  `_part`, `_cast` / `new_step` and `STATS` are also what the fused MLP path reads.
+Layers that cannot be grouped (trainable base weights, DoRA, dropout > 0, several adapters) are called one by one.
+`_part`, `_cast` / `new_step` and `STATS` are also what the fused MLP path reads.
 """
+import dataclasses
+
 import torch
 from torch import nn
 
-_THIN = 64  # a plain frozen Linear with at most this many outputs joins the S GEMM (in_proj_b/a: 16)
-STATS = {"gộp": 0, "gọi thẳng": 0}  # path counters, same keys as the reference (fused / called directly)
+_THIN = 64  # a plain frozen Linear with at most this many outputs joins the thin product (in_proj_b/a: 16)
+STATS = {"gộp": 0, "gọi thẳng": 0}  # path counters, the reference's keys (grouped / called directly)
 
 
 def _part(m):
     """(base Linear, A, B, scaling) of a PEFT LoRA Linear; (m, None, None, 1.0) for a plain frozen Linear;
-    None if the layer cannot take the fused path (fused_linear.py:30-48)."""
+    None if the layer cannot be grouped (fused_linear.py:30-48)."""
     base = getattr(m, "base_layer", None)
     if base is None:
         if type(m) is nn.Linear and m.bias is None and not m.weight.requires_grad:
@@ -60,6 +67,57 @@ def _mx(base):
     return getattr(base, "_mx_w", None) is not None
 
 
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+# ------------------------------------------------------------------------------------------- layout
+@dataclasses.dataclass(frozen=True)
+class _Slot:
+    """Columns [col, col + width) of xS = x·Sᵀ that belong to layer `layer`: the rows of its LoRA A (an adapter,
+    `index`-th of the group, scaled by `scale`) or the whole output of a thin frozen linear."""
+    layer: int
+    col: int
+    width: int
+    index: int = -1
+    scale: float = 1.0
+
+    @property
+    def cols(self):
+        return slice(self.col, self.col + self.width)
+
+
+class _Spec:
+    """The layout of one group (see the module docstring)."""
+
+    def __init__(self, parts):
+        self.parts = parts
+        self.adapters, self.thin = [], []
+        col = 0
+        for i, (base, A, B, s) in enumerate(parts):
+            if A is not None:
+                self.adapters.append(_Slot(i, col, A.shape[0], len(self.adapters), s))
+                col += A.shape[0]
+        for i, (base, A, B, s) in enumerate(parts):
+            if A is None and not _mx(base) and base.weight.shape[0] <= _THIN:
+                self.thin.append(_Slot(i, col, base.weight.shape[0]))
+                col += base.weight.shape[0]
+        self.width = col
+        self.adapter_cols = sum(sl.width for sl in self.adapters)
+        self.thin_ids = frozenset(sl.layer for sl in self.thin)
+        self._adapter = {sl.layer: sl for sl in self.adapters}
+        self.mx = [i for i, p in enumerate(parts) if _mx(p[0])]
+        self.plain = [i for i, p in enumerate(parts) if not _mx(p[0]) and i not in self.thin_ids]
+
+    def adapter(self, i):
+        return self._adapter.get(i)
+
+    def s_sources(self):
+        """The tensors whose rows make S, in column order."""
+        return [self.parts[sl.layer][1] for sl in self.adapters] + [self.parts[sl.layer][0].weight for sl in self.thin]
+
+
+# ------------------------------------------------------------------------------------------- native helpers
 def _vec_ok(t):
     """A bf16 [rows, r] view the native kernels read with 16-byte loads: row stride % 8, 16-byte aligned."""
     return t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
@@ -67,10 +125,7 @@ def _vec_ok(t):
 
 def _rp(n):
     """Padded row count of S / column count of dS for the native rank-r kernels (16, 32 or 64), None above 64."""
-    for rp in (16, 32, 64):
-        if n <= rp:
-            return rp
-    return None
+    return next((rp for rp in (16, 32, 64) if n <= rp), None)
 
 
 def _native_ok(x2, dt, n):
@@ -85,53 +140,95 @@ def _s_pad(S, key, rp):
     return _cast(key + ("pad", rp), lambda: torch.cat([S, S.new_zeros(rp - S.shape[0], S.shape[1])]))
 
 
-def _base_mm(base, x2, dt, q, T):
-    """x2 @ Wᵀ of a base weight: the MX GEMM when enable_mxfp8 covers the layer (q = the group's tiled MX codes of
-    x2), else a bf16 GEMM (fused_linear.py:72-76)."""
-    if _mx(base):
-        import mxfp8
-        tl = getattr(base, "_mx_w_tl", None)
-        if tl is not None:
-            return mxfp8.mx_mm(q[0], q[1], tl, base._mx_ws, layout=3, m=T)
-        return mxfp8.mx_mm(q[0], q[1], base._mx_w, base._mx_ws, layout=1, m=T)
-    return x2 @ base.weight.to(dt).t()
+def _thin_product(x2, S, skey, width, dt):
+    """bf16(x2 · Sᵀ): one read of x2 on the library's rank-r kernel (S zero-padded to 16/32/64 rows, so xS has
+    zero columns past `width`) when it applies, else a torch GEMM."""
+    if not _native_ok(x2, dt, width):
+        return x2 @ S.t()
+    import _native
+    rp = _rp(width)
+    xS = torch.empty((x2.shape[0], rp), dtype=dt, device=x2.device)
+    _native.lora_nt(x2, _s_pad(S, skey, rp), xS)
+    return xS
 
 
-def _fwd_merged(parts, lora, Bs, xS, q, T, dt, skey):
-    """Outputs of the group's MX layers from ONE GEMM over their concatenated forward weight (a consecutive range of
-    one mxfp8._CATS group), each written to its own contiguous tensor, with every layer's LoRA-B product in the
-    epilogue: P = xS (the padded x·Sᵀ), Q = the layers' B placed block-diagonally at their S columns (zeros adding
-    nothing), one alpha.  Same bits as one GEMM per layer.  None when the layers do not qualify (not a cat range,
-    LoRA scalings that differ, xS not in the padded native form)."""
+def _mx_out(base, codes, T, lora=None, alpha=1.0):
+    """MX GEMM of one layer from the group's tiled codes of x (its MX-tiled weight copy when it has one)."""
     import mxfp8
-    mxi = [i for i, p in enumerate(parts) if _mx(p[0])]
-    if len(mxi) < 2 or xS is None or not _vec_ok(xS) or xS.shape[1] not in (16, 32, 64):
+    tl = getattr(base, "_mx_w_tl", None)
+    w, layout = (tl, 3) if tl is not None else (base._mx_w, 1)
+    return mxfp8.mx_mm(codes[0], codes[1], w, base._mx_ws, lora=lora, alpha=alpha, layout=layout, m=T)
+
+
+def _base_mm(base, x2, dt, codes, T):
+    """x2 · Wᵀ of a base weight: the MX GEMM when enable_mxfp8 covers the layer, else a bf16 GEMM
+    (fused_linear.py:72-76)."""
+    return _mx_out(base, codes, T) if _mx(base) else x2 @ base.weight.to(dt).t()
+
+
+# ------------------------------------------------------------------------------------------- forward
+def _fwd_merged(spec, Bs, xS, codes, T, dt, skey):
+    """The outputs of the group's MX layers from ONE GEMM over their concatenated forward weight (a consecutive
+    range of one mxfp8._CATS group), each written to its own contiguous tensor, with every layer's LoRA-B
+    product in the epilogue: P = xS, Q = the layers' B placed block-diagonally at their S columns (zeros add
+    nothing), one alpha.  Same bits as one GEMM per layer.  None when the layers do not qualify (not a cat
+    range, LoRA scalings that differ, xS not in the padded native form)."""
+    import mxfp8
+    if len(spec.mx) < 2 or xS is None or not _vec_ok(xS) or xS.shape[1] not in (16, 32, 64):
         return None
-    op = mxfp8.group_fwd_operand([parts[i][0] for i in mxi])
+    op = mxfp8.group_fwd_operand([spec.parts[i][0] for i in spec.mx])
     if op is None:
         return None
-    lora_of = {i: (j, o, r, s) for j, (i, o, r, s) in enumerate(lora)}
-    scales = {lora_of[i][3] for i in mxi if i in lora_of}
+    slots = [spec.adapter(i) for i in spec.mx]
+    scales = {sl.scale for sl in slots if sl is not None}
     if len(scales) > 1:
         return None
     alpha = scales.pop() if scales else 1.0
+    widths = [spec.parts[i][0].out_features for i in spec.mx]
     rp = xS.shape[1]
-    widths = [parts[i][0].out_features for i in mxi]
 
-    def qcat():
+    def block_diagonal_b():
         Q = torch.zeros((sum(widths), rp), dtype=dt, device=xS.device)
-        r0 = 0
-        for i, n in zip(mxi, widths):
-            if i in lora_of:
-                j, o, r, s = lora_of[i]
-                Q[r0:r0 + n, o:o + r] = Bs[j]
-            r0 += n
+        row = 0
+        for sl, n in zip(slots, widths):
+            if sl is not None:
+                Q[row:row + n, sl.cols] = Bs[sl.index]
+            row += n
         return Q
 
-    Q = _cast(skey + ("qcat", tuple(mxi), rp), qcat)
+    Q = _cast(skey + ("qcat", tuple(spec.mx), rp), block_diagonal_b)
     outs = [torch.empty((T, n), dtype=dt, device=xS.device) for n in widths]
-    mxfp8.mx_mm_seg(q[0], q[1], op[0], op[1], outs, lora=(xS, Q), alpha=alpha, layout=3, m=T)
-    return dict(zip(mxi, outs))
+    mxfp8.mx_mm_seg(codes[0], codes[1], op[0], op[1], outs, lora=(xS, Q), alpha=alpha, layout=3, m=T)
+    return dict(zip(spec.mx, outs))
+
+
+def _forward_outputs(spec, x2, xS, Bs, skey, defer, dt):
+    """Every non-thin output of the group (fused_linear.py:104-117)."""
+    T = x2.shape[0]
+    outs = [None] * len(spec.parts)
+    codes = None
+    if spec.mx and T:
+        import mxfp8
+        codes = mxfp8.mx_quant_tiled(x2)  # once for the whole group
+        if defer is None and dt == torch.bfloat16:
+            for i, y in (_fwd_merged(spec, Bs, xS, codes, T, dt, skey) or {}).items():
+                outs[i] = y
+    for i, (base, A, B, s) in enumerate(spec.parts):
+        if outs[i] is not None or i in spec.thin_ids:
+            continue
+        sl = spec.adapter(i)
+        on_mx_bf16 = sl is not None and _mx(base) and dt == torch.bfloat16 and T > 0
+        if on_mx_bf16 and defer is not None:  # residual_add adds the LoRA part later
+            defer[i] = (xS[:, sl.cols], Bs[sl.index], sl.scale)
+            outs[i] = _mx_out(base, codes, T)
+        elif on_mx_bf16 and sl.width in (16, 32, 64) and _vec_ok(xS[:, sl.cols]):
+            # bf16(bf16(x·Wᵀ) + s · xa·Bᵀ) in the GEMM epilogue: the reference's addmm_
+            outs[i] = _mx_out(base, codes, T, lora=(xS[:, sl.cols], Bs[sl.index]), alpha=sl.scale)
+        else:
+            outs[i] = _base_mm(base, x2, dt, codes, T) if T else x2.new_empty(0, base.out_features)
+            if sl is not None:
+                outs[i].addmm_(xS[:, sl.cols], Bs[sl.index].t(), alpha=sl.scale)
+    return outs
 
 
 class _Group(torch.autograd.Function):
@@ -145,301 +242,243 @@ class _Group(torch.autograd.Function):
         x2 = x.reshape(-1, K)
         if x2.dtype != dt or not x2.is_contiguous():
             x2 = x2.to(dt).contiguous()
-        T = x2.shape[0]
-        # rows of the thin matrix S: the A of every LoRA layer (in order), then the weights of thin plain linears
-        rows, Bs, lora, thin = [], [], [], []
-        off = 0
-        for i, (base, A, B, s) in enumerate(parts):
-            if A is not None:
-                rows.append(A)
-                Bs.append(_cast((id(B), dt), lambda B=B: B.detach().to(dt)))
-                lora.append((i, off, A.shape[0], s))
-                off += A.shape[0]
-        for i, (base, A, B, s) in enumerate(parts):
-            if A is None and not _mx(base) and base.weight.shape[0] <= _THIN:
-                rows.append(base.weight)
-                thin.append((i, off, base.weight.shape[0]))
-                off += base.weight.shape[0]
-        skey = (tuple(id(r) for r in rows), dt)
-        S = _cast(skey, lambda: torch.cat([r.detach().to(dt) for r in rows])) if rows else None
-        xS = None
-        if rows and _native_ok(x2, dt, off):
-            # bf16(x·Sᵀ) from one read of x (the extra columns of the padded product are zero)
-            import _native
-            rp = _rp(off)
-            xS = torch.empty((T, rp), dtype=dt, device=x2.device)
-            _native.lora_nt(x2, _s_pad(S, skey, rp), xS)
-        elif rows:
-            xS = x2 @ S.t()
-        outs = [None] * len(parts)
-        thin_ids = {i for i, _, _ in thin}
-        lora_of = {i: (j, o, r, s) for j, (i, o, r, s) in enumerate(lora)}
+        spec = _Spec(parts)
+        Bs = [_cast((id(parts[sl.layer][2]), dt), lambda B=parts[sl.layer][2]: B.detach().to(dt))
+              for sl in spec.adapters]
+        src = spec.s_sources()
+        skey = (tuple(id(t) for t in src), dt)
+        S = _cast(skey, lambda: torch.cat([t.detach().to(dt) for t in src])) if src else None
+        xS = _thin_product(x2, S, skey, spec.width, dt) if src else None
         if need_out:
-            q = None
-            if any(_mx(p[0]) for p in parts) and T:
-                import mxfp8
-                q = mxfp8.mx_quant_tiled(x2)  # once for the whole group
-            merged = _fwd_merged(parts, lora, Bs, xS, q, T, dt, skey) if (
-                q is not None and defer is None and dt == torch.bfloat16) else None
-            if merged:
-                for i, y in merged.items():
-                    outs[i] = y
-            for i, (base, A, B, s) in enumerate(parts):
-                if i in thin_ids or (merged and i in merged):
-                    continue
-                if i in lora_of and _mx(base) and dt == torch.bfloat16 and T:
-                    j, o, r, s = lora_of[i]
-                    if defer is not None:
-                        defer[i] = (xS[:, o:o + r], Bs[j], s)  # residual_add adds the LoRA part
-                    elif r in (16, 32, 64) and _vec_ok(xS[:, o:o + r]):
-                        # bf16(bf16(x·Wᵀ) + s · xa·Bᵀ) in the GEMM epilogue: the addmm_ of the reference
-                        import mxfp8
-                        tl = getattr(base, "_mx_w_tl", None)
-                        w, lay = (tl, 3) if tl is not None else (base._mx_w, 1)
-                        outs[i] = mxfp8.mx_mm(q[0], q[1], w, base._mx_ws, lora=(xS[:, o:o + r], Bs[j]), alpha=s,
-                                              layout=lay, m=T)
-                        continue
-                outs[i] = _base_mm(base, x2, dt, q, T) if T else x2.new_empty(0, base.out_features)
-                if i in lora_of and (defer is None or i not in defer):
-                    j, o, r, s = lora_of[i]
-                    outs[i].addmm_(xS[:, o:o + r], Bs[j].t(), alpha=s)
+            outs = _forward_outputs(spec, x2, xS, Bs, skey, defer, dt)
         else:  # only the graph for backward is needed (x2, xS saved); nobody reads the outputs
             STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
-            for i, (base, A, B, s) in enumerate(parts):
-                if i not in thin_ids:
-                    outs[i] = x2.new_empty(x2.shape[0], base.out_features)
-        for i, o, n in thin:
-            outs[i] = xS[:, o:o + n].contiguous()
+            outs = [None if i in spec.thin_ids else x2.new_empty(x2.shape[0], p[0].out_features)
+                    for i, p in enumerate(parts)]
+        for sl in spec.thin:
+            outs[sl.layer] = xS[:, sl.cols].contiguous()
         ctx.save_for_backward(x2, xS, S, *Bs)
-        ctx.meta = (parts, lora, thin, lead, K, dt, x.dtype)
-        ctx.skey = skey
+        ctx.spec, ctx.skey, ctx.meta = spec, skey, (lead, K, dt, x.dtype)
         return tuple(y.view(*lead, y.shape[-1]) for y in outs)
 
     @staticmethod
     def backward(ctx, *dys):
         x2, xS, S, *Bs = ctx.saved_tensors
-        parts, lora, thin, lead, K, dt, xdt = ctx.meta
+        spec, (lead, K, dt, xdt) = ctx.spec, ctx.meta
         need_x = ctx.needs_input_grad[0]
         flat = [None if dy is None else dy.reshape(-1, dy.shape[-1]).to(dt) for dy in dys]
-        plan = _fused_bwd_plan(parts, flat, dt, need_x)
+        plan = _fused_bwd_plan(spec, flat, dt, need_x)
         if plan is not None:
-            return _fused_backward(ctx, x2, xS, S, Bs, flat, plan, need_x)
-        dx = None
-        if need_x:
-            thin_ids = {i for i, _, _ in thin}
-            for i, (base, A, B, s) in enumerate(parts):
-                dy = flat[i]
-                if dy is None or i in thin_ids:
-                    continue
-                if _mx(base):
-                    import mxfp8
-                    d = dy if dy.is_contiguous() else dy.contiguous()
-                    qd, sd = mxfp8.mx_quant(d)
-                    wt, wts = mxfp8.mx_wt(base)
-                    g = mxfp8.mx_mm(qd, sd, wt, wts)
-                    dx = g if dx is None else dx.add_(g)
-                else:
-                    w = base.weight.to(dt)
-                    dx = dy @ w if dx is None else dx.addmm_(dy, w)
-        # thin branches: columns of d(xS) for the LoRA layers (s · dy @ B) and thin linears (dy itself), with the
-        # matching rows of S
-        blocks, srows, grads = [], [], [None] * (2 * len(lora))
-        act_lora = []
-        for j, (i, o, r, s) in enumerate(lora):
-            dy = flat[i]
-            if dy is None:
-                continue
-            xa = xS[:, o:o + r]
-            dB = dy.t() @ xa
-            dxa = dy @ Bs[j]
-            if s != 1:
-                dB.mul_(s)
-                dxa.mul_(s)
-            grads[2 * j + 1] = dB
-            blocks.append(dxa)
-            srows.append((o, r))
-            act_lora.append(j)
-        n_act = sum(r for _, r in srows)
-        if need_x:
-            for i, o, n in thin:
-                if flat[i] is not None:
-                    blocks.append(flat[i])
-                    srows.append((o, n))
-        if blocks:
-            dS = torch.cat(blocks, 1) if len(blocks) > 1 else blocks[0]
-            if need_x:
-                full = len(srows) == len(lora) + len(thin)  # every row of S in use, in order
-                Sa = S if full else torch.cat([S[o:o + w] for o, w in srows])
-                dx = dS @ Sa if dx is None else dx.addmm_(dS, Sa)
-            if act_lora:
-                dA = dS[:, :n_act].t() @ x2
-                c = 0
-                for j in act_lora:
-                    r = lora[j][2]
-                    grads[2 * j] = dA[c:c + r]
-                    c += r
+            dx, grads = _fused_backward(spec, ctx.skey, x2, xS, S, Bs, flat, plan, need_x, dt)
+            STATS["lan ngược gộp"] = STATS.get("lan ngược gộp", 0) + 1
+        else:
+            dx, grads = _plain_backward(spec, x2, xS, S, Bs, flat, need_x, dt)
         # A / B may be fp32 parameters while the math runs in bf16: autograd casts the gradients to their dtype
-        ws_in = ctx.needs_input_grad[4:]
-        out = [None if (g is None or not ws_in[k]) else g for k, g in enumerate(grads)]
-        dx = None if dx is None else dx.view(*lead, K).to(xdt)
-        return (dx, None, None, None, *out)
+        wanted = ctx.needs_input_grad[4:]
+        grads = [g if (g is not None and wanted[k]) else None for k, g in enumerate(grads)]
+        return (None if dx is None else dx.view(*lead, K).to(xdt), None, None, None, *grads)
 
 
-def _cdiv(a, b):
-    return -(-a // b)
+# ------------------------------------------------------------------------------------------- backward
+def _add_dgrad(dx, base, dy, dt):
+    """dx += dy · W of one base layer (MX: the quantized dy times the weight's second axis; bf16: addmm_)."""
+    if _mx(base):
+        import mxfp8
+        qd, sd = mxfp8.mx_quant(dy if dy.is_contiguous() else dy.contiguous())
+        g = mxfp8.mx_mm(qd, sd, *mxfp8.mx_wt(base))
+        return g if dx is None else dx.add_(g)
+    w = base.weight.to(dt)
+    return dy @ w if dx is None else dx.addmm_(dy, w)
 
 
-def _fused_bwd_plan(parts, flat, dt, need_x):
-    """Whether the grouped backward applies (fused_linear.py:203-216): bf16 math, a gradient for every output,
-    every MX layer in mxfp8.FUSED_BWD and, when dx is needed, a concatenated Wᵀ covering exactly the group's MX
-    layers in order.  Returns (MX layer indices, (B operand, scales, layout) or None), or None for the plain path."""
-    if dt != torch.bfloat16 or any(dy is None for dy in flat):
+def _plain_backward(spec, x2, xS, S, Bs, flat, need_x, dt):
+    """Per-layer backward (fused_linear.py:128-196): the base layers' dgrads, then the thin branch as one
+    product dS = [s·dy·B of each adapter | dy of each thin linear] against the matching rows of S, and
+    dA = dS_adaptersᵀ · x2."""
+    dx = None
+    if need_x:
+        for i, (base, A, B, s) in enumerate(spec.parts):
+            if flat[i] is not None and i not in spec.thin_ids:
+                dx = _add_dgrad(dx, base, flat[i], dt)
+    grads = [None] * (2 * len(spec.adapters))
+    cols, used, live = [], [], []
+    for sl in spec.adapters:
+        dy = flat[sl.layer]
+        if dy is None:
+            continue
+        dB, dxa = dy.t() @ xS[:, sl.cols], dy @ Bs[sl.index]
+        if sl.scale != 1:
+            dB.mul_(sl.scale)
+            dxa.mul_(sl.scale)
+        grads[2 * sl.index + 1] = dB
+        cols.append(dxa)
+        used.append(sl)
+        live.append(sl)
+    if need_x:
+        for sl in spec.thin:
+            if flat[sl.layer] is not None:
+                cols.append(flat[sl.layer])
+                used.append(sl)
+    if not cols:
+        return dx, grads
+    dS = cols[0] if len(cols) == 1 else torch.cat(cols, 1)
+    if need_x:
+        rows = S if len(used) == len(spec.adapters) + len(spec.thin) else torch.cat([S[sl.cols] for sl in used])
+        dx = dS @ rows if dx is None else dx.addmm_(dS, rows)
+    if live:
+        dA = dS[:, :sum(sl.width for sl in live)].t() @ x2
+        c = 0
+        for sl in live:
+            grads[2 * sl.index] = dA[c:c + sl.width]
+            c += sl.width
+    return dx, grads
+
+
+def _fused_bwd_plan(spec, flat, dt, need_x):
+    """The B operand of the group's one dx GEMM ((codes, scales, layout), or None without dx) when the grouped
+    backward applies (fused_linear.py:203-216): bf16 math, a gradient for every output, every MX layer in
+    mxfp8.FUSED_BWD and, for dx, a concatenated Wᵀ covering exactly the group's MX layers in order.  None for
+    the per-layer backward."""
+    if dt != torch.bfloat16 or any(dy is None for dy in flat) or not spec.mx:
         return None
-    mxi = [i for i, p in enumerate(parts) if _mx(p[0])]
-    if not mxi or not all(getattr(parts[i][0], "_mx_fbwd", False) for i in mxi):
+    if not all(getattr(spec.parts[i][0], "_mx_fbwd", False) for i in spec.mx):
         return None
+    if not need_x:
+        return (None,)
     import mxfp8
-    wt = mxfp8.group_operand([parts[i][0] for i in mxi]) if need_x else None
-    if need_x and wt is None:
-        return None
-    return mxi, wt
+    wt = mxfp8.group_operand([spec.parts[i][0] for i in spec.mx])
+    return None if wt is None else (wt,)
 
 
-def _fused_backward(ctx, x2, xS, S, Bs, flat, plan, need_x):
-    """_Group.backward through mxfp8.lora_bwd (fused_linear.py:219-279): each dy is read ONCE (MX codes into a
-    buffer concatenated along the group's N, d(xa), dB) and dx of the group is ONE MX GEMM with the concatenated
-    Wᵀ (fp32 accumulation across the layers instead of a bf16 add per layer).  The columns of dS follow the rows
-    of S (the LoRA d(xa) in order, then the thin linears' dy); dx.addmm_(dS, S) and dA = dSᵀ·x2 as in the plain
-    path."""
+def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
+    """Grouped backward through mxfp8.lora_bwd (fused_linear.py:219-279): each MX dy is read ONCE (its MX codes
+    into a buffer concatenated along the group's N, its d(xa) into dS, its dB), then dx of the group is ONE MX
+    GEMM with the concatenated Wᵀ (fp32 accumulation across the layers instead of a bf16 add per layer).  dS·S
+    rides in that GEMM's epilogue and dA = dSᵀ·x2 runs on the token-reduction kernel when dS fits a padded
+    width of 16/32/64 and no plain bf16 linear has to be added into dx first."""
     import mxfp8
-    parts, lora, thin, lead, K, dt, xdt = ctx.meta
-    mxi, wt = plan
-    T, dev = x2.shape[0], x2.device
-    lora_of = {i: (j, o, r, s) for j, (i, o, r, s) in enumerate(lora)}
-    n_act = sum(r for _, _, r, _ in lora)
-    n_cols = n_act + (sum(n for _, _, n in thin) if need_x else 0)
-    plain = [i for i, p in enumerate(parts) if not _mx(p[0]) and i not in {t[0] for t in thin}]
-    # dS·S rides in the dx GEMM's epilogue and dA = dSᵀ·x2 runs on the token-reduction kernel when dS fits a
-    # padded width of 16/32/64 (zero columns) and no plain bf16 linear has to be added into dx first
-    native = n_cols > 0 and _native_ok(x2, dt, n_cols) and not plain
+    (wt,) = plan
+    T, K, dev = x2.shape[0], x2.shape[1], x2.device
+    n_cols = spec.adapter_cols + (sum(sl.width for sl in spec.thin) if need_x else 0)
+    native = n_cols > 0 and _native_ok(x2, dt, n_cols) and not spec.plain
     width = _rp(n_cols) if native else n_cols
     dS = torch.empty((T, width), dtype=dt, device=dev) if n_cols else None
     if native and width > n_cols:
         dS[:, n_cols:].zero_()
-    grads = [None] * (2 * len(lora))
-    q = s_buf = None
+    grads = [None] * (2 * len(spec.adapters))
+    q = sbuf = None
     if need_x:
-        n_mx = sum(flat[i].shape[1] for i in mxi)
+        n_mx = sum(flat[i].shape[1] for i in spec.mx)
         q = torch.empty((T, n_mx), dtype=mxfp8.F8, device=dev)
-        s_buf = torch.empty(_cdiv(T, 128) * (n_mx // 128) * 512, dtype=torch.uint8, device=dev)
+        sbuf = torch.empty(_cdiv(T, 128) * (n_mx // 128) * 512, dtype=torch.uint8, device=dev)
     tile = 0
-    for i in mxi:
+    for i in spec.mx:
         dy = flat[i] if flat[i].stride(1) == 1 else flat[i].contiguous()
-        if i in lora_of:
-            j, o, r, s = lora_of[i]
-            if r in (16, 32) and _vec_ok(xS[:, o:o + r]):
-                grads[2 * j + 1] = mxfp8.lora_bwd(dy, xS[:, o:o + r], Bs[j], s, q=q, s=s_buf, col_tile_off=tile,
-                                                  dxa_out=dS[:, o:o + r])
-            else:  # a rank or xa layout the fused kernel does not take: codes from it, the products as GEMMs
-                if q is not None:
-                    mxfp8.lora_bwd(dy, q=q, s=s_buf, col_tile_off=tile)
-                xa = xS[:, o:o + r]
-                grads[2 * j + 1] = (dy.t().float() @ xa.float()).mul_(s)
-                dS[:, o:o + r] = (dy.float() @ Bs[j].float()).mul_(s)
-        elif q is not None:
-            mxfp8.lora_bwd(dy, q=q, s=s_buf, col_tile_off=tile)
+        sl = spec.adapter(i)
+        if sl is not None and sl.width in (16, 32) and _vec_ok(xS[:, sl.cols]):
+            grads[2 * sl.index + 1] = mxfp8.lora_bwd(dy, xS[:, sl.cols], Bs[sl.index], sl.scale, q=q, s=sbuf,
+                                                     col_tile_off=tile, dxa_out=dS[:, sl.cols])
+        else:
+            if q is not None:
+                mxfp8.lora_bwd(dy, q=q, s=sbuf, col_tile_off=tile)
+            if sl is not None:  # a rank or xa layout the fused kernel does not take: the products as GEMMs
+                grads[2 * sl.index + 1] = (dy.t().float() @ xS[:, sl.cols].float()).mul_(sl.scale)
+                dS[:, sl.cols] = (dy.float() @ Bs[sl.index].float()).mul_(sl.scale)
         tile += dy.shape[1] // 128
-    for j, (i, o, r, s) in enumerate(lora):  # LoRA on a non-MX base layer (rare): as the plain path
-        if i in mxi:
+    mx_ids = set(spec.mx)
+    for sl in spec.adapters:  # LoRA on a non-MX base layer (rare): as the per-layer backward
+        if sl.layer in mx_ids:
             continue
-        dy = flat[i]
-        dB = dy.t() @ xS[:, o:o + r]
-        dS[:, o:o + r] = dy @ Bs[j]
-        if s != 1:
-            dB.mul_(s)
-            dS[:, o:o + r].mul_(s)
-        grads[2 * j + 1] = dB
+        dy = flat[sl.layer]
+        dB = dy.t() @ xS[:, sl.cols]
+        dS[:, sl.cols] = dy @ Bs[sl.index]
+        if sl.scale != 1:
+            dB.mul_(sl.scale)
+            dS[:, sl.cols].mul_(sl.scale)
+        grads[2 * sl.index + 1] = dB
     dx = None
     if need_x:
         wq, ws, lay = wt
-        for i, o, n in thin:
-            dS[:, o:o + n].copy_(flat[i])
+        for sl in spec.thin:
+            dS[:, sl.cols].copy_(flat[sl.layer])
+        codes = (q, sbuf.view(mxfp8.E8))
         if native:
-            # bf16(bf16(MX GEMM) + dS·S): the dx.addmm_(dS, S) of the reference in the GEMM epilogue
-            St = _cast(ctx.skey + ("padT", width), lambda: _s_pad(S, ctx.skey, width).t().contiguous())
-            dx = mxfp8.mx_mm(q, s_buf.view(mxfp8.E8), wq, ws, layout=lay, lora=(dS, St), alpha=1.0)
+            # bf16(bf16(MX GEMM) + dS·S): the reference's dx.addmm_(dS, S) in the GEMM epilogue
+            St = _cast(skey + ("padT", width), lambda: _s_pad(S, skey, width).t().contiguous())
+            dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=(dS, St), alpha=1.0)
         else:
-            dx = mxfp8.mx_mm(q, s_buf.view(mxfp8.E8), wq, ws, layout=lay)
-            for i in plain:  # plain bf16 linears (neither MX nor thin)
-                dx.addmm_(flat[i], parts[i][0].weight.to(dt))
+            dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay)
+            for i in spec.plain:  # plain bf16 linears (neither MX nor thin)
+                dx.addmm_(flat[i], spec.parts[i][0].weight.to(dt))
             if dS is not None:
                 dx.addmm_(dS, S)
-        del q, s_buf
-    if lora:
+        del codes, q, sbuf
+    if spec.adapters:
         if native:
             import _native
             dA = torch.empty((width, K), dtype=dt, device=dev)
             part = torch.empty(_native.lora_tn_chunks(T, K) * width * K, dtype=torch.float32, device=dev)
             _native.lora_tn(x2, dS, dA, part)  # bf16(dSᵀ·x2)
         else:
-            dA = dS[:, :n_act].t() @ x2
-        for j, (i, o, r, s) in enumerate(lora):
-            grads[2 * j] = dA[o:o + r]
-    STATS["lan ngược gộp"] = STATS.get("lan ngược gộp", 0) + 1
-    ws_in = ctx.needs_input_grad[4:]
-    out = [None if (g is None or not ws_in[k]) else g for k, g in enumerate(grads)]
-    dx = None if dx is None else dx.view(*lead, K).to(xdt)
-    return (dx, None, None, None, *out)
+            dA = dS[:, :spec.adapter_cols].t() @ x2
+        for sl in spec.adapters:
+            grads[2 * sl.index] = dA[sl.cols]
+    return dx, grads
 
 
-# ---------------------------------------------------------------- residual + LoRA-B (fused_linear.py:282-312)
+# ------------------------------------------------------------------------------------------- residual + LoRA-B
 class Deferred(tuple):
-    """(y, xa, B, scaling): the bf16 MX output of o_proj / out_proj WITHOUT its LoRA part; residual_add adds it."""
+    """(y, xa, B, scaling): the bf16 MX output of o_proj / out_proj WITHOUT its LoRA part; residual_add adds it
+    (fused_linear.py:282-284)."""
 
 
 class _ResidualLoRA(torch.autograd.Function):
-    """x + (y + s · xa @ Bᵀ) in ONE kernel (mxfp8.res_lora): the residual add reads y and x and writes the new x
-    anyway; adding the rank-r product there drops the addmm_ that reads and writes [T, N] once more.  xa and B are
-    detached: the LoRA gradients (dB, d(xa) -> dA, dx) come from _Group.backward with the same dy; here only dy
-    passes through."""
+    """x + (y + s · xa·Bᵀ) in ONE kernel (mxfp8.res_lora): the residual add reads y and x and writes the new x
+    anyway, so adding the rank-r product there saves a read and a write of [T, N].  xa and B are detached: the
+    LoRA gradients (dB, d(xa) -> dA, dx) come from _Group.backward with the same upstream gradient, which passes
+    through here to both x and y (fused_linear.py:287-300)."""
 
     @staticmethod
     def forward(ctx, x, y, xa, B, s):
         import mxfp8
-        N = x.shape[-1]
-        return mxfp8.res_lora(x.reshape(-1, N), y.reshape(-1, N), xa, B, s).view(x.shape)
+        n = x.shape[-1]
+        return mxfp8.res_lora(x.reshape(-1, n), y.reshape(-1, n), xa, B, s).view(x.shape)
 
     @staticmethod
-    def backward(ctx, dy):
-        return dy, dy, None, None, None
+    def backward(ctx, g):
+        return g, g, None, None, None
+
+
+def _res_kernel_ok(x, y, xa, B):
+    return (x.dtype == y.dtype == torch.bfloat16 and x.shape == y.shape and x.is_contiguous() and y.is_contiguous()
+            and x.shape[-1] % 128 == 0 and xa.stride(1) == 1 and B.is_contiguous() and xa.shape[1] in (16, 32))
 
 
 def residual_add(x, y):
-    """x + y; when y is Deferred (group_linear(..., defer=True)) the LoRA part is added inside the residual
-    kernel."""
+    """x + y; a Deferred y gets its LoRA part added inside the residual kernel when it qualifies, else by a torch
+    addmm first (fused_linear.py:303-312)."""
     if not isinstance(y, Deferred):
         return x + y
-    y, xa, B, s = y
-    N = x.shape[-1]
-    if (x.dtype == y.dtype == torch.bfloat16 and x.shape == y.shape and x.is_contiguous() and y.is_contiguous()
-            and N % 128 == 0 and xa.stride(1) == 1 and B.is_contiguous() and xa.shape[1] in (16, 32)):
+    y0, xa, B, s = y
+    if _res_kernel_ok(x, y0, xa, B):
         STATS["residual LoRA"] = STATS.get("residual LoRA", 0) + 1
-        return _ResidualLoRA.apply(x, y, xa, B, s)
-    return x + torch.addmm(y.reshape(-1, N), xa, B.t(), alpha=s).view(y.shape)  # other dtype/shape: as before
+        return _ResidualLoRA.apply(x, y0, xa, B, s)
+    n = x.shape[-1]
+    return x + torch.addmm(y0.reshape(-1, n), xa, B.t(), alpha=s).view(y0.shape)
 
 
 def group_linear(x, mods, need_out=True, defer=False):
-    """(m(x) for m in mods), computed as one group (fused_linear.py:315-330).
-    need_out=False: only the graph for backward (outputs uninitialised), for the recomputation of a checkpointed
-    segment's last layer whose outputs nobody reads (the gradients are the same).
-    defer=True: MX bf16 outputs with LoRA come back as Deferred (LoRA not yet added), for a residual_add right
+    """The outputs m(x) of every module in `mods`, computed as one group (fused_linear.py:315-330).
+    need_out=False builds only the graph for backward (outputs uninitialised), for the recomputation of a
+    checkpointed segment's last layer whose outputs nobody reads; the gradients are the same.
+    defer=True returns MX bf16 outputs with LoRA as Deferred (LoRA not yet added), for a residual_add right
     after."""
     parts = tuple(_part(m) for m in mods)
     if any(p is None for p in parts):
         STATS["gọi thẳng"] += 1
         return tuple(m(x) for m in mods)
     STATS["gộp"] += 1
-    ws = [w for p in parts if p[1] is not None for w in (p[1], p[2])]
+    ws = [t for base, A, B, s in parts if A is not None for t in (A, B)]
     box = {} if defer and need_out else None
     outs = _Group.apply(x, parts, need_out, box, *ws)
     if not box:

@@ -15,6 +15,7 @@ gate_proj + up_proj of one MLP share one quantized copy W_gu = [W_gate; W_up] [2
 W_guᵀ [K, 2N] (fused_mlp.py runs one forward GEMM and one K = 2N dgrad GEMM).  32-blocks never straddle the
 gate/up boundary, so codes and scales equal those of separate copies byte for byte (mxfp8.py:20-23).
 """
+import itertools
 import os
 import types
 import weakref
@@ -229,260 +230,313 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
 
 
 # ---------------------------------------------------------------- generic MX linear (mxfp8.py:296-341)
-_last = [None, 0, None, None]  # (weakref tensor, _version, q, s) of the last quantized activation
+class _ActivationMemo:
+    """The codes of the activation an MX linear quantized last, keyed by (weak reference, version).  Linears that
+    read one input back to back (q/k/v, qkv/z, gate/up outside the fused MLP) quantize it once.  The weak
+    reference keeps no activation alive, and a dead one never matches a new tensor that reuses the address; an
+    in-place change bumps the version (mxfp8.py:296-312)."""
+
+    __slots__ = ("ref", "version", "codes")
+
+    def __init__(self):
+        self.forget()
+
+    def forget(self):
+        self.ref, self.version, self.codes = None, -1, None
+
+    def lookup(self, x):
+        live = self.ref() if self.ref is not None else None
+        return self.codes if (live is x and self.version == x._version) else None
+
+    def remember(self, x, codes):
+        self.ref, self.version, self.codes = weakref.ref(x), x._version, codes
+
+
+_ACT = _ActivationMemo()
+
+
+def _rows_bf16(t):
+    """[..., C] -> a contiguous bf16 [R, C] matrix (a view when t already is one)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    return t2 if t2.dtype == torch.bfloat16 and t2.is_contiguous() else t2.to(torch.bfloat16).contiguous()
 
 
 def _quant_act(x):
-    """Quantize the input of a linear layer, reusing the last result if x is the same live tensor at the
-    same version (qkv/z, q/k/v and gate/up share one input) (mxfp8.py:299-312)."""
-    if _last[0] is not None and _last[0]() is x and _last[1] == x._version:
+    """(codes, scales) of a linear layer's input, reused when x is the live tensor quantized last, at the same
+    version; STATS counts both cases."""
+    codes = _ACT.lookup(x)
+    if codes is not None:
         STATS["reuse"] += 1
-        return _last[2], _last[3]
-    x2 = x.reshape(-1, x.shape[-1])
-    if x2.dtype != torch.bfloat16 or not x2.is_contiguous():
-        x2 = x2.to(torch.bfloat16).contiguous()
-    q, s = mx_quant(x2)
+        return codes
+    codes = mx_quant(_rows_bf16(x))
     STATS["quant"] += 1
-    _last[:] = [weakref.ref(x), x._version, q, s]
-    return q, s
+    _ACT.remember(x, codes)
+    return codes
 
 
 class _MXLinear(torch.autograd.Function):
-    """x @ Wᵀ of a frozen MX weight, backward dx = MX(dy) @ W (mxfp8.py:315-333)."""
+    """x·Wᵀ of a frozen MX weight from the input's codes; backward dx = MX(dy)·W through the weight's second
+    quantization axis (mx_wt).  The weight has no gradient (mxfp8.py:315-333)."""
 
     @staticmethod
     def forward(ctx, x, q, s, lin):
-        out = mx_mm(q, s, lin._mx_w, lin._mx_ws)
         ctx.lin = lin
-        return out.view(*x.shape[:-1], out.shape[-1])
+        y = mx_mm(q, s, lin._mx_w, lin._mx_ws)
+        return y.view(x.shape[:-1] + (y.shape[-1],))
 
     @staticmethod
     def backward(ctx, dy):
-        lin = ctx.lin
-        n = dy.shape[-1]
-        dy2 = dy.reshape(-1, n)
-        if dy2.dtype != torch.bfloat16 or not dy2.is_contiguous():
-            dy2 = dy2.to(torch.bfloat16).contiguous()
-        q, s = mx_quant(dy2)
+        qd, sd = mx_quant(_rows_bf16(dy))
         STATS["quant"] += 1
-        wt, wts = mx_wt(lin)
-        dx = mx_mm(q, s, wt, wts)
-        return dx.view(*dy.shape[:-1], dx.shape[-1]), None, None, None
+        dx = mx_mm(qd, sd, *mx_wt(ctx.lin))
+        return dx.view(dy.shape[:-1] + (dx.shape[-1],)), None, None, None
 
 
 @torch.compiler.disable
 def _forward(self, x):
-    q, s = _quant_act(x)
-    return _MXLinear.apply(x, q, s, self)
+    """The forward enable_mxfp8 installs on a frozen linear (outside any torch.compile region, as the reference
+    keeps it: mxfp8.py:336-341)."""
+    return _MXLinear.apply(x, *_quant_act(x), self)
 
 
-_NAMES = {"q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "in_proj_qkv", "in_proj_z",
-          "out_proj"}
-
-
-def _base_linears(model):
-    """Frozen base linears of the decoder layers (mxfp8.py:347-356)."""
-    for name, m in model.named_modules():
-        if not isinstance(m, torch.nn.Linear) or m.weight.requires_grad or ".layers." not in name:
-            continue
-        parts = name.split(".")
-        leaf = parts[-2] if parts[-1] == "base_layer" else parts[-1]
-        if leaf in _NAMES:
-            yield name, m
-
-
-def _leaf_parent(name):
-    parts = name.split(".")
-    if parts[-1] == "base_layer":
-        return parts[-2], ".".join(parts[:-2])
-    return parts[-1], ".".join(parts[:-1])
-
-
-# Groups whose Wᵀ is kept once, concatenated along N, so that dx of the whole group is one GEMM over the
-# concatenated dy codes (mxfp8.py:360-366).  Every N is a multiple of 128, so no 32-block straddles two layers and
-# each layer's codes and scales equal its own quantization.  gate/up/down go through fused_mlp instead.
+# ---------------------------------------------------------------- which linears, grouped how (mxfp8.py:345-366)
+# leaf names of the decoder-layer linears that run on MX GEMMs
+_NAMES = frozenset({"q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "in_proj_qkv",
+                    "in_proj_z", "out_proj"})
+# Sibling layers whose Wᵀ is kept once, concatenated along N, so that dx of the group is one GEMM over the
+# concatenated dy codes.  Every N is a multiple of 128, so no 32-block straddles two layers and each layer's
+# codes and scales equal its own quantization.  gate/up/down go through fused_mlp instead.
 _CATS = (("in_proj_qkv", "in_proj_z"), ("q_proj", "k_proj", "v_proj"))
 # Linears whose backward takes the grouped path of fused_linear._Group (one read of dy through lora_bwd)
 FUSED_BWD = {"in_proj_qkv", "in_proj_z", "q_proj", "k_proj", "v_proj", "o_proj", "out_proj"}
+FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
+# what enable_mxfp8 attaches to a linear (disable_mxfp8 removes exactly these)
+_MX_ATTRS = ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_cat", "_mx_gu", "_mx_fbwd",
+             "_bf16_cpu", "forward")
+
+
+def _mx_target(name, mod):
+    """(leaf name, owner path) of a frozen base linear of a decoder layer that takes MX GEMMs, else None.  A PEFT
+    wrapper's base_layer counts under the wrapper's name."""
+    if not isinstance(mod, torch.nn.Linear) or mod.weight.requires_grad or ".layers." not in name:
+        return None
+    path = name.split(".")
+    if path[-1] == "base_layer":
+        path.pop()
+    leaf = path.pop()
+    return (leaf, ".".join(path)) if leaf in _NAMES else None
+
+
+def _base_linears(model):
+    """(name, linear) of every module _mx_target accepts, in module order."""
+    return ((name, mod) for name, mod in model.named_modules() if _mx_target(name, mod) is not None)
+
+
+def _col_tiles(scales, rows, cols, c0, c1):
+    """The blocked scales of columns [c0, c1) of an MX operand [rows, cols] quantized along its columns: in every
+    128-row tile row, the 512-byte tiles of that column range, cut out contiguously (c0, c1 multiples of 128).
+    Byte for byte the quantization of those columns alone."""
+    tiles = scales.view(torch.uint8).view(_cdiv(rows, 128), cols // 128, 512)
+    return tiles[:, c0 // 128:c1 // 128].contiguous().view(-1).view(E8)
+
+
+class _GateUp:
+    """The one MX copy that gate_proj and up_proj of an MLP share (`_mx_gu = (hold, 0 | 1)`): W_gu = [W_gate;
+    W_up] [2N, K] along K (w, ws) for the one forward GEMM and W_guᵀ [K, 2N] along 2N (wt, wts) for the one
+    K = 2N dgrad GEMM, both from one read, with MX-tiled copies for the fused MLP (w_tl, wt_tl).  The scale tile
+    rows of ws are ordered by row, so its first half is gate's (mxfp8.py:472-484).  half_t caches the per-half
+    dgrad operands that mx_wt cuts out."""
+
+    def __init__(self, gate_w, up_w):
+        self.n = gate_w.shape[0]
+        self.w, self.ws, self.wt, self.wts = quant_both(torch.cat([gate_w, up_w]).to(torch.bfloat16))
+        self.w_tl, self.wt_tl = tile_codes(self.w), tile_codes(self.wt)
+        self.half_t = [None, None]
+
+    def rows(self, i):
+        half = self.ws.numel() // 2
+        return self.w[i * self.n:(i + 1) * self.n], self.ws[i * half:(i + 1) * half]
 
 
 class _Cat:
-    """Wᵀ of a group concatenated along N: codes [K, ΣN] quantized along ΣN with their blocked scales, and the
-    MX-tiled copy the whole-group GEMM reads (mxfp8.py:369-395)."""
+    """One MX copy of a group's weights concatenated along N, [ΣN, K]: the forward codes along K (w, ws; each
+    layer's are a row range) and Wᵀ [K, ΣN] along ΣN (qt, st), from one read, with MX-tiled copies (w_tl, qt_tl).
+    offs are the layers' first columns of Wᵀ (mxfp8.py:369-395)."""
 
-    def __init__(self, qt, st, ns):
-        self.qt, self.st = qt, st
-        self.qt_tl = tile_codes(qt)
-        self.offs = [0]
-        for n in ns:
-            self.offs.append(self.offs[-1] + n)
-        self.n = len(ns)
-        self._sub = {}
+    def __init__(self, lins):
+        self.n = len(lins)
+        self.offs = list(itertools.accumulate((lin.weight.shape[0] for lin in lins), initial=0))
+        self.w, self.ws, self.qt, self.st = quant_both(torch.cat([lin.weight.data for lin in lins]).to(torch.bfloat16))
+        self.w_tl, self.qt_tl = tile_codes(self.w), tile_codes(self.qt)
+        self._cuts = {}
+
+    def fwd_rows(self, k):
+        """(codes, scales, tiled codes) of layer k's forward operand: rows offs[k]..offs[k+1] of w."""
+        c0, c1 = self.offs[k], self.offs[k + 1]
+        per_tile_row = (self.w.shape[1] // 128) * 512  # scale bytes of one 128-row tile row
+        return self.w[c0:c1], self.ws[c0 // 128 * per_tile_row:c1 // 128 * per_tile_row], self.w_tl[c0:c1]
 
     def range(self, a, b):
-        """(mat2 [N_a+..+N_{b-1}, K] column-major view, scales) of layers a..b-1, the torch._scaled_mm form.  The
-        scales of a column range are its 128x4 tiles of every 128-row block, cut out contiguously on first use:
-        byte for byte the quantization of that range alone."""
+        """(mat2 [N_a + .. + N_(b-1), K] as a column-major view of Wᵀ, scales) of layers a..b-1, the form
+        torch._scaled_mm takes; the scales of a partial range are cut out on first use and kept."""
         c0, c1 = self.offs[a], self.offs[b]
-        mat2 = self.qt[:, c0:c1].t()
         if (a, b) == (0, self.n):
-            return mat2, self.st
-        sc = self._sub.get((a, b))
-        if sc is None:
-            K, ntot = self.qt.shape
-            blk = self.st.view(torch.uint8).view(_cdiv(K, 128), ntot // 128, 512)
-            sc = self._sub[(a, b)] = blk[:, c0 // 128:c1 // 128].contiguous().view(-1).view(E8)
-        return mat2, sc
+            return self.qt.t(), self.st
+        if (a, b) not in self._cuts:
+            self._cuts[(a, b)] = _col_tiles(self.st, self.qt.shape[0], self.qt.shape[1], c0, c1)
+        return self.qt[:, c0:c1].t(), self._cuts[(a, b)]
 
 
 def is_mx(lin):
     return getattr(lin, "_mx_w", None) is not None
 
 
+def _cat_span(lins):
+    """(group, first index) when `lins` are consecutive layers of one concatenated group, else None."""
+    tags = [lin.__dict__.get("_mx_cat") for lin in lins]
+    if tags[0] is None:
+        return None
+    cat, k = tags[0]
+    return (cat, k) if all(t is not None and t[0] is cat and t[1] == k + d for d, t in enumerate(tags)) else None
+
+
 def mx_wt(lin):
-    """(fp8 Wᵀ [K, N] as the B operand of dx = dy @ W, scales).  For a gate/up pair: a column view of W_guᵀ
-    (row stride 2N) plus that half's scale tiles cut out contiguously, made on first use and kept
-    (mxfp8.py:402-415); for a layer of a concatenated group, its column range of the group's Wᵀ."""
-    gu = lin.__dict__.get("_mx_gu")
-    if gu is None:
-        if "_mx_cat" in lin.__dict__:
-            m, sc = wt_of(lin)
-            return m.t(), sc
-        return lin._mx_wt, lin._mx_wts
-    hold, i = gu
-    if hold.half_t[i] is None:
-        n, k = hold.n, hold.wt.shape[0]
-        s3 = hold.wts.view(torch.uint8).view(k // 128, 2 * n // 128, 512)
-        hold.half_t[i] = (hold.wt[:, i * n:(i + 1) * n],
-                          s3[:, i * (n // 128):(i + 1) * (n // 128)].reshape(-1).view(E8))
-    return hold.half_t[i]
+    """(fp8 Wᵀ [K, N], scales): the B operand of dx = dy · W in mx_mm's form (mxfp8.py:402-415).  A gate/up half
+    is a column view of the shared W_guᵀ (row stride 2N) with its scale tiles cut out on first use; a layer of a
+    concatenated group, its column range of the group's Wᵀ; any other MX linear, its own Wᵀ."""
+    pair = lin.__dict__.get("_mx_gu")
+    if pair is not None:
+        hold, i = pair
+        if hold.half_t[i] is None:
+            n, k = hold.n, hold.wt.shape[0]
+            hold.half_t[i] = (hold.wt[:, i * n:(i + 1) * n], _col_tiles(hold.wts, k, 2 * n, i * n, (i + 1) * n))
+        return hold.half_t[i]
+    tag = lin.__dict__.get("_mx_cat")
+    if tag is not None:
+        mat2, sc = tag[0].range(tag[1], tag[1] + 1)
+        return mat2.t(), sc
+    return lin._mx_wt, lin._mx_wts
 
 
 def wt_of(lin):
-    """(mat2, scale) of dy @ W in torch._scaled_mm form: mat2 = Wᵀ codes as an [N, K] column-major view
-    (mxfp8.py:418-426)."""
-    c = lin.__dict__.get("_mx_cat")
-    if c is not None:
-        return c[0].range(c[1], c[1] + 1)
-    wt, s = mx_wt(lin)
-    return wt.t(), s
+    """(mat2 [N, K] = Wᵀ as a column-major view, scales): mx_wt in the torch._scaled_mm form (mxfp8.py:418-426)."""
+    wt, sc = mx_wt(lin)
+    return wt.t(), sc
 
 
 def group_wt(lins):
-    """(mat2 [ΣN, K], scale) of dx = [dy_1|dy_2|..] @ [W_1; W_2; ..] for consecutive layers of one concatenated
-    group (or a single layer); None when no concatenated copy fits (mxfp8.py:429-439)."""
-    c = lins[0].__dict__.get("_mx_cat")
-    if c is None:
-        return wt_of(lins[0]) if len(lins) == 1 else None
-    cat, k = c
-    for d, lin in enumerate(lins):
-        if lin.__dict__.get("_mx_cat") != (cat, k + d):
-            return None
-    return cat.range(k, k + len(lins))
+    """(mat2 [ΣN, K], scales) of dx = [dy_1 | dy_2 | ..] · [W_1; W_2; ..] for consecutive layers of one concatenated
+    group, or of a single ungrouped layer; None otherwise (mxfp8.py:429-439)."""
+    span = _cat_span(lins)
+    if span is not None:
+        return span[0].range(span[1], span[1] + len(lins))
+    if len(lins) == 1 and "_mx_cat" not in lins[0].__dict__:
+        return wt_of(lins[0])
+    return None
 
 
 def group_fwd_operand(lins):
-    """(B operand [ΣN, K] of the forward GEMM of consecutive layers of one concatenated group (MX-tiled), scales),
-    or None when the layers are not such a range."""
-    c = lins[0].__dict__.get("_mx_cat")
-    if c is None or getattr(c[0], "w_tl", None) is None:
+    """(MX-tiled B operand [ΣN, K] of one forward GEMM over consecutive layers of a concatenated group, scales),
+    or None when the layers are not such a range.  No reference counterpart (the reference runs one GEMM per
+    layer)."""
+    span = _cat_span(lins)
+    if span is None:
         return None
-    cat, k = c
-    for d, lin in enumerate(lins):
-        if lin.__dict__.get("_mx_cat") != (cat, k + d):
-            return None
+    cat, k = span
     c0, c1 = cat.offs[k], cat.offs[k + len(lins)]
-    tile_b = (cat.w_tl.shape[1] // 128) * 512
-    return cat.w_tl[c0:c1], cat.ws[c0 // 128 * tile_b:c1 // 128 * tile_b]
+    per_tile_row = (cat.w.shape[1] // 128) * 512
+    return cat.w_tl[c0:c1], cat.ws[c0 // 128 * per_tile_row:c1 // 128 * per_tile_row]
 
 
 def group_operand(lins):
-    """(B operand [K, ΣN] of mx_mm, scales, layout bit) for dx of `lins` (group_wt): the MX-tiled copy when the
-    range is a whole concatenated group, else the row-major column view (row stride = the group's ΣN)."""
+    """(B operand [K, ΣN] of mx_mm, scales, layout bit) of dx for `lins` (group_wt): the MX-tiled copy when the
+    range is a whole concatenated group or a single layer that has one, else the row-major column view (row
+    stride ΣN of the group)."""
     g = group_wt(lins)
     if g is None:
         return None
     mat2, sc = g
-    c = lins[0].__dict__.get("_mx_cat")
-    if c is not None and c[1] == 0 and len(lins) == c[0].n:
-        return c[0].qt_tl, sc, 2
-    if c is None and "_mx_wt_tl" in lins[0].__dict__:
+    span = _cat_span(lins)
+    if span is not None and span[1] == 0 and len(lins) == span[0].n:
+        return span[0].qt_tl, sc, 2
+    if span is None and "_mx_wt_tl" in lins[0].__dict__:
         return lins[0]._mx_wt_tl, sc, 2
     return mat2.t(), sc, 0
 
 
-FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
+# ---------------------------------------------------------------- enable / disable (mxfp8.py:452-509)
+def _prep_single(lin):
+    lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(lin.weight.data.to(torch.bfloat16))
+    lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
+
+
+def _prep_gate_up(gate, up):
+    hold = _GateUp(gate.weight.data, up.weight.data)
+    for i, lin in enumerate((gate, up)):
+        lin._mx_w, lin._mx_ws = hold.rows(i)
+        lin._mx_gu = (hold, i)
+
+
+def _prep_concat(lins):
+    cat = _Cat(lins)
+    for k, lin in enumerate(lins):
+        lin._mx_w, lin._mx_ws, lin._mx_w_tl = cat.fwd_rows(k)
+        lin._mx_cat = (cat, k)
+
+
+def _install(lin, leaf):
+    """Move the bf16 weight to host memory (an empty tensor of the same dtype and device stays for code that
+    reads them) and route forward through the MX GEMM."""
+    w = lin.weight.data
+    lin._mx_fbwd = leaf in FUSED_BWD
+    lin._bf16_cpu = w.to("cpu", copy=True)
+    lin.weight.data = torch.empty((0,), dtype=w.dtype, device=w.device)
+    lin.forward = types.MethodType(_forward, lin)
 
 
 def enable_mxfp8(model):
-    """Quantize every frozen base linear of the decoder layers along both axes, pair gate/up into one shared
-    copy, move the bf16 weights to host memory and patch forward (mxfp8.py:452-498).  Both axes of each weight
-    come from one read (quant_both)."""
-    lins = list(_base_linears(model))
-    fam = {}
-    for name, lin in lins:
+    """Quantize every frozen base linear of the decoder layers along both axes, share one copy per gate/up pair
+    and one concatenated Wᵀ per _CATS group, move the bf16 weights to host memory and patch forward
+    (mxfp8.py:452-498).  Both axes of each weight come from one read (quant_both).  Returns the linear count."""
+    found, owners = [], {}
+    for name, lin in _base_linears(model):
         assert lin.bias is None
-        w = lin.weight.data
-        assert w.is_cuda and w.shape[0] % 128 == 0 and w.shape[1] % 128 == 0, w.shape
-        leaf, parent = _leaf_parent(name)
-        fam.setdefault(parent, {})[leaf] = lin
-    in_cat, paired = set(), set()
-    for d in fam.values():
+        assert lin.weight.is_cuda and lin.weight.shape[0] % 128 == 0 and lin.weight.shape[1] % 128 == 0, \
+            lin.weight.shape
+        leaf, owner = _mx_target(name, lin)
+        found.append((leaf, lin))
+        owners.setdefault(owner, {})[leaf] = lin
+    prepared, n_cat, n_pair = set(), 0, 0
+    for sib in owners.values():  # the siblings under one owner module
         for names in _CATS:
-            if all(k in d for k in names):
-                # one read of the concatenated weight gives every layer's forward codes (rows of q) and the
-                # group's Wᵀ along ΣN
-                grp = [d[k] for k in names]
-                w = torch.cat([lin.weight.data for lin in grp]).to(torch.bfloat16)  # [ΣN, K]
-                q, sq, qt, st = quant_both(w)
-                del w
-                cat = _Cat(qt, st, [lin.weight.shape[0] for lin in grp])
-                # the forward codes of the whole group (MX-tiled) for one GEMM over consecutive layers; each
-                # layer's own codes and scales are row slices of them
-                cat.w_tl, cat.ws = tile_codes(q), sq
-                tile_b = (q.shape[1] // 128) * 512  # scale bytes of one 128-row tile row
-                for k, lin in enumerate(grp):
-                    c0, c1 = cat.offs[k], cat.offs[k + 1]
-                    lin._mx_w, lin._mx_ws = q[c0:c1], sq[c0 // 128 * tile_b:c1 // 128 * tile_b]
-                    lin._mx_w_tl = cat.w_tl[c0:c1]
-                    lin._mx_cat = (cat, k)
-                    in_cat.add(id(lin))
-        gb, ub = d.get("gate_proj"), d.get("up_proj")
-        if FUSE_GU and gb is not None and ub is not None and gb.weight.shape == ub.weight.shape:
-            w = torch.cat([gb.weight.data, ub.weight.data]).to(torch.bfloat16)  # [2N, K]
-            n = gb.weight.shape[0]
-            hold = types.SimpleNamespace(n=n, half_t=[None, None])
-            hold.w, hold.ws, hold.wt, hold.wts = quant_both(w)
-            hold.w_tl, hold.wt_tl = tile_codes(hold.w), tile_codes(hold.wt)  # GEMM operand layout of the fused path
-            del w
-            ns = hold.ws.numel() // 2  # forward scales are ordered by tile row: first half = gate
-            for i, lin in enumerate((gb, ub)):
-                lin._mx_w, lin._mx_ws = hold.w[i * n:(i + 1) * n], hold.ws[i * ns:(i + 1) * ns]
-                lin._mx_gu = (hold, i)
-                paired.add(id(lin))
-    for name, lin in lins:
-        w = lin.weight.data
-        if id(lin) not in paired and id(lin) not in in_cat:
-            lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(w.to(torch.bfloat16))
-            lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
-        lin._mx_fbwd = _leaf_parent(name)[0] in FUSED_BWD
-        lin._bf16_cpu = w.to("cpu", copy=True)
-        lin.weight.data = torch.empty((0,), dtype=w.dtype, device=w.device)
-        lin.forward = types.MethodType(_forward, lin)
+            if all(k in sib for k in names):
+                grp = [sib[k] for k in names]
+                _prep_concat(grp)
+                prepared.update(id(lin) for lin in grp)
+                n_cat += len(grp)
+        gate, up = sib.get("gate_proj"), sib.get("up_proj")
+        if FUSE_GU and gate is not None and up is not None and gate.weight.shape == up.weight.shape:
+            _prep_gate_up(gate, up)
+            prepared.update((id(gate), id(up)))
+            n_pair += 1
+    for leaf, lin in found:
+        if id(lin) not in prepared:
+            _prep_single(lin)
+        _install(lin, leaf)
     torch.cuda.empty_cache()
-    print(f"MXFP8: {len(lins)} frozen linears on MX GEMMs (bf16 weights moved to host memory;"
-          f" {len(in_cat)} with a concatenated group Wᵀ, {len(paired) // 2} gate/up pairs shared)", flush=True)
-    return len(lins)
+    print(f"MXFP8: {len(found)} frozen linears on MX GEMMs (bf16 weights moved to host memory;"
+          f" {n_cat} with a concatenated group Wᵀ, {n_pair} gate/up pairs shared)", flush=True)
+    return len(found)
 
 
 def disable_mxfp8(model):
-    """Restore the bf16 weights and the original forward (mxfp8.py:501-509)."""
+    """Put the bf16 weights back on their device, drop the MX copies and the patched forward (mxfp8.py:501-509)."""
     for _, lin in _base_linears(model):
-        if hasattr(lin, "_bf16_cpu"):
-            lin.weight.data = lin._bf16_cpu.to(lin.weight.device)
-            for a in ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_cat", "_mx_gu", "_mx_fbwd",
-                      "_bf16_cpu", "forward"):
-                if a in lin.__dict__:
-                    delattr(lin, a)
-    _last[:] = [None, 0, None, None]
+        saved = lin.__dict__.get("_bf16_cpu")
+        if saved is None:
+            continue
+        lin.weight.data = saved.to(lin.weight.device)
+        for a in _MX_ATTRS:
+            lin.__dict__.pop(a, None)
+    _ACT.forget()
     torch.cuda.empty_cache()
