@@ -277,6 +277,22 @@ int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, const void*
                   float* part, float scale, int64_t transpose, int64_t out_f32, void* out, void* stream);
 
 /*
+ * Allocation-free variant of mxfp8_lora_tn: same arguments without `chunks` / `part`, same result bit for bit as
+ * mxfp8_lora_tn(..., chunks = mxfp8_lora_tn_noalloc_chunks(T, K, rp), ...).  No counterpart in the reference; it
+ * is for callers that cannot allocate device memory (code under HIP graph capture, tight serving or training
+ * loops, harnesses that forbid hipMalloc): the chunk partials live in a static 16 MiB device array of the
+ * library, one per GPU, held until the process ends, so nothing here allocates or frees.  Limit: rp * K * 4 bytes
+ * must fit in it (K <= 65536 at rp = 64); the chunk count is capped so that chunks * rp * K * 4 <= 16 MiB.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialized by the caller.  Returns MXFP8_ERR_ARG when the sizes do not fit.
+ */
+int mxfp8_lora_tn_noalloc(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp, float scale,
+                          int64_t transpose, int64_t out_f32, void* out, void* stream);
+
+/* Chunk count mxfp8_lora_tn_noalloc uses for [T, K] at rank rp (0 for bad sizes). */
+int64_t mxfp8_lora_tn_noalloc_chunks(int64_t T, int64_t K, int64_t rp);
+
+/*
  * The backward kernel's partial sums, added in order, scaled and cast as the reference's backward does
  * (/root/reference/scripts/fused_mlp.py:258, :319-326): dxa [T, 2r] bf16 = bf16(s_g · Σ dxa_g | s_u · Σ dxa_u),
  * xsd [T, r] bf16 = bf16(Σ xS_down), dB_g, dB_u [N, r] fp32 = s · Σ, dA_d [r, N] fp32 = Σ.  Partials as written by

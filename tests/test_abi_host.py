@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 26, names
+    assert len(names) == 28, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -58,6 +58,11 @@ def test_argument_checks_reject_before_launch(lib):
     # transpose: C outside {16, 32, 64}, padded length below T
     assert lib.mxfp8_transpose_pad(p, 8, 24, 24, p, 128, None) == -1
     assert lib.mxfp8_transpose_pad(p, 200, 32, 32, p, 128, None) == -1
+    # allocation-free token reduction: rp * K * 4 bytes beyond its 16 MiB static scratch (checked first, no GPU call)
+    assert lib.mxfp8_lora_tn_noalloc(p, 64, 65536 + 128, 65536 + 128, p, 64, 1.0, 0, 0, p, None) == -1
+    assert b"static scratch" in lib.mxfp8_last_error()
+    assert lib.mxfp8_lora_tn_noalloc_chunks(10752, 2048, 32) == lib.mxfp8_lora_tn_chunks(10752, 2048)
+    assert lib.mxfp8_lora_tn_noalloc_chunks(10752, 2048, 32) * 32 * 2048 * 4 <= 16 << 20
     # GEMM K not a multiple of 128
     assert lib.mxfp8_gemm_nt(p, p, 96, p, p, 96, 4, 128, 96, p, 128, None, 0, None, 0, 0, 1.0, 0, None, 0, None) == -1
     # GEMM epilogue rank not supported

@@ -48,12 +48,15 @@ SIGNATURES = {
     "mxfp8_lora_bwd": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _i64,
                        _ptr, _ptr, _ptr],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
+    "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr],
+    "mxfp8_lora_tn_noalloc_chunks": [_i64, _i64, _i64],
     "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
                              _ptr, _ptr],
 }
 
 _RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64, "mxfp8_mlp_fwd_groups": _i64,
-             "mxfp8_lora_tn_chunks": _i64, "mxfp8_lora_bwd_chunks": _i64}
+             "mxfp8_lora_tn_chunks": _i64, "mxfp8_lora_bwd_chunks": _i64,
+             "mxfp8_lora_tn_noalloc_chunks": _i64}
 
 _lib = None
 _WORKSPACE = {}  # (device index, stream) -> zero-initialised uint8 workspace of the MX GEMM
@@ -276,6 +279,17 @@ def transpose_pad(x, out):
     """out [C, Tpad] = xᵀ of x [T, C] bf16, zero past T."""
     T, C = x.shape
     call("mxfp8_transpose_pad", _p(x), T, C, x.stride(0), _p(out), out.shape[1], like=x)
+
+
+def lora_tn_noalloc(x, p, out, scale=1.0, transpose=False):
+    """lora_tn with the chunk partials in the library's static scratch (nothing allocated)."""
+    T, K = x.shape
+    call("mxfp8_lora_tn_noalloc", _p(x), T, K, x.stride(0), _p(p), p.shape[1], float(scale), int(transpose),
+         int(out.dtype == torch.float32), _p(out), like=x)
+
+
+def lora_tn_noalloc_chunks(T, K, rp):
+    return int(load().mxfp8_lora_tn_noalloc_chunks(T, K, rp))
 
 
 def lora_tn_chunks(T, K):

@@ -14,6 +14,7 @@
 // in chunk order by a second kernel (deterministic); inside a chunk both operands are transposed through LDS
 // with ds_read_b64_tr_b16 so that k runs along the tokens.
 #include <algorithm>
+#include <mutex>
 
 #include "abi_common.h"
 #include "mx_device.h"
@@ -794,9 +795,12 @@ extern "C" int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K) {
   return (blocks + per - 1) / per;
 }
 
-extern "C" int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp,
-                             int64_t chunks, float* part, float scale, int64_t transpose, int64_t out_f32, void* out,
-                             void* stream) {
+namespace {
+
+// Token reduction through the caller's partial buffer `part` (chunks * rp * K floats, every used chunk's slice
+// fully overwritten, so it needs no clearing): the body of mxfp8_lora_tn and mxfp8_lora_tn_noalloc.
+int lora_tn_launch(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp, int64_t chunks,
+                   float* part, float scale, int64_t transpose, int64_t out_f32, void* out, void* stream) {
   MX_CHECK_ARG(x && p && part && out, "mxfp8_lora_tn: null pointer");
   MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
                "mxfp8_lora_tn: need K %% 128 == 0, rp in {16, 32, 64}");
@@ -827,6 +831,71 @@ extern "C" int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, 
                                                               (int)out_f32, out);
   MX_CHECK_LAUNCH("mxfp8_lora_tn");
   return MXFP8_OK;
+}
+
+}  // namespace
+
+extern "C" int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp,
+                             int64_t chunks, float* part, float scale, int64_t transpose, int64_t out_f32, void* out,
+                             void* stream) {
+  return lora_tn_launch(x, T, K, ld_x, p, rp, chunks, part, scale, transpose, out_f32, out, stream);
+}
+
+// ------------------------------------------------------------------ allocation-free token reduction
+// The chunk partials of mxfp8_lora_tn_noalloc live in this file-scope device array, one copy per GPU, held until
+// the process ends.  Host code never passes `scratch` itself (in host code the name is a stand-in, not a device
+// address): the device address comes from hipGetSymbolAddress, looked up once per device on its first call with
+// that device current, and kept in scratch_dev.  Every call on one GPU shares that GPU's array; calls that
+// overlap on one GPU (different streams, or threads) race on it.
+constexpr int64_t kNoAllocScratchBytes = 16LL << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / 4];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+float* scratch_dev[kMaxDevices] = {};
+
+// Device address of this GPU's `scratch` (nullptr and the error message set on failure).
+float* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    mxabi::set_error("mxfp8_lora_tn_noalloc: no current device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      mxabi::set_error("mxfp8_lora_tn_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+      return nullptr;
+    }
+    scratch_dev[dev] = static_cast<float*>(ptr);
+  }
+  return scratch_dev[dev];
+}
+
+}  // namespace
+
+extern "C" int64_t mxfp8_lora_tn_noalloc_chunks(int64_t T, int64_t K, int64_t rp) {
+  if (T <= 0 || K <= 0 || K % 128 || rp <= 0) return 0;
+  const int64_t fit = kNoAllocScratchBytes / 4 / (rp * K);
+  return std::min(mxfp8_lora_tn_chunks(T, K), fit);
+}
+
+extern "C" int mxfp8_lora_tn_noalloc(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp,
+                                     float scale, int64_t transpose, int64_t out_f32, void* out, void* stream) {
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && (rp == 16 || rp == 32 || rp == 64),
+               "mxfp8_lora_tn_noalloc: need T > 0, K %% 128 == 0, rp in {16, 32, 64}");
+  MX_CHECK_ARG(rp * K * 4 <= kNoAllocScratchBytes,
+               "mxfp8_lora_tn_noalloc: rp * K * 4 = %lld bytes exceeds the %lld-byte static scratch",
+               (long long)(rp * K * 4), (long long)kNoAllocScratchBytes);
+  float* part = scratch_on_current_device();
+  if (!part) return MXFP8_ERR_ARG;
+  return lora_tn_launch(x, T, K, ld_x, p, rp, mxfp8_lora_tn_noalloc_chunks(T, K, rp), part, scale, transpose, out_f32,
+                        out, stream);
 }
 
 extern "C" int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part, const float* dbu_part,
