@@ -21,6 +21,7 @@ namespace {
 constexpr int kTile = 128;
 constexpr int kThreads = 256;
 constexpr int kLdT = kTile + 8;  // bf16 row stride of the LDS copy used by the transposed axis (16-B aligned)
+constexpr int kLdC = kTile + 16;  // byte row stride of the LDS tile of transposed codes (16-B aligned)
 
 // Quantize 8 consecutive bf16 (one uint4) whose 4-lane group forms one 32-block; returns the codes and the
 // block's scale byte.
@@ -45,6 +46,7 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
   __shared__ uint32_t stile[kTile];                          // row-axis scale tile (512 B)
   __shared__ uint32_t sttile[kTile];                         // transposed-axis scale tile
   __shared__ __attribute__((aligned(16))) uint16_t xt[kCols ? kTile * kLdT : 1];
+  __shared__ __attribute__((aligned(16))) uint8_t qtt[kCols ? kTile * kLdC : 16];  // the xᵀ tile's codes
   const int tid = threadIdx.x;
   const int64_t ct = blockIdx.x;  // column tile
   const int64_t rt = blockIdx.y;  // row tile
@@ -86,7 +88,6 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
     const int cl = wv * 32 + (lane & 15) * 2;  // first of the 2 columns within the tile
     const int rg = lane >> 4;                   // 8-row group within a 32-row block
     uint8_t* stb = reinterpret_cast<uint8_t*>(sttile);
-    const int64_t n_rows_t = rows;              // row count of x = column count of xᵀ
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
       float a0[8], a1[8];
@@ -105,11 +106,11 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
       m1 = max(m1, (uint32_t)__shfl_xor((int)m1, 16));
       m1 = max(m1, (uint32_t)__shfl_xor((int)m1, 32));
       const uint32_t e0 = e8m0_from_amax_bits(m0), e1 = e8m0_from_amax_bits(m1);
-      const int64_t c0 = ct * kTile + cl;                 // row of xᵀ
-      const int64_t r0 = rt * kTile + rb * 32 + rg * 8;   // first column of xᵀ
-      *reinterpret_cast<uint2*>(qt + c0 * n_rows_t + r0) =
+      // codes of xᵀ rows cl, cl + 1 (tile-local), columns rb*32 + rg*8 .. + 7, into the LDS tile
+      const int cc = rb * 32 + rg * 8;
+      *reinterpret_cast<uint2*>(qtt + cl * kLdC + cc) =
           make_uint2(encode4(a0[0], a0[1], a0[2], a0[3], e0), encode4(a0[4], a0[5], a0[6], a0[7], e0));
-      *reinterpret_cast<uint2*>(qt + (c0 + 1) * n_rows_t + r0) =
+      *reinterpret_cast<uint2*>(qtt + (cl + 1) * kLdC + cc) =
           make_uint2(encode4(a1[0], a1[1], a1[2], a1[3], e1), encode4(a1[4], a1[5], a1[6], a1[7], e1));
       if (rg == 0) {
         stb[(cl & 31) * 16 + (cl >> 5) * 4 + rb] = (uint8_t)e0;
@@ -118,6 +119,15 @@ __global__ __launch_bounds__(kThreads) void quant_kernel(const uint16_t* __restr
     }
   }
   __syncthreads();
+  if (kCols) {
+    // the xᵀ tile leaves as whole 128-byte row pieces: 8 lanes per row, 16 bytes each, 32 rows per pass
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int rr = (tid >> 3) + 32 * j, ch = tid & 7;
+      store_codes<MX_NT_QUANT>(qt + (ct * kTile + rr) * rows + rt * kTile + ch * 16,
+                               *reinterpret_cast<const uint4*>(qtt + rr * kLdC + ch * 16));
+    }
+  }
   if (kRows && tid < 32)
     store_codes<MX_NT_QUANT>(s + (rt * s_col_tiles + s_tile0 + ct) * 512 + tid * 16,
                              reinterpret_cast<const uint4*>(stile)[tid]);

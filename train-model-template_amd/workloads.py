@@ -56,6 +56,13 @@ def quant_bytes(rows, cols, dual=False):
     return rows * cols * 4 + s + st
 
 
+def quant_lora_bytes(T, K, rp, transposed=False):
+    """Algorithmic HBM bytes of one quant_lora over x [T, K] bf16 with w [rp, K]: read x and w, write the MX codes
+    and blocked scales of x and the bf16 product [T, rp] (with its zero-padded transpose [rp, ceil(T/128)*128])."""
+    tpad = -(-T // 128) * 128
+    return quant_bytes(T, K) + rp * K * 2 + T * rp * 2 + (rp * tpad * 2 if transposed else 0)
+
+
 def lora_bwd_bytes(T, N, r, quant=True):
     """Algorithmic HBM bytes of one lora_bwd over dy [T, N] bf16: read dy, xa [T, r], B [N, r]; write d(xa) [T, r]
     bf16 and dB [N, r] fp32; with quantization also the codes and blocked scales of dy (the partial sums are
