@@ -46,6 +46,7 @@ for p in (ROOT, os.path.join(ROOT, "train-model-template_amd")):
 PEAK_MXFP8_TFLOPS = 5000.0  # MI355X dense MXFP8 (f8f6f4 MFMA) peak, public figure
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E peak
 COPY_CALIB_BYTES = 1 << 30  # bytes read (and written) by one --copy-calib launch
+N_XCD = 8                   # accelerator complex dies of an MI355X (GRBM_GUI_ACTIVE counts on each)
 
 
 def _traffic_path(cfg, ext):
@@ -393,6 +394,98 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
                       "algorithmic_bytes_per_launch": summary["algorithmic_bytes_per_launch"]}))
 
 
+def _kernel_key(name, grid):
+    """A short kernel name: the template head of the demangled name, and for the MX GEMM the MLP shape its grid
+    and epilogue rank identify at configuration 3 (4032 / 2016 / 672 workgroups of 256 threads)."""
+    m = re.search(r"(\w+_kernel)(<[^>]*>)?", name)
+    k = (m.group(1) + (m.group(2) or "")) if m else name[:48]
+    if m and m.group(1) == "gemm_kernel":
+        wg = int(grid) // 256 if grid else 0
+        shape = {(4032, "0"): "gate|up", (2016, "0"): "dh", (672, "16"): "down", (672, "32"): "dx"}
+        r = (m.group(2) or "<0").strip("<>").split(",")[0].strip()
+        k += " " + shape.get((wg, r), f"{wg} WGs")
+    return k
+
+
+def _counters_summary(name, dirs, cmds):
+    """Per-kernel medians over the dispatches of the rocprofv3 --pmc passes in `dirs` (one counter set per pass; each dispatch row
+    carries its start and end timestamps), with the derived figures: sustained shader clock = GRBM_GUI_ACTIVE / kernel duration; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES
+    / (GRBM_GUI_ACTIVE x 256 CUs x 4 SIMDs); FP8 MFMA flops = 512 x SQ_INSTS_VALU_MFMA_MOPS_F8; L2 hit rate =
+    TCC_HIT / (TCC_HIT + TCC_MISS); TA / TD busy = TA_TA_BUSY_sum / TD_TD_BUSY_sum / (GRBM_GUI_ACTIVE x 256); HBM read / write = FETCH_SIZE
+    / WRITE_SIZE scaled by their reading on a 1 GiB copy kernel in the same pass (--copy-calib).
+    Writes profiles/<name>.md and .json."""
+    per = {}  # kernel key -> counter -> [per-dispatch values]
+    for d in dirs:
+        dur, vals = {}, {}
+        for row in _pmc_rows(d):
+            k = (row["Dispatch_Id"], row["Kernel_Name"], row.get("Grid_Size", ""))
+            vals.setdefault(k, {})
+            c = row["Counter_Name"]
+            vals[k][c] = vals[k].get(c, 0.0) + float(row["Counter_Value"])
+            dur[row["Dispatch_Id"]] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+        # FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled to bytes by what they read on the 1 GiB copy kernel
+        for c in ("FETCH_SIZE", "WRITE_SIZE"):
+            calib = sorted(cs[c] for (_, kname, _), cs in vals.items() if "neg" in kname and c in cs)
+            for cs in vals.values():
+                if c in cs:
+                    cs[c] = cs[c] * COPY_CALIB_BYTES / calib[len(calib) // 2] if calib else float("nan")
+        for (did, kname, grid), cs in vals.items():
+            if "at::native" in kname:  # torch's own kernels (input generation, the copy calibration)
+                continue
+            key = _kernel_key(kname, grid)
+            ent = per.setdefault(key, {})
+            for c, v in cs.items():
+                ent.setdefault(c, []).append(v)
+            if did in dur and "GRBM_GUI_ACTIVE" in cs:
+                ent.setdefault("_clock_mhz", []).append(cs["GRBM_GUI_ACTIVE"] / dur[did] * 1e3)
+            if did in dur:
+                ent.setdefault("_us_" + os.path.basename(d.rstrip("/")), []).append(dur[did] / 1e3)
+    med = lambda v: sorted(v)[len(v) // 2] if v else float("nan")  # noqa: E731  (robust to a warm-up dispatch)
+    table = {}
+    for key, ent in per.items():
+        m = {c: med(v) for c, v in ent.items()}
+        if "GRBM_GUI_ACTIVE" in m:  # summed over the 8 XCDs' graphics register bus managers
+            m["GRBM_GUI_ACTIVE"] /= N_XCD
+            m["_clock_mhz"] /= N_XCD
+        gui = m.get("GRBM_GUI_ACTIVE")
+        row = {"dispatches": max(len(v) for v in ent.values())}
+        us = [v for c, v in m.items() if c.startswith("_us_")]
+        if "_clock_mhz" in m and us and min(us) >= 50:  # short dispatches: profiling overhead dominates GUI_ACTIVE
+            row["clock_MHz"] = round(m["_clock_mhz"])
+        if gui and "SQ_VALU_MFMA_BUSY_CYCLES" in m:
+            row["mfma_busy"] = round(m["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * 256 * 4), 4)
+        if "SQ_INSTS_VALU_MFMA_MOPS_F8" in m:
+            row["fp8_mfma_GFLOP"] = round(512 * m["SQ_INSTS_VALU_MFMA_MOPS_F8"] / 1e9, 1)
+        if "TCC_HIT_sum" in m and "TCC_MISS_sum" in m and m["TCC_HIT_sum"] + m["TCC_MISS_sum"] > 0:
+            row["l2_hit"] = round(m["TCC_HIT_sum"] / (m["TCC_HIT_sum"] + m["TCC_MISS_sum"]), 4)
+        for c, out_name in (("FETCH_SIZE", "hbm_read_MB"), ("WRITE_SIZE", "hbm_write_MB")):
+            if c in m:
+                row[out_name] = round(m[c] / 1e6, 1)
+        for c, out_name in (("TA_TA_BUSY_sum", "ta_busy"), ("TD_TD_BUSY_sum", "td_busy")):
+            if c in m and gui:
+                row[out_name] = round(m[c] / (gui * 256), 4)
+        for c, v in m.items():
+            if c.startswith("_us_"):
+                row["us[" + c[4:] + "]"] = round(v, 1)
+        table[key] = row
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, "profiles", name + ".json"), "w") as f:
+        json.dump({"commands": cmds, "kernels": table}, f, indent=1)
+    cols = sorted({c for r in table.values() for c in r})
+    with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
+        f.write(f"# rocprofv3 counters per kernel: {name}\n\n")
+        f.write("Commands (GPU box, one pass each; repo root as `$GRAFT_REPO_ROOT`):\n\n```\ncd /tmp && export "
+                "TMPDIR=/tmp\n" + "\n".join(cmds) + "\n```\n\n")
+        f.write(_counters_summary.__doc__.split("derived figures:")[1].split("Writes")[0].strip()
+                .replace("\n    ", " ") + "\n\n")
+        f.write("Durations (`us[...]`) are each pass's own dispatch timestamps (counter collection serializes and "
+                "instruments every dispatch, so they run a little longer than in the timed bench).\n\n")
+        f.write("| kernel | " + " | ".join(cols) + " |\n|" + "---|" * (len(cols) + 1) + "\n")
+        for key in sorted(table):
+            f.write(f"| {key} | " + " | ".join(str(table[key].get(c, "")) for c in cols) + " |\n")
+    print(json.dumps(table))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -407,7 +500,13 @@ def main():
                     "(one JSON line of those figures, not the MLP metric line): the profiling command of that section")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"))
     ap.add_argument("--traffic-commands", nargs=2, default=("", ""), metavar=("CMD_FETCH", "CMD_WRITE"))
+    ap.add_argument("--counters-summary", nargs="+", metavar=("NAME", "DIR"),
+                    help="summarize rocprofv3 --pmc passes (each with --kernel-trace) into profiles/NAME.{md,json}")
+    ap.add_argument("--counters-commands", nargs="*", default=[], help="the profiling commands, for the summary")
     args = ap.parse_args()
+    if args.counters_summary:
+        _counters_summary(args.counters_summary[0], args.counters_summary[1:], args.counters_commands)
+        return
     if args.traffic_summary:
         _traffic_summary(args.config, *args.traffic_summary, *args.traffic_commands)
         return
