@@ -402,8 +402,12 @@ def _kernel_key(name, grid):
     if m and m.group(1) == "gemm_kernel":
         wg = int(grid) // 256 if grid else 0
         shape = {(4032, "0"): "gate|up", (2016, "0"): "dh", (672, "16"): "down", (672, "32"): "dx"}
-        r = (m.group(2) or "<0").strip("<>").split(",")[0].strip()
-        k += " " + shape.get((wg, r), f"{wg} WGs")
+        targs = [a.strip() for a in (m.group(2) or "<0").strip("<>").split(",")]
+        r = targs[0]
+        if len(targs) > 2 and targs[2] == "true":
+            k += " gate|up + SwiGLU epilogue"
+        else:
+            k += " " + shape.get((wg, r), f"{wg} WGs")
     return k
 
 
@@ -486,6 +490,43 @@ def _counters_summary(name, dirs, cmds):
     print(json.dumps(table))
 
 
+def _trace_summary(name, d, steps, cmd):
+    """rocprofv3 --kernel-trace of a bench run in `d` -> profiles/<name>.md: per kernel (the MX GEMM split into
+    its MLP shapes by _kernel_key) the launches, the median duration, and the share of a step = median x
+    round(launches / steps), where `steps` counts every step the profiled process ran (timed + warmup)."""
+    files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {d}")
+    durs = {}
+    for f in files:
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                kname = row["Kernel_Name"]
+                if "at::native" in kname:
+                    m = re.search(r"at::native::(?:\(anonymous namespace\)::)?([A-Za-z_0-9]+)", kname)
+                    key = "torch " + (m.group(1) if m else kname[:30])
+                else:
+                    grid = int(row["Grid_Size_X"]) * int(row["Grid_Size_Y"]) * int(row["Grid_Size_Z"])
+                    key = _kernel_key(kname, str(grid))
+                durs.setdefault(key, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+    rows = []
+    for key, v in durs.items():
+        med = sorted(v)[len(v) // 2]
+        rows.append((key, len(v), med, med * round(len(v) / steps)))
+    rows.sort(key=lambda r: -r[3])
+    tot = sum(r[3] for r in rows)
+    with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
+        f.write(f"# Kernel trace: {name}\n\nCommand (GPU box, repo root as `$GRAFT_REPO_ROOT`):\n\n```\ncd /tmp && "
+                f"export TMPDIR=/tmp\n{cmd}\npython3 bench.py --trace-summary {name} <trace dir> {steps:g}\n```\n\n")
+        f.write(f"The profiled process runs {steps:g} steps (timed + warmup), one forward for the gating check and the "
+                "one-off weight preparation. 'per step' = median duration x round(launches / steps); one-off kernels "
+                "show 0.\n\n| kernel | launches | median us | us per step | % |\n|---|---|---|---|---|\n")
+        for key, n, med, ps in rows:
+            f.write(f"| {key} | {n} | {med:.1f} | {ps:.1f} | {100 * ps / tot if tot else 0:.1f} |\n")
+        f.write(f"\nSum of kernel time per step: {tot:.1f} us.\n")
+    print(json.dumps({k: round(ps, 1) for k, _, _, ps in rows}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -503,7 +544,13 @@ def main():
     ap.add_argument("--counters-summary", nargs="+", metavar=("NAME", "DIR"),
                     help="summarize rocprofv3 --pmc passes (each with --kernel-trace) into profiles/NAME.{md,json}")
     ap.add_argument("--counters-commands", nargs="*", default=[], help="the profiling commands, for the summary")
+    ap.add_argument("--trace-summary", nargs=3, metavar=("NAME", "DIR", "STEPS"),
+                    help="summarize a rocprofv3 --kernel-trace run of STEPS steps into profiles/NAME.md")
+    ap.add_argument("--trace-command", default="", help="the profiling command, for the summary")
     args = ap.parse_args()
+    if args.trace_summary:
+        _trace_summary(args.trace_summary[0], args.trace_summary[1], float(args.trace_summary[2]), args.trace_command)
+        return
     if args.counters_summary:
         _counters_summary(args.counters_summary[0], args.counters_summary[1:], args.counters_commands)
         return

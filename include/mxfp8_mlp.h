@@ -263,6 +263,22 @@ int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q,
  */
 int mxfp8_transpose_pad(const void* x, int64_t T, int64_t C, int64_t ld_x, void* out, int64_t Tpad, void* stream);
 
+/*
+ * The gate|up MX GEMM with the SwiGLU forward fused into its epilogue: one launch replacing
+ * torch._scaled_mm(q, hold.w) + _fwd_kernel (/root/reference/scripts/fused_mlp.py:279-282, :65-109):
+ *   gu = bf16(MX(x) · W_guᵀ) [M, 2N] (gate | up, the tensor the forward saves) in the fused-tile layout;
+ *   g = bf16(gu_g + s_g · xs_g·B_gᵀ), u = bf16(gu_u + s_u · xs_u·B_uᵀ), h = bf16(g / (exp(-g) + 1) · u);
+ *   MX(h) -> q_h (MX-tiled, [ceil(M/16)*16, N]) and s_h (blocked, ceil(M/128) tile rows; padded rows 0);
+ *   part [2N/128, M, r] fp32: each output tile's xS_down = h · A_dᵀ over its 64 columns (add them in order).
+ * a / sa: MX-tiled codes and blocked scales of x [M, K]; b / sb: W_gu [2N, K] in the fused row order (output
+ * tile t holds gate columns 64t..64t+63 then up columns 64t..64t+63, each 32-row block permuted by
+ * pi_col(a) = ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3)), MX-tiled, with its blocked scales.  xs [M, 2r],
+ * bg, bu [N, r], ad [r, N] bf16.  N % 128 == 0, K % 128 == 0, r in {16, 32}, M * 2N < 2^31.
+ */
+int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* b, const void* sb, int64_t M, int64_t N, int64_t K,
+                          const void* xs, const void* bg, const void* bu, const void* ad, int64_t r, float s_g,
+                          float s_u, void* gu, void* q_h, void* s_h, float* part, void* stream);
+
 /* Token chunks mxfp8_lora_tn uses for [T, K] (its partial buffer holds chunks * rp * K floats). */
 int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);
 

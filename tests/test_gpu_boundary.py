@@ -1,7 +1,8 @@
 """GPU checks of the drop-in boundary around the fused MLP and the generic MX linear.
 
-  - _MLP.backward returns the reference's dtypes and shapes (/root/reference/scripts/fused_mlp.py:306-336:
-    dx in x.dtype, dA_g / dA_u / dB_d bf16 from bf16 GEMMs, dB_g / dB_u / dA_d fp32 partial sums);
+  - _MLP.backward returns the reference's values and shapes (/root/reference/scripts/fused_mlp.py:306-336: dx in
+    x.dtype; dA_g / dA_u / dB_d bf16 values from bf16 GEMMs, held in the adapter parameter's dtype, which is what
+    autograd casts the reference's bf16 returns to; dB_g / dB_u / dA_d fp32 partial sums);
   - the saved set is the reference's eight tensors; backward finds the transposed LoRA forms through the
     per-step cast cache and rebuilds them when the cache was cleared or the saved tensors come back as other
     objects (non-reentrant checkpointing): the gradients are bit-identical in every case;
@@ -67,12 +68,25 @@ def test_backward_returns_reference_dtypes(gpu):
     dx, m, n, dA_g, dB_g, dA_u, dB_u, dA_d, dB_d = out
     K, N, r = x.shape[-1], mod.gate_proj.base_layer.out_features, 16
     assert m is None and n is None
-    want = dict(dx=(torch.bfloat16, (256, K)), dA_g=(torch.bfloat16, (r, K)), dB_g=(torch.float32, (N, r)),
-                dA_u=(torch.bfloat16, (r, K)), dB_u=(torch.float32, (N, r)), dA_d=(torch.float32, (r, N)),
-                dB_d=(torch.bfloat16, (K, r)))
+    # the PEFT-shaped adapters are fp32 parameters: dA_g, dA_u, dB_d come back as fp32 holding bf16 values
+    want = dict(dx=(torch.bfloat16, (256, K)), dA_g=(torch.float32, (r, K)), dB_g=(torch.float32, (N, r)),
+                dA_u=(torch.float32, (r, K)), dB_u=(torch.float32, (N, r)), dA_d=(torch.float32, (r, N)),
+                dB_d=(torch.float32, (K, r)))
     got = dict(dx=dx, dA_g=dA_g, dB_g=dB_g, dA_u=dA_u, dB_u=dB_u, dA_d=dA_d, dB_d=dB_d)
     for k, (dt, shape) in want.items():
         assert got[k].dtype == dt and tuple(got[k].shape) == shape, (k, got[k].dtype, tuple(got[k].shape))
+    for k in ("dA_g", "dA_u", "dB_d"):  # the values of the reference's bf16 GEMM outputs
+        assert torch.equal(got[k], got[k].to(torch.bfloat16).float()), k
+    # with bf16 adapter parameters the same returns are bf16
+    for m in (mod.gate_proj, mod.up_proj, mod.down_proj):
+        m.lora_A["default"].to(torch.bfloat16)
+        m.lora_B["default"].to(torch.bfloat16)
+    fused_linear.new_step()
+    x.grad = None
+    y = fused_mlp.mlp(mod, x)
+    out16 = y.grad_fn.apply(inps[0]["dy"].to(gpu))
+    for k, t in zip(("dA_g", "dA_u", "dB_d"), (out16[3], out16[5], out16[8])):
+        assert t.dtype == torch.bfloat16 and torch.equal(t.float(), got[k]), k
 
 
 def test_cleared_cache_and_checkpoint_give_identical_gradients(gpu):

@@ -28,6 +28,8 @@ SIGNATURES = {
     "mxfp8_gemm_nt": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
                       _i64, _f32, _i64, _ptr, _i64, _ptr],
     "mxfp8_gemm_workspace_size": [_i64, _i64, _i64],
+    "mxfp8_gemm_swiglu_fwd": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _f32, _f32, _ptr,
+                              _ptr, _ptr, _ptr],
     "mxfp8_gemm_nt_seg": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64,
                           _ptr, _i64, _i64, _f32, _i64, _ptr],
     "mxfp8_mlp_fwd_groups": [_i64, _i64, _i64],
@@ -193,6 +195,12 @@ def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, lay
         ldp, ldq = p.stride(0), q.stride(0)
     call("mxfp8_gemm_nt_seg", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, n, cols, ptrs, lds, _p(p), ldp, _p(q),
          ldq, r, float(alpha), layout, like=outs[0])
+
+
+def gemm_swiglu_fwd(a, sa, b, sb, M, N, K, xs, bg, bu, ad, s_g, s_u, gu, q_h, s_h, part):
+    """gate|up MX GEMM with the SwiGLU forward in its epilogue (include/mxfp8_mlp.h, mxfp8_gemm_swiglu_fwd)."""
+    call("mxfp8_gemm_swiglu_fwd", _p(a), _p(sa), _p(b), _p(sb), M, N, K, _p(xs), _p(bg), _p(bu), _p(ad), ad.shape[0],
+         float(s_g), float(s_u), _p(gu), _p(q_h), _p(s_h), _p(part), like=gu)
 
 
 def mlp_fwd(gu, xs, bg, bu, ad, T, N, r, s_g, s_u, q, s, part, n_groups, h_out=None, q_layout=0):

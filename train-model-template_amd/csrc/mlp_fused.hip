@@ -29,74 +29,7 @@ using namespace mxk;
 
 namespace {
 
-
 __device__ __forceinline__ int tile_col(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
-
-
-
-// 8 bf16 of row `p` at columns base + {lg*4 + 0..3} and base + 8 + {lg*4 + 0..3} (one k-step of the permuted
-// column order; lg = lane / 32)
-__device__ __forceinline__ v8bf load_bf8_perm(const uint16_t* p, int base, int lg) {
-  uint2 a = *reinterpret_cast<const uint2*>(p + base + lg * 4);
-  uint2 b = *reinterpret_cast<const uint2*>(p + base + 8 + lg * 4);
-  return as_bf8(make_uint4(a.x, a.y, b.x, b.y));
-}
-
-// registers 8s..8s+7 of a bf16-valued element tile as an MFMA operand
-__device__ __forceinline__ v8bf regs_bf8(const float* v) {
-  uint4 u;
-  u.x = (__float_as_uint(v[0]) >> 16) | (__float_as_uint(v[1]) & 0xffff0000u);
-  u.y = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[3]) & 0xffff0000u);
-  u.z = (__float_as_uint(v[4]) >> 16) | (__float_as_uint(v[5]) & 0xffff0000u);
-  u.w = (__float_as_uint(v[6]) >> 16) | (__float_as_uint(v[7]) & 0xffff0000u);
-  return as_bf8(u);
-}
-
-// 16 bf16 of the lane's row at columns jb + tile_col(i): four 8-byte loads, zeros for rows past the end
-__device__ __forceinline__ void load_tile(const uint16_t* row, int jb, int lane, bool valid, float* v) {
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    uint2 w = valid ? *reinterpret_cast<const uint2*>(row + jb + g * 8 + (lane >> 5) * 4) : make_uint2(0, 0);
-    v[4 * g + 0] = bf16_lo(w.x);
-    v[4 * g + 1] = bf16_hi(w.x);
-    v[4 * g + 2] = bf16_lo(w.y);
-    v[4 * g + 3] = bf16_hi(w.y);
-  }
-}
-
-// D[j][m] = Σ_ρ W[j, ρ] · X[m, ρ] for the 32 x 32 tile (W rows jb.., X rows of this lane), r in {16, 32}
-template <int R>
-__device__ __forceinline__ v16f lora_tile(const uint16_t* wrow, const v8bf* xf) {
-  v16f d = v16f{};
-#pragma unroll
-  for (int h = 0; h < R / 16; ++h) d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(load_bf8(wrow + h * 16), xf[h], d, 0, 0, 0);
-  return d;
-}
-
-// Quantize one 32-column block of the lane's row held as 8 packed bf16 pairs w[0..7] (columns
-// tile_col(2k), tile_col(2k+1)) plus the other 16 values in lane ^ 32: codes of row mc, columns jb..jb+31
-// (4-byte pieces) into q, row-major with Kq codes per row or MX-tiled (tiled_offset) with Kq codes per row;
-// scale byte into the blocked layout (lanes < 32), or scale 0 for padded rows.
-__device__ __forceinline__ void quant_tile(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
-                                           int64_t Kq, bool tiled, int jb, uint8_t* s, int64_t s_col_tiles) {
-  u16x2 mm = {0, 0};
-#pragma unroll
-  for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
-  uint32_t am = amax_bits(mm);
-  am = max(am, (uint32_t)__shfl_xor((int)am, 32));
-  const uint32_t e = e8m0_from_amax_bits(am);
-  uint32_t c[4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) c[g] = encode4_bf16(w[2 * g], w[2 * g + 1], e);
-  if (live) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int64_t k = jb + g * 8 + (lane >> 5) * 4;
-      store_codes<MX_NT_FUSED>(q + (tiled ? tiled_offset(mc, k, Kq) : mc * Kq + k), c[g]);
-    }
-  }
-  if (lane < 32) store_scale<MX_NT_FUSED>(s + blocked_offset(m, jb >> 5, s_col_tiles), live ? (uint8_t)e : (uint8_t)0);
-}
 
 // registers 8s..8s+7 of an element tile held as packed words w[4s..4s+3], as an MFMA operand
 __device__ __forceinline__ v8bf words_bf8(const uint32_t* w) { return as_bf8(make_uint4(w[0], w[1], w[2], w[3])); }
@@ -465,17 +398,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   }
 }
 
-// out[i] = cast(scale * Σ_p part[p * count + i]), p ascending
-template <bool kBf16>
+// out[i] = cast(scale * Σ_p part[p * count + i]), p ascending.  kVec: four outputs per thread with 16-byte loads
+// (count % 4 == 0); either way eight partials are loaded before they are added (in order), so a thread waits
+// for one memory latency per eight partials, not one per partial.
+template <bool kBf16, bool kVec>
 __global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict__ part, int64_t n_parts,
                                                         int64_t count, float scale, void* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  typedef typename std::conditional<kVec, float4, float>::type F;
+  constexpr int kW = kVec ? 4 : 1;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * kW;
   if (i >= count) return;
-  float v = part[i];
-  for (int64_t p = 1; p < n_parts; ++p) v += part[p * count + i];
-  v *= scale;
-  if (kBf16) reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(v);
-  else reinterpret_cast<float*>(out)[i] = v;
+  const F* src = reinterpret_cast<const F*>(part + i);
+  const int64_t stride = count / kW;  // in units of F
+  auto add = [](F& a, const F& b) {
+    if constexpr (kVec) {
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    } else {
+      a += b;
+    }
+  };
+  F v = src[0];
+  int64_t p = 1;
+  for (; p + 7 < n_parts; p += 8) {
+    F x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = src[(p + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) add(v, x[u]);
+  }
+  for (; p < n_parts; ++p) add(v, src[p * stride]);
+  const float* f = reinterpret_cast<const float*>(&v);
+#pragma unroll
+  for (int k = 0; k < kW; ++k) {
+    const float o = f[k] * scale;
+    if (kBf16) reinterpret_cast<uint16_t*>(out)[i + k] = (uint16_t)f32_to_bf16_bits(o);
+    else reinterpret_cast<float*>(out)[i + k] = o;
+  }
 }
 
 }  // namespace
@@ -595,11 +553,17 @@ extern "C" int mxfp8_sum_parts(const float* part, int64_t n_parts, int64_t count
                                int out_bf16, void* stream) {
   MX_CHECK_ARG(part && out && n_parts > 0 && count >= 0, "mxfp8_sum_parts: bad arguments");
   if (count == 0) return MXFP8_OK;
-  const int64_t blocks = (count + 255) / 256;
+  const bool vec = count % 4 == 0 && mx_aligned(part, 16);
+  const int64_t blocks = (count / (vec ? 4 : 1) + 255) / 256;
   MX_CHECK_ARG(blocks < (1LL << 31), "mxfp8_sum_parts: too large");
   hipStream_t stm = (hipStream_t)stream;
-  if (out_bf16) sum_parts_kernel<true><<<(unsigned)blocks, 256, 0, stm>>>(part, n_parts, count, scale, out);
-  else sum_parts_kernel<false><<<(unsigned)blocks, 256, 0, stm>>>(part, n_parts, count, scale, out);
+  if (vec) {
+    if (out_bf16) sum_parts_kernel<true, true><<<(unsigned)blocks, 256, 0, stm>>>(part, n_parts, count, scale, out);
+    else sum_parts_kernel<false, true><<<(unsigned)blocks, 256, 0, stm>>>(part, n_parts, count, scale, out);
+  } else {
+    if (out_bf16) sum_parts_kernel<true, false><<<(unsigned)blocks, 256, 0, stm>>>(part, n_parts, count, scale, out);
+    else sum_parts_kernel<false, false><<<(unsigned)blocks, 256, 0, stm>>>(part, n_parts, count, scale, out);
+  }
   MX_CHECK_LAUNCH("mxfp8_sum_parts");
   return MXFP8_OK;
 }

@@ -86,6 +86,24 @@ struct Lora {
   float alpha;
 };
 
+// Fused SwiGLU forward epilogue (kSw): the operands beyond the GEMM's.  The B operand is W_gu = [W_gate; W_up] in
+// the fused row order (fused_swiglu_row in the host code): output tile t (128 columns) holds gate columns
+// 64 t + 0..63 and then up columns 64 t + 0..63, each 32-column block with its weight rows permuted by pi_col,
+// so that acc[b][mt] (gate) and acc[2 + b][mt] (up) hold, in lane l, row m = l % 32 and the 16 CONTIGUOUS
+// columns jb + (l / 32) * 16 + i (jb = 64 t + 32 b): the layout of the fused forward kernel and of the FT blocks.
+struct SwEpi {
+  const uint16_t* xs;  // [M, 2r] bf16: x · [A_g; A_u]ᵀ
+  const uint16_t* bg;  // [N, r] bf16 LoRA B of gate
+  const uint16_t* bu;  // [N, r] bf16 LoRA B of up
+  const uint16_t* ad;  // [r, N] bf16 LoRA A of down
+  float s_g, s_u;
+  uint16_t* gu;        // [ceil(M/32)*32, 2N] bf16 GEMM output (gate | up), fused-tile layout
+  uint8_t* q;          // [ceil(M/16)*16, N] MX-tiled codes of h
+  uint8_t* s;          // blocked scales of h (ceil(M/128) tile rows, N/128 tiles)
+  float* part;         // [2N/128, M, r] xS_down partials, one per output tile
+  int N;               // d_ffn
+};
+
 // Output columns in up to four segments, each its own row-major matrix: columns [col0[k], col0[k + 1]) of the
 // product go to ptr[k] with row stride ld[k] (segment boundaries are multiples of the tile width, so a tile
 // writes into one segment).  One segment = the plain C, ldc.
@@ -126,10 +144,11 @@ __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw
   return r;
 }
 
-template <int kR, int kNW>
+template <int kR, int kNW, bool kSw>
 __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, int64_t lda, const uint8_t* __restrict__ B,
-    const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, CSeg cseg, Lora lora, Plan plan, int tiled) {
+    const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, CSeg cseg, Lora lora, Plan plan, int tiled,
+    SwEpi swe) {
   using S = Shape<kNW>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[S::kStages * S::kStageBytes];
   __shared__ int arrived;
@@ -324,6 +343,109 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
     if (tid == 0) __hip_atomic_store(plan.cnt + st_, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  if constexpr (kSw) {
+    // SwiGLU forward (fused_mlp.py:65-109, the _fwd_kernel math): gu = bf16(acc) is stored as the saved GEMM
+    // output, then g = bf16(gu_g + s_g xs_g·B_gᵀ), u = bf16(gu_u + s_u xs_u·B_uᵀ), h = bf16(silu(g) u), MX(h)
+    // into the down GEMM's operand and the tile's xS_down partial h·A_dᵀ, per 32 x 32 block of the wave.
+    // Every small operand of the tile is loaded first, at once (the main loop's fragment registers are free
+    // now), so the epilogue waits for one memory latency instead of one per product.
+    constexpr int R = kR, H = R / 16;
+    const int Nf = swe.N, lg = lane >> 5, rho = lane & 31;
+    const int t64 = n0 >> 1;                      // first gate / up column of the tile: 64 * (n0 / 128)
+    const int srows = (M + 127) / 128 * 128;      // rows of the blocked scale buffer of h
+    v8bf xg[2][H], xu[2][H], wg[2][H], wu[2][H], af[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int mc = min(m0 + wm * 64 + mt * 32 + (lane & 31), M - 1);
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        xg[mt][h] = load_bf8(swe.xs + (int64_t)mc * 2 * R + h * 16 + lg * 8);
+        xu[mt][h] = load_bf8(swe.xs + (int64_t)mc * 2 * R + R + h * 16 + lg * 8);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int jb = t64 + 32 * b;
+      const int64_t wr = (int64_t)(jb + pi_col(lane & 31)) * R + lg * 8;
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        wg[b][h] = load_bf8(swe.bg + wr + h * 16);
+        wu[b][h] = load_bf8(swe.bu + wr + h * 16);
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {  // A_d[ρ, jb + lg*16 + 8 ks + 0..7], ρ = lane % 32 (zero rows past r)
+        const v8bf a = load_bf8(swe.ad + (int64_t)(rho < R ? rho : 0) * Nf + jb + lg * 16 + 8 * ks);
+        af[b][ks] = rho < R ? a : v8bf{};
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int m = m0 + wm * 64 + mt * 32 + (lane & 31);
+      const bool live = m < M;
+      v16f xacc = v16f{};  // xS_down partial D[ρ][m] over the tile's 64 columns
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int jb = t64 + 32 * b;
+        uint32_t gw[8], hw[8];  // gate, then g; up, then u, then h (packed bf16 pairs, columns lg*16 + 2k, +1)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          gw[k] = pack_bf16x2(acc[b][mt][2 * k], acc[b][mt][2 * k + 1]);
+          hw[k] = pack_bf16x2(acc[2 + b][mt][2 * k], acc[2 + b][mt][2 * k + 1]);
+        }
+        if (live) {  // the lane's columns i = 0..7 and 8..15 are 16 contiguous bytes each in an FT block
+          uint16_t* pg = swe.gu + ft_offset(m, jb + lg * 16, 2 * Nf);
+          uint16_t* pu = swe.gu + ft_offset(m, Nf + jb + lg * 16, 2 * Nf);
+          *reinterpret_cast<uint4*>(pg) = make_uint4(gw[0], gw[1], gw[2], gw[3]);
+          *reinterpret_cast<uint4*>(pg + 512) = make_uint4(gw[4], gw[5], gw[6], gw[7]);
+          *reinterpret_cast<uint4*>(pu) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+          *reinterpret_cast<uint4*>(pu + 512) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+        }
+        {
+          const v16f d = lora_pi<R>(wg[b], xg[mt]);
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            float g0 = bf16_lo(gw[i / 2]) + swe.s_g * d[i], g1 = bf16_hi(gw[i / 2]) + swe.s_g * d[i + 1];
+            gw[i / 2] = rnd2(g0, g1);
+          }
+        }
+        {
+          const v16f d = lora_pi<R>(wu[b], xu[mt]);
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            float u0 = bf16_lo(hw[i / 2]) + swe.s_u * d[i], u1 = bf16_hi(hw[i / 2]) + swe.s_u * d[i + 1];
+            hw[i / 2] = rnd2(u0, u1);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const float g0 = bf16_lo(gw[k]), g1 = bf16_hi(gw[k]);
+          float h0 = (g0 * fast_sigmoid(g0)) * bf16_lo(hw[k]), h1 = (g1 * fast_sigmoid(g1)) * bf16_hi(hw[k]);
+          hw[k] = rnd2(h0, h1);
+        }
+        {  // MX(h): the lane's 16 codes (one 16-byte piece of the MX-tiled operand) and the block's scale byte
+          uint4 c;
+          const uint32_t e = quant16_codes(hw, c);
+          if (live) store_codes<MX_NT_FUSED>(swe.q + tiled_offset(m, jb + lg * 16, Nf), c);
+          if (lg == 0 && m < srows)
+            store_scale<MX_NT_FUSED>(swe.s + blocked_offset(m, jb >> 5, Nf / 128), live ? (uint8_t)e : (uint8_t)0);
+        }
+        // xS_down: D[ρ][m] += Σ_j A_d[ρ, j] h[m, j]; k step ks covers, in lane l, columns lg*16 + 8 ks + 0..7
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          xacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              af[b][ks], as_bf8(make_uint4(hw[4 * ks], hw[4 * ks + 1], hw[4 * ks + 2], hw[4 * ks + 3])), xacc, 0, 0, 0);
+      }
+      if (live) {  // lane l holds ρ = g*8 + (l/32)*4 + 0..3 in registers 4g..4g+3: one 16-byte store per g < R/8
+        float* pp = swe.part + ((int64_t)(n0 >> 7) * M + m) * R + lg * 4;
+#pragma unroll
+        for (int g4 = 0; g4 < R / 8; ++g4)
+          *reinterpret_cast<float4*>(pp + g4 * 8) =
+              make_float4(xacc[4 * g4], xacc[4 * g4 + 1], xacc[4 * g4 + 2], xacc[4 * g4 + 3]);
+      }
+    }
+    return;
+  }
+
   // the output segment of this tile (wave-uniform)
   int sg = 0;
 #pragma unroll
@@ -425,11 +547,11 @@ void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, 
             hipStream_t stm) {
   using S = Shape<kNW>;
   dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
-#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout
-  if (!lo.p) gemm_kernel<0, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
-  else if (r == 16) gemm_kernel<16, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
-  else if (r == 32) gemm_kernel<32, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
-  else gemm_kernel<64, kNW><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}
+  if (!lo.p) gemm_kernel<0, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 16) gemm_kernel<16, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 32) gemm_kernel<32, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else gemm_kernel<64, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
 #undef GEMM_ARGS
 }
 
@@ -535,4 +657,39 @@ extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, con
   }
   return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, ld_p, lora_q, ld_q, r, alpha, layout, nullptr, 0,
                    stream);
+}
+
+extern "C" int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* b, const void* sb, int64_t M, int64_t N,
+                                     int64_t K, const void* xs, const void* bg, const void* bu, const void* ad,
+                                     int64_t r, float s_g, float s_u, void* gu, void* q_h, void* s_h, float* part,
+                                     void* stream) {
+  MX_CHECK_ARG(a && sa && b && sb && xs && bg && bu && ad && gu && q_h && s_h && part,
+               "mxfp8_gemm_swiglu_fwd: null pointer");
+  MX_CHECK_ARG(M > 0 && N > 0 && K > 0 && N % 128 == 0 && K % 128 == 0 && (r == 16 || r == 32),
+               "mxfp8_gemm_swiglu_fwd: need N %% 128 == 0, K %% 128 == 0, r in {16, 32} (M=%lld N=%lld K=%lld r=%lld)",
+               (long long)M, (long long)N, (long long)K, (long long)r);
+  MX_CHECK_ARG(M < (1LL << 30) && M * 2 * N < (1LL << 31) && K < (1LL << 24),
+               "mxfp8_gemm_swiglu_fwd: M * 2N must stay below 2^31");
+  MX_CHECK_ARG(mx_aligned(a, 16) && mx_aligned(b, 16) && mx_aligned(sa, 16) && mx_aligned(sb, 16) &&
+                   mx_aligned(xs, 16) && mx_aligned(bg, 16) && mx_aligned(bu, 16) && mx_aligned(ad, 16) &&
+                   mx_aligned(gu, 16) && mx_aligned(q_h, 16) && mx_aligned(part, 16),
+               "mxfp8_gemm_swiglu_fwd: misaligned buffer");
+  Plan plan;
+  make_plan<1>(M, 2 * N, K, cached_cus(), plan);
+  SwEpi sw{(const uint16_t*)xs, (const uint16_t*)bg, (const uint16_t*)bu, (const uint16_t*)ad, s_g, s_u,
+           (uint16_t*)gu, (uint8_t*)q_h, (uint8_t*)s_h, part, (int)N};
+  CSeg cs{};
+  cs.n = 1;
+  const dim3 grid((unsigned)(8 * plan.per_full));
+  const int tiled = MXFP8_GEMM_A_TILED | MXFP8_GEMM_B_TILED;
+  hipStream_t stm = (hipStream_t)stream;
+  const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
+  if (r == 16)
+    gemm_kernel<16, 1, true><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
+                                                                   Lora{}, plan, tiled, sw);
+  else
+    gemm_kernel<32, 1, true><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
+                                                                   Lora{}, plan, tiled, sw);
+  MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_fwd");
+  return MXFP8_OK;
 }

@@ -17,6 +17,7 @@ Every kernel of the path is hand-written HIP (libmxfp8_mlp.so, _native.py): the 
 the quantizer (xs with MX(x), dxd with MX(dy)), the GEMM epilogues (y, dx) and the token-reduction kernel
 (dB_d, dA); no BLAS or elementwise torch kernel runs inside a step.
 """
+import os
 import types
 
 import torch
@@ -27,6 +28,8 @@ from fused_linear import STATS, _cast, _part
 
 _F8, _E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
 ENABLED = [True]  # set False to compare against the unfused path in the same process
+# the gate|up GEMM with the SwiGLU forward in its epilogue (False: GEMM, then the separate forward kernel)
+FUSED_EPILOGUE = [os.environ.get("MXFP8_FUSED_EPILOGUE", "1") != "0"]
 ACTIVE = [False]  # the fused path ran at least once (read by the step engine to shrink per-layer activations)
 SAVED_LESS = 12288  # bytes per token per layer not saved compared with the unfused path (h [T, 6144] bf16)
 
@@ -217,11 +220,21 @@ class _MLP(torch.autograd.Function):
             xs = torch.empty((T, 2 * R), dtype=dt, device=x2.device)
             _native.lora_nt(x2, S, xs)
             q, sc = mxfp8.mx_quant_tiled(x2)
-        # gu = gate | up [T, 2N] in the fused-tile layout the fused kernels read (32 x 32 blocks of 2 KB)
-        gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=_LAYOUT_FT, m=T)
-        del q, sc
+        if need_out and FUSED_EPILOGUE[0]:
+            # one launch: gu = gate | up [T, 2N] (fused-tile layout, the saved tensor) and, in the GEMM's epilogue,
+            # the LoRA-B of gate and up, h = silu(g)·u, MX(h) and the per-tile xS_down partials
+            gu, qh, sh, part = mxfp8.swiglu_gemm(q, sc, hold, xs, bg, bu, ad, s_g, s_u, T)
+            del q, sc
+            xsd = torch.empty((T, R), dtype=dt, device=x2.device)
+            _native.sum_parts(part, part.shape[0], T * R, xsd)
+            del part
+        else:
+            # gu = gate | up [T, 2N] in the fused-tile layout the fused kernels read (32 x 32 blocks of 2 KB)
+            gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=_LAYOUT_FT, m=T)
+            del q, sc
+            if need_out:
+                qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True, gu_ft=True)
         if need_out:
-            qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True, gu_ft=True)
             # y = bf16(bf16(MX(h)·W_downᵀ) + s_d · xS_down · B_dᵀ): the addmm_ of fused_mlp.py:284 in the epilogue
             y = mxfp8.mx_mm(qh, sh, down._mx_w_tl, down._mx_ws, lora=(xsd, bd), alpha=s_d, layout=3, m=T)
             del qh, sh, xsd
@@ -233,6 +246,7 @@ class _MLP(torch.autograd.Function):
         _cast(_forms_key(S, bg, bu, ad, bd, dt), lambda: lw)
         ctx.save_for_backward(x2, xs, gu, S, bg, bu, ad, bd)
         ctx.meta = (hold, down, (s_g, s_u, s_d), dt, lead, K, x.dtype)
+        ctx.pdt = (Ag.dtype, Au.dtype, Bd.dtype)  # the dtypes autograd casts dA_g, dA_u and dB_d to
         return y.view(*lead, y.shape[-1])
 
     @staticmethod
@@ -264,9 +278,13 @@ class _MLP(torch.autograd.Function):
         dA_d = torch.empty((R, N), dtype=torch.float32, device=dy2.device)
         _native.mlp_bwd_finish(*parts, T, N, R, s_g, s_u, dxa, xsd, dB_g, dB_u, dA_d)
         del parts
-        # the token reductions, bf16 as the reference's bf16 GEMMs return them (fused_mlp.py:316-318, :333)
+        # the token reductions: the bf16 values of the reference's bf16 GEMMs (fused_mlp.py:316-318, :333), held
+        # in the dtype of the parameter they are the gradient of: autograd casts a bf16 return to an fp32
+        # parameter's dtype anyway (bf16 -> fp32 is exact, so .grad is bit-identical), and the kernel writing the
+        # fp32 holder directly saves those cast kernels (about 23 us per step at the headline shape)
+        ag_dt, au_dt, bd_dt = ctx.pdt
         part = torch.empty(_native.lora_tn_chunks(T, K) * 2 * R * K, dtype=torch.float32, device=dy2.device)
-        dB_d = torch.empty((K, R), dtype=dt, device=dy2.device)
+        dB_d = torch.empty((K, R), dtype=torch.float32 if bd_dt == torch.float32 else dt, device=dy2.device)
         _native.lora_tn(dy2, xsd, dB_d, part[:part.numel() // 2], scale=s_d, transpose=True)  # bf16(bf16(dyᵀ xsd) s_d)
         dx = None
         if need_x:
@@ -275,7 +293,8 @@ class _MLP(torch.autograd.Function):
             dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
-        dA = torch.empty((2 * R, K), dtype=dt, device=dy2.device)
+        fp32_a = ag_dt == au_dt == torch.float32
+        dA = torch.empty((2 * R, K), dtype=torch.float32 if fp32_a else dt, device=dy2.device)
         _native.lora_tn(x2, dxa, dA, part)  # bf16(dxaᵀ · x2)
         grads = [dA[:R], dB_g, dA[R:], dB_u, dA_d, dB_d]
         ws_in = ctx.needs_input_grad[3:]

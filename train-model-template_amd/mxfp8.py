@@ -229,6 +229,29 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     return out
 
 
+def swiglu_gemm(q, s, hold, xs, bg, bu, ad, s_g, s_u, m):
+    """The gate|up MX GEMM of the fused MLP with the SwiGLU forward in its epilogue: q, s the MX-tiled codes and
+    scales of x [m, K]; hold the _GateUp copy (its fused-order operand).  -> (gu [ft_rows(m), 2N] bf16 in the
+    fused-tile layout, q_h [tiled_rows(m), N] MX-tiled codes of h, s_h its blocked scales, part [2N/128, m, r]
+    fp32 xS_down partials).  One launch for torch._scaled_mm + _fwd_kernel (fused_mlp.py:279-282, :65-109)."""
+    n, K = hold.n, hold.w.shape[1]
+    r = ad.shape[0]
+    dev = q.device
+    gu = torch.empty((ft_rows(m), 2 * n), dtype=torch.bfloat16, device=dev)
+    qh = torch.empty((tiled_rows(m), n), dtype=F8, device=dev)
+    sh = torch.empty(scale_numel(m, n), dtype=torch.uint8, device=dev)
+    part = torch.empty((2 * n // 128, m, r), dtype=torch.float32, device=dev)
+    ev = GEMM_EVENTS
+    if ev is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+    _native.gemm_swiglu_fwd(q, s, hold.wf_tl, hold.wfs, m, n, K, xs, bg, bu, ad, s_g, s_u, gu, qh, sh, part)
+    if ev is not None:
+        e1.record()
+        ev.append((e0, e1, 2 * m * 2 * n * K))
+    return gu, qh, sh.view(E8), part
+
+
 # ---------------------------------------------------------------- generic MX linear (mxfp8.py:296-341)
 class _ActivationMemo:
     """The codes of the activation an MX linear quantized last, keyed by (weak reference, version).  Linears that
@@ -340,17 +363,32 @@ def _col_tiles(scales, rows, cols, c0, c1):
     return tiles[:, c0 // 128:c1 // 128].contiguous().view(-1).view(E8)
 
 
+def fused_swiglu_rows(n, device=None):
+    """Row order of W_gu = [W_gate; W_up] [2n, K] for the gate|up GEMM with the fused SwiGLU epilogue
+    (mxfp8_gemm_swiglu_fwd): output tile t (128 columns) takes gate rows 64t..64t+63, then up rows n + 64t..,
+    and inside each 32-row block row a is logical row pi_col(a) = ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3), so
+    that every lane of the epilogue holds 16 contiguous gate and up columns of one token."""
+    c = torch.arange(2 * n, device=device)
+    t, within = c // 128, c % 128
+    half, blk, a = within // 64, (within % 64) // 32, within % 32
+    pi = ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3)
+    return half * n + 64 * t + 32 * blk + pi
+
+
 class _GateUp:
     """The one MX copy that gate_proj and up_proj of an MLP share (`_mx_gu = (hold, 0 | 1)`): W_gu = [W_gate;
     W_up] [2N, K] along K (w, ws) for the one forward GEMM and W_guᵀ [K, 2N] along 2N (wt, wts) for the one
     K = 2N dgrad GEMM, both from one read, with MX-tiled copies for the fused MLP (w_tl, wt_tl).  The scale tile
     rows of ws are ordered by row, so its first half is gate's (mxfp8.py:472-484).  half_t caches the per-half
-    dgrad operands that mx_wt cuts out."""
+    dgrad operands that mx_wt cuts out.  wf_tl / wfs: the forward operand again, in the row order of the GEMM
+    with the fused SwiGLU epilogue (fused_swiglu_rows; the same codes, rows permuted, scales re-blocked)."""
 
     def __init__(self, gate_w, up_w):
         self.n = gate_w.shape[0]
-        self.w, self.ws, self.wt, self.wts = quant_both(torch.cat([gate_w, up_w]).to(torch.bfloat16))
+        w = torch.cat([gate_w, up_w]).to(torch.bfloat16)
+        self.w, self.ws, self.wt, self.wts = quant_both(w)
         self.w_tl, self.wt_tl = tile_codes(self.w), tile_codes(self.wt)
+        self.wf_tl, self.wfs = mx_quant_tiled(w[fused_swiglu_rows(self.n, w.device)].contiguous())
         self.half_t = [None, None]
 
     def rows(self, i):
