@@ -492,23 +492,32 @@ def _counters_summary(name, dirs, cmds):
 
 def _trace_summary(name, d, steps, cmd):
     """rocprofv3 --kernel-trace of a bench run in `d` -> profiles/<name>.md: per kernel (the MX GEMM split into
-    its MLP shapes by _kernel_key) the launches, the median duration, and the share of a step = median x
-    round(launches / steps), where `steps` counts every step the profiled process ran (timed + warmup)."""
+    its MLP shapes by _kernel_key) the launches from the first MX GEMM on, the median duration, and the share of a
+    step = median x round(launches / steps), where `steps` counts every step the profiled process ran (timed +
+    warmup)."""
     files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
         raise SystemExit(f"no *kernel_trace.csv under {d}")
-    durs = {}
+    rows_all = []
     for f in files:
         with open(f) as fh:
-            for row in csv.DictReader(fh):
-                kname = row["Kernel_Name"]
-                if "at::native" in kname:
-                    m = re.search(r"at::native::(?:\(anonymous namespace\)::)?([A-Za-z_0-9]+)", kname)
-                    key = "torch " + (m.group(1) if m else kname[:30])
-                else:
-                    grid = int(row["Grid_Size_X"]) * int(row["Grid_Size_Y"]) * int(row["Grid_Size_Z"])
-                    key = _kernel_key(kname, str(grid))
-                durs.setdefault(key, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+            rows_all += list(csv.DictReader(fh))
+    # the steps' window: from the first MX GEMM launch (the gating forward) on; input generation, the model's
+    # host-to-device copies and the weight preparation before it are one-off work
+    gemm_starts = [int(r["Start_Timestamp"]) for r in rows_all if "gemm_kernel" in r["Kernel_Name"]]
+    t0 = min(gemm_starts) if gemm_starts else 0
+    durs = {}
+    for row in rows_all:
+        if int(row["Start_Timestamp"]) < t0:
+            continue
+        kname = row["Kernel_Name"]
+        if "at::native" in kname:
+            m = re.search(r"at::native::(?:\(anonymous namespace\)::)?([A-Za-z_0-9]+)", kname)
+            key = "torch " + (m.group(1) if m else kname[:30])
+        else:
+            grid = int(row["Grid_Size_X"]) * int(row["Grid_Size_Y"]) * int(row["Grid_Size_Z"])
+            key = _kernel_key(kname, str(grid))
+        durs.setdefault(key, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
     rows = []
     for key, v in durs.items():
         med = sorted(v)[len(v) // 2]
@@ -518,9 +527,11 @@ def _trace_summary(name, d, steps, cmd):
     with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
         f.write(f"# Kernel trace: {name}\n\nCommand (GPU box, repo root as `$GRAFT_REPO_ROOT`):\n\n```\ncd /tmp && "
                 f"export TMPDIR=/tmp\n{cmd}\npython3 bench.py --trace-summary {name} <trace dir> {steps:g}\n```\n\n")
-        f.write(f"The profiled process runs {steps:g} steps (timed + warmup), one forward for the gating check and the "
-                "one-off weight preparation. 'per step' = median duration x round(launches / steps); one-off kernels "
-                "show 0.\n\n| kernel | launches | median us | us per step | % |\n|---|---|---|---|---|\n")
+        f.write(f"The profiled process runs {steps:g} steps (timed + warmup) after one forward for the gating check; "
+                "dispatches before that forward's first MX GEMM (input generation, host-to-device copies, weight "
+                "preparation) are left out. 'per step' = median duration x round(launches / steps); kernels of the "
+                "gating forward alone show 0.\n\n| kernel | launches | median us | us per step | % |\n"
+                "|---|---|---|---|---|\n")
         for key, n, med, ps in rows:
             f.write(f"| {key} | {n} | {med:.1f} | {ps:.1f} | {100 * ps / tot if tot else 0:.1f} |\n")
         f.write(f"\nSum of kernel time per step: {tot:.1f} us.\n")
