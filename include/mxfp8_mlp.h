@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 6
+#define MXFP8_MLP_ABI_VERSION 7
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -278,6 +278,31 @@ int mxfp8_transpose_pad(const void* x, int64_t T, int64_t C, int64_t ld_x, void*
 int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* b, const void* sb, int64_t M, int64_t N, int64_t K,
                           const void* xs, const void* bg, const void* bu, const void* ad, int64_t r, float s_g,
                           float s_u, void* gu, void* q_h, void* s_h, float* part, void* stream);
+
+/*
+ * The dgrad GEMM of h with the SwiGLU backward fused into its epilogue: one launch replacing
+ * torch._scaled_mm(MX(dy), W_down) + _bwd_kernel (/root/reference/scripts/fused_mlp.py:307-314, :112-175):
+ *   dhm = bf16(MX(dy) · W_down) [M, N] stays in registers (it is never stored);
+ *   g, u, h recomputed from gu as in the forward; dh = bf16(dhm + dxd · A_dᵀ); du = bf16(dh · silu(g)),
+ *   dg = bf16(dh · u · σ(g) · (1 + g (1 - σ(g))));
+ *   MX(dg) | MX(du) -> q (MX-tiled, [ceil(M/16)*16, 2N], dg at columns 0..N-1, du at N..2N-1) and s (blocked,
+ *   ceil(M/128) tile rows; padded rows 0);
+ *   dxa_part [N/128, M, 3r]: each 128-column tile's dg · B_g | du · B_u | h · A_dᵀ (add them in order; the same
+ *   bits as mxfp8_mlp_bwd with CG = 128);
+ *   dbg_part, dbu_part [ceil(M/256), N, r] and dad_part [ceil(M/256), r, N]: each 256-row tile row's dgᵀ · xs_g,
+ *   duᵀ · xs_u and dxdᵀ · h (add them in order).
+ * a / sa: MX-tiled codes and blocked scales of dy [M, K]; b / sb: W_downᵀ [N, K] with each 32-row block in the
+ * dgrad row order (row a holds logical row pi_col(a), as in mxfp8_gemm_swiglu_fwd), MX-tiled, with its blocked
+ * scales.  gu [ceil(M/32)*32, 2N] in the fused-tile layout (mxfp8_gemm_swiglu_fwd's output); xs [M, 2r] and its
+ * transpose xsT [2r, Tpad]; dxd [M, r] = bf16(bf16(dy · B_d) · s_d) and dxdT [r, Tpad] (Tpad = ceil(M/128)*128,
+ * zero past M: mxfp8_quant_lora's outputs); bg, bu [N, r], adT [N, r] and their transposes bgT, buT, ad [r, N],
+ * bf16.  N % 128 == 0, K % 128 == 0, r == 16, M * 2N < 2^31.
+ */
+int mxfp8_gemm_swiglu_bwd(const void* a, const void* sa, const void* b, const void* sb, int64_t M, int64_t N, int64_t K,
+                          const void* gu, const void* xs, const void* xsT, const void* dxd, const void* dxdT,
+                          const void* bg, const void* bgT, const void* bu, const void* buT, const void* ad,
+                          const void* adT, int64_t r, float s_g, float s_u, void* q, void* s, float* dxa_part,
+                          float* dbg_part, float* dbu_part, float* dad_part, void* stream);
 
 /* Token chunks mxfp8_lora_tn uses for [T, K] (its partial buffer holds chunks * rp * K floats). */
 int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);

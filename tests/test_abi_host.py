@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 29, names
+    assert len(names) == 30, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -74,6 +74,18 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 0,
                              ctypes.c_void_p(16), 1 << 20, None) == -1
     assert b"workspace" in lib.mxfp8_last_error()
+    # GEMMs with the SwiGLU epilogues: the backward takes r = 16 only; null pointers are refused
+    fp = ctypes.cast(p, ctypes.POINTER(ctypes.c_float))
+    bwd = [p] * 4 + [256, 512, 256] + [p] * 11 + [32, 1.0, 1.0, p, p] + [fp] * 4 + [None]
+    assert lib.mxfp8_gemm_swiglu_bwd(*bwd) == -1
+    assert b"r == 16" in lib.mxfp8_last_error()
+    bwd[18] = 16
+    bwd[8] = None
+    assert lib.mxfp8_gemm_swiglu_bwd(*bwd) == -1
+    assert b"null" in lib.mxfp8_last_error()
+    fwd = [p] * 4 + [256, 512, 256] + [p] * 4 + [64, 1.0, 1.0, p, p, p, fp, None]
+    assert lib.mxfp8_gemm_swiglu_fwd(*fwd) == -1
+    assert b"r in {16, 32}" in lib.mxfp8_last_error()
     # backward column group must divide N and be a multiple of 128
     args = [p] * 12 + [256, 512, 16, 1.0, 1.0, 128, 384] + [p] * 2 + [ctypes.cast(p, ctypes.POINTER(ctypes.c_float))] * 4 + [None, 0, None]
     assert lib.mxfp8_mlp_bwd(*args) == -1

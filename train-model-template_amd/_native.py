@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT = 1, 2, 4, 8  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -30,6 +30,7 @@ SIGNATURES = {
     "mxfp8_gemm_workspace_size": [_i64, _i64, _i64],
     "mxfp8_gemm_swiglu_fwd": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _f32, _f32, _ptr,
                               _ptr, _ptr, _ptr],
+    "mxfp8_gemm_swiglu_bwd": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64] + [_ptr] * 11 + [_i64, _f32, _f32] + [_ptr] * 7,
     "mxfp8_gemm_nt_seg": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64,
                           _ptr, _i64, _i64, _f32, _i64, _ptr],
     "mxfp8_mlp_fwd_groups": [_i64, _i64, _i64],
@@ -201,6 +202,14 @@ def gemm_swiglu_fwd(a, sa, b, sb, M, N, K, xs, bg, bu, ad, s_g, s_u, gu, q_h, s_
     """gate|up MX GEMM with the SwiGLU forward in its epilogue (include/mxfp8_mlp.h, mxfp8_gemm_swiglu_fwd)."""
     call("mxfp8_gemm_swiglu_fwd", _p(a), _p(sa), _p(b), _p(sb), M, N, K, _p(xs), _p(bg), _p(bu), _p(ad), ad.shape[0],
          float(s_g), float(s_u), _p(gu), _p(q_h), _p(s_h), _p(part), like=gu)
+
+
+def gemm_swiglu_bwd(a, sa, b, sb, M, N, K, gu, xs, xsT, dxd, dxdT, bg, bgT, bu, buT, ad, adT, s_g, s_u, q, s, dxa_part,
+                    dbg_part, dbu_part, dad_part):
+    """dgrad MX GEMM of h with the SwiGLU backward in its epilogue (include/mxfp8_mlp.h, mxfp8_gemm_swiglu_bwd)."""
+    call("mxfp8_gemm_swiglu_bwd", _p(a), _p(sa), _p(b), _p(sb), M, N, K, _p(gu), _p(xs), _p(xsT), _p(dxd), _p(dxdT),
+         _p(bg), _p(bgT), _p(bu), _p(buT), _p(ad), _p(adT), ad.shape[0], float(s_g), float(s_u), _p(q), _p(s),
+         _p(dxa_part), _p(dbg_part), _p(dbu_part), _p(dad_part), like=gu)
 
 
 def mlp_fwd(gu, xs, bg, bu, ad, T, N, r, s_g, s_u, q, s, part, n_groups, h_out=None, q_layout=0):

@@ -86,7 +86,7 @@ struct Lora {
   float alpha;
 };
 
-// Fused SwiGLU forward epilogue (kSw): the operands beyond the GEMM's.  The B operand is W_gu = [W_gate; W_up] in
+// Fused SwiGLU forward epilogue (kEpi == kEpiSwiGluFwd): the operands beyond the GEMM's.  The B operand is W_gu = [W_gate; W_up] in
 // the fused row order (fused_swiglu_row in the host code): output tile t (128 columns) holds gate columns
 // 64 t + 0..63 and then up columns 64 t + 0..63, each 32-column block with its weight rows permuted by pi_col,
 // so that acc[b][mt] (gate) and acc[2 + b][mt] (up) hold, in lane l, row m = l % 32 and the 16 CONTIGUOUS
@@ -103,6 +103,45 @@ struct SwEpi {
   float* part;         // [2N/128, M, r] xS_down partials, one per output tile
   int N;               // d_ffn
 };
+
+// Fused SwiGLU backward epilogue (kEpi == kEpiSwiGluBwd).  The GEMM is dhm = MX(dy) · W_down with B = W_downᵀ
+// [N, K] in the dgrad row order (fused_dgrad_row in the host code: inside each 32-row block row a is logical row
+// pi_col(a)), so that acc[nt][mt] holds, in lane l, row m = l % 32 and the 16 contiguous columns
+// n0 + 32 nt + (l / 32) * 16 + i, the lane layout of the fused backward kernel.  The epilogue is that kernel's
+// per-tile work (mlp_fused.hip, bwd_kernel) with dhm taken from the accumulators instead of memory.
+struct SwBwd {
+  const uint16_t* gu;    // [ceil(M/32)*32, 2N] bf16 saved gate | up GEMM output, fused-tile layout
+  const uint16_t* xs;    // [M, 2r] bf16: x · [A_g; A_u]ᵀ
+  const uint16_t* xsT;   // [2r, Tpad] its transpose, zero past M (Tpad = ceil(M/128)*128)
+  const uint16_t* dxd;   // [M, r] bf16(bf16(dy · B_d) s_d)
+  const uint16_t* dxdT;  // [r, Tpad] its transpose, zero past M
+  const uint16_t* bg;    // [N, r] LoRA B of gate, and its transpose bgT [r, N]
+  const uint16_t* bgT;
+  const uint16_t* bu;    // [N, r] LoRA B of up, and buT [r, N]
+  const uint16_t* buT;
+  const uint16_t* ad;    // [r, N] LoRA A of down, and adT [N, r]
+  const uint16_t* adT;
+  float s_g, s_u;
+  uint8_t* q;            // [ceil(M/16)*16, 2N] MX-tiled codes of dg | du (the dgrad GEMM's A operand)
+  uint8_t* s;            // their blocked scales (ceil(M/128) tile rows, 2N/128 tiles)
+  float* dxa;            // [N/128, M, 3r] partials dxa_g | dxa_u | xS_down, one per output tile
+  float* dbg;            // [ceil(M/256), N, r] dB_g partials, one per tile row
+  float* dbu;            // [ceil(M/256), N, r] dB_u partials
+  float* dad;            // [ceil(M/256), r, N] dA_d partials
+};
+
+constexpr int kEpiPlain = 0, kEpiSwiGluFwd = 1, kEpiSwiGluBwd = 2;
+// LDS of the backward epilogue (r = 16), in the operand ring:
+//   per wave three [32][kTrLd] bf16 transpose tiles (dg, du, h), which afterwards carry the wave's dB_g, dB_u,
+//   dA_dᵀ sums of the block (3 x [32 x 16] fp32) to the cross-wave reduction;
+//   the tile's dB_g, dB_u, dA_d sums over its first row blocks, [4 column blocks][3][512] fp32;
+//   the tile's LoRA weights, bf16: rows n0..n0+127 of B_g, B_u, A_dᵀ ([128][16] each) and the same columns of
+//   B_gᵀ, B_uᵀ, A_d ([16][128] each).
+constexpr int kBwdTrBytes = 3 * 32 * kTrLd * 2;
+constexpr int kBwdDbOff = 4 * kBwdTrBytes, kBwdDbBytes = 4 * 3 * 512 * 4;
+constexpr int kBwdWOff = kBwdDbOff + kBwdDbBytes, kBwdWBytes = 6 * 128 * 16 * 2;
+static_assert(kBwdWOff + kBwdWBytes <= Shape<1>::kStages * Shape<1>::kStageBytes, "backward epilogue LDS");
+static_assert(3 * 32 * 16 * 4 <= kBwdTrBytes, "dB exchange fits a wave's transpose tiles");
 
 // Output columns in up to four segments, each its own row-major matrix: columns [col0[k], col0[k + 1]) of the
 // product go to ptr[k] with row stride ld[k] (segment boundaries are multiples of the tile width, so a tile
@@ -144,11 +183,11 @@ __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw
   return r;
 }
 
-template <int kR, int kNW, bool kSw>
+template <int kR, int kNW, int kEpi>
 __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, int64_t lda, const uint8_t* __restrict__ B,
     const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, CSeg cseg, Lora lora, Plan plan, int tiled,
-    SwEpi swe) {
+    SwEpi swe, SwBwd swb) {
   using S = Shape<kNW>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[S::kStages * S::kStageBytes];
   __shared__ int arrived;
@@ -343,7 +382,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
     if (tid == 0) __hip_atomic_store(plan.cnt + st_, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  if constexpr (kSw) {
+  if constexpr (kEpi == kEpiSwiGluFwd) {
     // SwiGLU forward (fused_mlp.py:65-109, the _fwd_kernel math): gu = bf16(acc) is stored as the saved GEMM
     // output, then g = bf16(gu_g + s_g xs_g·B_gᵀ), u = bf16(gu_u + s_u xs_u·B_uᵀ), h = bf16(silu(g) u), MX(h)
     // into the down GEMM's operand and the tile's xS_down partial h·A_dᵀ, per 32 x 32 block of the wave.
@@ -442,6 +481,243 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
           *reinterpret_cast<float4*>(pp + g4 * 8) =
               make_float4(xacc[4 * g4], xacc[4 * g4 + 1], xacc[4 * g4 + 2], xacc[4 * g4 + 3]);
       }
+    }
+    return;
+  }
+
+  if constexpr (kEpi == kEpiSwiGluBwd) {
+    // SwiGLU backward (fused_mlp.py:112-175, the _bwd_kernel math) on dhm = bf16(acc), the reference's _scaled_mm
+    // output.  The wave walks its 8 blocks of 32 x 32 (row block mt outer, column block nt inner); per block it
+    // recomputes g, u, h from the saved gu, forms dh = bf16(dhm + dxd·A_dᵀ), du and dg, writes MX(dg) and MX(du)
+    // into the dgrad GEMM's operand, and computes, as bwd_kernel does for one column tile of its quad:
+    //   the dxa_g | dxa_u | xS_down products D[ρ][m] over the block's columns, added in registers over the tile's
+    //   column blocks in order nt = 0..3 (bwd_kernel's fixed-order sum over the quad's waves: the partials are
+    //   the same bits) and stored as the tile's partial after the row block's last column block;
+    //   the dB_g, dB_u, dA_dᵀ contributions D[j][ρ] over the block's 32 rows (LDS transposes, 16x16x32 products),
+    //   summed over the 4 waves in wave order and over the two row blocks in order, in LDS, and stored as the
+    //   tile row's partial.
+    // gu of the next block is loaded before the current block's stores, so waiting for it never waits for them
+    // (the memory counter completes in order); the small per-row operands are loaded once per row block and the
+    // weights are staged in LDS once per tile.
+    constexpr int R = kR;
+    static_assert(R == 16, "the backward epilogue's LDS is laid out for r = 16");
+    const int lg = lane >> 5, rho = lane & 31;
+    const int Tpad = (M + 127) / 128 * 128;  // rows of the transposed operands and of the scale buffer
+    // dhm as packed bf16 pairs (columns lg*16 + 2k, +1 of each block): the fp32 accumulators are dead from here
+    uint32_t dm[4][2][8];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          dm[nt][mt][k] = pack_bf16x2(acc[nt][mt][2 * k], acc[nt][mt][2 * k + 1]);
+          // pin the packed value here: left alone, the compiler sinks each conversion to its block and keeps
+          // all 128 fp32 accumulators live through the first blocks (and spills)
+          asm volatile("" : "+v"(dm[nt][mt][k]));
+        }
+    // the ring is free once every wave's DMAs have landed (vmcnt(0) above) and its fragment reads are done
+    lds_barrier();
+    const uint32_t lw0 = lds0 + kBwdWOff;
+    {  // the tile's weights into LDS: 6 arrays of 4 KB, 24 DMAs of 1 KB, 6 per wave (lane i lands at 16 i)
+#pragma unroll
+      for (int j = 0; j < 6; ++j) {
+        const int i = wave * 6 + j, arr = i >> 2, k = i & 3;  // wave-uniform
+        const uint16_t* src;
+        if (arr < 3) {  // B_g, B_u, A_dᵀ rows n0 + (k*1024 + 16 lane) / 32: contiguous 4 KB
+          const uint16_t* base = arr == 0 ? swb.bg : arr == 1 ? swb.bu : swb.adT;
+          src = base + (int64_t)n0 * R + k * 512 + lane * 8;
+        } else {  // B_gᵀ, B_uᵀ, A_d row ρ = 4 k + lane / 16, columns n0 + 8 (lane % 16) ..
+          const uint16_t* base = arr == 3 ? swb.bgT : arr == 4 ? swb.buT : swb.ad;
+          src = base + (int64_t)(4 * k + (lane >> 4)) * N + n0 + (lane & 15) * 8;
+        }
+        dma16(src, lw0 + arr * 4096 + k * 1024);
+      }
+    }
+    const uint16_t* const wl = reinterpret_cast<const uint16_t*>(lds + kBwdWOff);
+    uint16_t* const trw = reinterpret_cast<uint16_t*>(lds + wave * kBwdTrBytes);
+    float* const dbx = reinterpret_cast<float*>(trw);  // the wave's dB exchange (after its transposes are read)
+    float* const dbl = reinterpret_cast<float*>(lds + kBwdDbOff);
+    auto fetch = [&](int b, uint32_t* w) {  // g | u of block b (nt = b % 4, mt = b / 4)
+      const int mc = min(m0 + wm * 64 + (b >> 2) * 32 + (lane & 31), M - 1);
+      const int c = n0 + (b & 3) * 32 + lg * 16;
+      load16_rc(swb.gu, mc, c, 2 * N, true, w);
+      load16_rc(swb.gu, mc, N + c, 2 * N, true, w + 8);
+    };
+    uint32_t gbuf[2][16];
+    fetch(0, gbuf[0]);
+    wait_vmcnt<4>();  // the weight DMAs, issued before the 4 loads of block 0's gu, have landed
+    lds_barrier();
+    v8bf xg, xu, xd, tg, tu, td;  // the row block's xs, dxd rows and their transposed forms
+    float4 xa[3][2];              // dxa | dxa_u | xS_down of the row block, running over its column blocks
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int nt = b & 3, mt = b >> 2;
+      const int jb = n0 + nt * 32;
+      const int rb = m0 + wm * 64 + mt * 32;
+      const int m = rb + (lane & 31);
+      const bool live = m < M;
+      const int mc = live ? m : M - 1;
+      __builtin_amdgcn_sched_barrier(0);  // blocks stay in order: only the explicit prefetch runs ahead
+      if (b + 1 < 8) fetch(b + 1, gbuf[(b + 1) & 1]);
+      if (nt == 0) {
+        xg = load_bf8(swb.xs + (int64_t)mc * 2 * R + lg * 8);
+        xu = load_bf8(swb.xs + (int64_t)mc * 2 * R + R + lg * 8);
+        xd = load_bf8(swb.dxd + (int64_t)mc * R + lg * 8);
+        const int rr = lane & 15, mo = min(rb, Tpad - 32) + (lane >> 4) * 8;  // rows past Tpad: any (they add 0)
+        tg = load_bf8(swb.xsT + (int64_t)rr * Tpad + mo);
+        tu = load_bf8(swb.xsT + (int64_t)(R + rr) * Tpad + mo);
+        td = load_bf8(swb.dxdT + (int64_t)rr * Tpad + mo);
+      }
+      // Every block runs branch-free, also a block of rows past Tpad (in the last tile row only): its loads are
+      // clamped to real rows, it stores nothing, and its zeroed values add nothing to the sums.  (Under a
+      // branch the compiler's counter waits, merged over both paths, would also wait for the prefetch.)
+      v4f dbg[2], dbu[2], dad[2];
+      {
+        uint32_t* gw = gbuf[b & 1];
+        uint32_t* uw = gbuf[b & 1] + 8;
+        // weights of these 32 columns from LDS: LoRA-B rows jb + pi_col(lane % 32) (B_g, B_u, A_dᵀ)
+        const int wrow = (nt * 32 + pi_col(lane & 31)) * R + lg * 8;
+        {
+          const v16f d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const v8bf*>(wl + wrow), xg,
+                                                                 v16f{}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            float a = bf16_lo(gw[i / 2]) + swb.s_g * d[i], c = bf16_hi(gw[i / 2]) + swb.s_g * d[i + 1];
+            gw[i / 2] = rnd2(a, c);
+          }
+        }
+        {
+          const v16f d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const v8bf*>(wl + 2048 + wrow),
+                                                                 xu, v16f{}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            float a = bf16_lo(uw[i / 2]) + swb.s_u * d[i], c = bf16_hi(uw[i / 2]) + swb.s_u * d[i + 1];
+            uw[i / 2] = rnd2(a, c);
+          }
+        }
+        uint32_t dp[8];
+        {
+          const v16f d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const v8bf*>(wl + 4096 + wrow),
+                                                                 xd, v16f{}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 16; i += 2) {
+            float a = bf16_lo(dm[nt][mt][i / 2]) + d[i], c = bf16_hi(dm[nt][mt][i / 2]) + d[i + 1];
+            dp[i / 2] = rnd2(a, c);  // dh
+          }
+        }
+        uint32_t dgw[8], duw[8], hw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float g0 = bf16_lo(gw[i]), g1 = bf16_hi(gw[i]);
+          const float u0 = bf16_lo(uw[i]), u1 = bf16_hi(uw[i]);
+          const float d0 = bf16_lo(dp[i]), d1 = bf16_hi(dp[i]);
+          const float sg0 = fast_sigmoid(g0), sg1 = fast_sigmoid(g1);
+          const float sl0 = g0 * sg0, sl1 = g1 * sg1;
+          float h0 = sl0 * u0, h1 = sl1 * u1;
+          hw[i] = rnd2(h0, h1);
+          float du0 = d0 * sl0, du1 = d1 * sl1;
+          duw[i] = rnd2(du0, du1);
+          float dg0 = ((d0 * u0) * sg0) * (g0 * (1.0f - sg0) + 1.0f);
+          float dg1 = ((d1 * u1) * sg1) * (g1 * (1.0f - sg1) + 1.0f);
+          dgw[i] = rnd2(dg0, dg1);
+        }
+        {  // MX(dg) at columns jb.., MX(du) at N + jb.. of the [*, 2N] operand: codes of live rows, scale bytes
+           // of every row below Tpad (0 for padded rows)
+          uint4 c;
+          const uint32_t eg = quant16_codes(dgw, c);
+          if (live) store_codes<MX_NT_FUSED>(swb.q + tiled_offset(m, jb + lg * 16, 2 * N), c);
+          const uint32_t eu = quant16_codes(duw, c);
+          if (live) store_codes<MX_NT_FUSED>(swb.q + tiled_offset(m, N + jb + lg * 16, 2 * N), c);
+          if (lg == 0 && rb < Tpad) {
+            store_scale<MX_NT_FUSED>(swb.s + blocked_offset(m, jb >> 5, 2 * N / 128), live ? (uint8_t)eg : (uint8_t)0);
+            store_scale<MX_NT_FUSED>(swb.s + blocked_offset(m, (N + jb) >> 5, 2 * N / 128),
+                                     live ? (uint8_t)eu : (uint8_t)0);
+          }
+        }
+        if (!live) {  // padded rows add nothing to the sums below
+#pragma unroll
+          for (int i = 0; i < 8; ++i) dgw[i] = duw[i] = hw[i] = 0u;
+        }
+        // dxa_g | dxa_u | xS_down over this block's columns, D[ρ][m] (lane l: m = l % 32, ρ = (i / 4) * 8 +
+        // (l / 32) * 4 + i % 4: registers 0..7 hold ρ < 16), with rows ρ of B_gᵀ, B_uᵀ, A_d (zero past r) at the
+        // lane's columns as the first operand
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+          const uint32_t* w = p == 0 ? dgw : p == 1 ? duw : hw;
+          v16f d = v16f{};
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const v8bf f = *reinterpret_cast<const v8bf*>(wl + (3 + p) * 2048 + (rho & 15) * 128 + nt * 32 + lg * 16 +
+                                                          8 * ks);
+            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                rho < R ? f : v8bf{}, as_bf8(make_uint4(w[4 * ks], w[4 * ks + 1], w[4 * ks + 2], w[4 * ks + 3])), d,
+                0, 0, 0);
+          }
+          const float4 lo = make_float4(d[0], d[1], d[2], d[3]), hi = make_float4(d[4], d[5], d[6], d[7]);
+          if (nt == 0) {
+            xa[p][0] = lo;
+            xa[p][1] = hi;
+          } else {
+            xa[p][0] = make_float4(xa[p][0].x + lo.x, xa[p][0].y + lo.y, xa[p][0].z + lo.z, xa[p][0].w + lo.w);
+            xa[p][1] = make_float4(xa[p][1].x + hi.x, xa[p][1].y + hi.y, xa[p][1].z + hi.z, xa[p][1].w + hi.w);
+          }
+          if (nt == 3 && live) {  // the tile's partial: row m, columns p*R + g4*8 + (l/32)*4 + 0..3
+            float* pp = swb.dxa + ((int64_t)(n0 >> 7) * M + m) * 3 * R + p * R + lg * 4;
+            *reinterpret_cast<float4*>(pp) = xa[p][0];
+            *reinterpret_cast<float4*>(pp + 8) = xa[p][1];
+          }
+        }
+        // dB_g, dB_u, dA_dᵀ: D[j][ρ] = Σ_m dg[m, j] xs_g[m, ρ] etc. over the block's 32 rows
+        tr_store(trw, lane, dgw);
+        tr_store(trw + 32 * kTrLd, lane, duw);
+        tr_store(trw + 64 * kTrLd, lane, hw);
+#pragma unroll
+        for (int jh = 0; jh < 2; ++jh) {
+          dbg[jh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tr_operand(trw, jh * 16, lane), tg, v4f{}, 0, 0, 0);
+          dbu[jh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tr_operand(trw + 32 * kTrLd, jh * 16, lane), tu, v4f{},
+                                                            0, 0, 0);
+          dad[jh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tr_operand(trw + 64 * kTrLd, jh * 16, lane), td, v4f{},
+                                                            0, 0, 0);
+        }
+      }
+      // the 4 waves' dB sums of this block, added in wave order: each wave puts its [3][32 x 16] floats in its
+      // own transpose tiles (dB_g, dB_u as [j][ρ], dA_d as [ρ][j]), then
+      // every thread adds one or two float4 of the four: into the tile's sums (first row block) or onto them and
+      // into the tile row's partial (second row block)
+#pragma unroll
+      for (int jh = 0; jh < 2; ++jh) {
+        const int j0 = jh * 16 + (lane >> 4) * 4, r0 = lane & 15;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dbx[(j0 + i) * 16 + r0] = dbg[jh][i];
+          dbx[512 + (j0 + i) * 16 + r0] = dbu[jh][i];
+        }
+        *reinterpret_cast<float4*>(dbx + 1024 + r0 * 32 + j0) = make_float4(dad[jh][0], dad[jh][1], dad[jh][2], dad[jh][3]);
+      }
+      lds_barrier();
+      for (int f = tid; f < 384; f += 256) {  // 3 x 128 float4 per wave
+        const int e = (f & 127) * 4, p = f >> 7;
+        const float* base = reinterpret_cast<const float*>(lds) + p * 512 + e;
+        float4 v = *reinterpret_cast<const float4*>(base);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+          const float4 t = *reinterpret_cast<const float4*>(base + w * (kBwdTrBytes / 4));
+          v = make_float4(v.x + t.x, v.y + t.y, v.z + t.z, v.w + t.w);
+        }
+        float4* acc_db = reinterpret_cast<float4*>(dbl + (nt * 3 + p) * 512 + e);
+        if (mt == 0) {
+          *acc_db = v;
+        } else {
+          const float4 a = *acc_db;
+          v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+          float* dst = p == 0   ? swb.dbg + ((int64_t)mt_ * N + jb + e / 16) * R + e % 16
+                       : p == 1 ? swb.dbu + ((int64_t)mt_ * N + jb + e / 16) * R + e % 16
+                                : swb.dad + ((int64_t)mt_ * R + e / 32) * N + jb + e % 32;
+          *reinterpret_cast<float4*>(dst) = v;
+        }
+      }
+      lds_barrier();
     }
     return;
   }
@@ -547,11 +823,11 @@ void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, 
             hipStream_t stm) {
   using S = Shape<kNW>;
   dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
-#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}
-  if (!lo.p) gemm_kernel<0, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
-  else if (r == 16) gemm_kernel<16, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
-  else if (r == 32) gemm_kernel<32, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
-  else gemm_kernel<64, kNW, false><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}, SwBwd{}
+  if (!lo.p) gemm_kernel<0, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 16) gemm_kernel<16, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 32) gemm_kernel<32, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else gemm_kernel<64, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
 #undef GEMM_ARGS
 }
 
@@ -685,11 +961,49 @@ extern "C" int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* 
   hipStream_t stm = (hipStream_t)stream;
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   if (r == 16)
-    gemm_kernel<16, 1, true><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
-                                                                   Lora{}, plan, tiled, sw);
+    gemm_kernel<16, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
+                                                                   Lora{}, plan, tiled, sw, SwBwd{});
   else
-    gemm_kernel<32, 1, true><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
-                                                                   Lora{}, plan, tiled, sw);
+    gemm_kernel<32, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
+                                                                   Lora{}, plan, tiled, sw, SwBwd{});
   MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_fwd");
+  return MXFP8_OK;
+}
+
+extern "C" int mxfp8_gemm_swiglu_bwd(const void* a, const void* sa, const void* b, const void* sb, int64_t M, int64_t N,
+                                     int64_t K, const void* gu, const void* xs, const void* xsT, const void* dxd,
+                                     const void* dxdT, const void* bg, const void* bgT, const void* bu, const void* buT,
+                                     const void* ad, const void* adT, int64_t r, float s_g, float s_u, void* q,
+                                     void* s, float* dxa_part, float* dbg_part, float* dbu_part, float* dad_part,
+                                     void* stream) {
+  MX_CHECK_ARG(a && sa && b && sb && gu && xs && xsT && dxd && dxdT && bg && bgT && bu && buT && ad && adT && q && s &&
+                   dxa_part && dbg_part && dbu_part && dad_part,
+               "mxfp8_gemm_swiglu_bwd: null pointer");
+  MX_CHECK_ARG(M > 0 && N > 0 && K > 0 && N % 128 == 0 && K % 128 == 0 && r == 16,
+               "mxfp8_gemm_swiglu_bwd: need N %% 128 == 0, K %% 128 == 0, r == 16 (M=%lld N=%lld K=%lld r=%lld)",
+               (long long)M, (long long)N, (long long)K, (long long)r);
+  MX_CHECK_ARG(M < (1LL << 30) && M * 2 * N < (1LL << 31) && K < (1LL << 24),
+               "mxfp8_gemm_swiglu_bwd: M * 2N must stay below 2^31");
+  MX_CHECK_ARG(mx_aligned(a, 16) && mx_aligned(b, 16) && mx_aligned(sa, 16) && mx_aligned(sb, 16) &&
+                   mx_aligned(gu, 16) && mx_aligned(xs, 16) && mx_aligned(xsT, 16) && mx_aligned(dxd, 16) &&
+                   mx_aligned(dxdT, 16) && mx_aligned(bg, 16) && mx_aligned(bgT, 16) && mx_aligned(bu, 16) &&
+                   mx_aligned(buT, 16) && mx_aligned(ad, 16) && mx_aligned(adT, 16) && mx_aligned(q, 16) &&
+                   mx_aligned(dxa_part, 16) && mx_aligned(dbg_part, 16) && mx_aligned(dbu_part, 16) &&
+                   mx_aligned(dad_part, 16),
+               "mxfp8_gemm_swiglu_bwd: misaligned buffer");
+  Plan plan;
+  make_plan<1>(M, N, K, cached_cus(), plan);
+  SwBwd sw{(const uint16_t*)gu,  (const uint16_t*)xs,  (const uint16_t*)xsT, (const uint16_t*)dxd,
+           (const uint16_t*)dxdT, (const uint16_t*)bg, (const uint16_t*)bgT, (const uint16_t*)bu,
+           (const uint16_t*)buT, (const uint16_t*)ad,  (const uint16_t*)adT, s_g, s_u, (uint8_t*)q, (uint8_t*)s,
+           dxa_part, dbg_part, dbu_part, dad_part};
+  CSeg cs{};
+  cs.n = 1;
+  const dim3 grid((unsigned)(8 * plan.per_full));
+  const int tiled = MXFP8_GEMM_A_TILED | MXFP8_GEMM_B_TILED;
+  gemm_kernel<16, 1, kEpiSwiGluBwd><<<grid, Shape<1>::kThreads, 0, (hipStream_t)stream>>>(
+      (const uint8_t*)a, (const uint8_t*)sa, K, (const uint8_t*)b, (const uint8_t*)sb, K, (int)M, (int)N, (int)K, cs,
+      Lora{}, plan, tiled, SwEpi{}, sw);
+  MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_bwd");
   return MXFP8_OK;
 }

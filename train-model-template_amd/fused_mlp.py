@@ -5,13 +5,20 @@ mlp_fwd, mlp_bwd), same saved-tensor set, same return dtypes and the same None f
 
   Every MX GEMM operand of the path is in the MX-tiled layout (mxfp8.mx_quant_tiled, tile_codes): the same codes
   and scales as mx_quant in 1 KB blocks the GEMM streams without strided row pieces.
-  forward : xs = x·[A_g; A_u]ᵀ (bf16) -> MX(x) -> MX GEMM gate|up (W_gu [2N, K]) -> fused kernel reading gu
-            once: LoRA-B of gate and up, bf16 rounding, h = silu(g)·u, MX(h) and the xS_down partials ->
-            MX GEMM down with the LoRA epilogue y = bf16(y + s_d · xS_down · B_dᵀ) inside the GEMM.
+  forward : xs = x·[A_g; A_u]ᵀ (bf16) with MX(x) from one read -> MX GEMM gate|up (W_gu [2N, K]) whose
+            epilogue stores gu and applies the LoRA-B of gate and up, bf16 rounding, h = silu(g)·u, MX(h) and
+            the xS_down partials -> MX GEMM down with the LoRA epilogue y = bf16(y + s_d · xS_down · B_dᵀ).
             h is not stored (backward recomputes it from gu).
-  backward: MX(dy) -> MX GEMM dh = dy·W_down -> fused kernel reading gu and dh once: recompute g, u, h;
-            dh += dxd·A_d; SwiGLU backward; MX(dg | du) into one [T, 2N] buffer; dxa, dB, dA_d partials ->
-            one K = 2N MX GEMM dx = [dg | du]·W_gu with the LoRA epilogue dx = bf16(dx + dxa·S).
+  backward: MX(dy) with dxd = dy·B_d from one read -> MX GEMM dhm = dy·W_down (fused-tile layout) -> fused
+            kernel reading gu and dhm once: recompute g, u, h; dh = dhm + dxd·A_d; SwiGLU backward; MX(dg | du)
+            into one [T, 2N] buffer; dxa, dB, dA_d partials -> one K = 2N MX GEMM dx = [dg | du]·W_gu with the
+            LoRA epilogue dx = bf16(dx + dxa·S).
+  FUSED_EPILOGUE[0] = False (MXFP8_FUSED_EPILOGUE=0) runs the gate|up GEMM alone and the SwiGLU forward in the
+  separate fused kernel (mlp_fwd), the reference's own split.  FUSED_BWD_EPILOGUE[0] = True
+  (MXFP8_FUSED_BWD_EPILOGUE=1) moves the backward kernel's work into the dhm GEMM's epilogue (dhm never leaves
+  the registers); it measured slower than the split at the headline shape (the epilogue's loads, stores and
+  waits do not hide behind the co-resident workgroup's main loop), so it is off by default.  Every mode gives
+  the same bits except the xS_down and dB / dA_d partial sums, which are grouped by other tiles.
   need_out=False (checkpoint recompute): only xs, MX(x) and the gate|up GEMM run (fused_mlp.py:286-288).
 Every kernel of the path is hand-written HIP (libmxfp8_mlp.so, _native.py): the rank-r LoRA products come from
 the quantizer (xs with MX(x), dxd with MX(dy)), the GEMM epilogues (y, dx) and the token-reduction kernel
@@ -28,8 +35,10 @@ from fused_linear import STATS, _cast, _part
 
 _F8, _E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
 ENABLED = [True]  # set False to compare against the unfused path in the same process
-# the gate|up GEMM with the SwiGLU forward in its epilogue (False: GEMM, then the separate forward kernel)
+# the SwiGLU forward in the epilogue of the gate|up GEMM (False: the GEMM, then the separate forward kernel)
 FUSED_EPILOGUE = [os.environ.get("MXFP8_FUSED_EPILOGUE", "1") != "0"]
+# the SwiGLU backward in the epilogue of the dhm GEMM (False: the GEMM, then the separate backward kernel)
+FUSED_BWD_EPILOGUE = [os.environ.get("MXFP8_FUSED_BWD_EPILOGUE", "0") == "1"]
 ACTIVE = [False]  # the fused path ran at least once (read by the step engine to shrink per-layer activations)
 SAVED_LESS = 12288  # bytes per token per layer not saved compared with the unfused path (h [T, 6144] bf16)
 
@@ -265,11 +274,18 @@ class _MLP(torch.autograd.Function):
         xsT = _transposed_padded(xs, _cdiv(T, 128) * 128)  # the backward kernel's operand form of xs
         # one read of dy2: its MX operand and dxd = bf16(bf16(dy2 · bd) · s_d) [T, R] with its zero-padded transpose
         qd, sd, dxd, dxdT = mxfp8.mx_quant_lora(dy2, lw.bdT, scale=s_d)
-        dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)  # MX(dy) · W_down, FT
-        del qd, sd
-        qg, sg, parts = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, lw.bgT, lw.buT, ad, lw.adT, s_g, s_u,
-                                    need_x, None, True, gu_ft=True)
-        del dhm
+        if need_x and R == 16 and FUSED_BWD_EPILOGUE[0]:
+            # one launch: dhm = MX(dy) · W_down in registers and, in the GEMM's epilogue, the SwiGLU backward:
+            # MX(dg | du) and the dxa / dB / dA_d partials
+            qg, sg, parts = mxfp8.swiglu_bwd_gemm(qd, sd, down, gu, xs, xsT, dxd, dxdT, bg, lw.bgT, bu, lw.buT, ad,
+                                                  lw.adT, s_g, s_u, T)
+            del qd, sd
+        else:
+            dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)  # MX(dy) · W_down, FT
+            del qd, sd
+            qg, sg, parts = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, lw.bgT, lw.buT, ad, lw.adT, s_g, s_u,
+                                        need_x, None, True, gu_ft=True)
+            del dhm
         # the partial sums, scaled and cast as fused_mlp.py:258, :319-326 do, in one kernel
         dxa = torch.empty((T, 2 * R), dtype=dt, device=dy2.device)  # bf16(s_g dxa_g | s_u dxa_u)
         xsd = torch.empty((T, R), dtype=dt, device=dy2.device)      # bf16(xS_down)

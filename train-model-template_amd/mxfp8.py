@@ -252,6 +252,35 @@ def swiglu_gemm(q, s, hold, xs, bg, bu, ad, s_g, s_u, m):
     return gu, qh, sh.view(E8), part
 
 
+def swiglu_bwd_gemm(q, s, down, gu, xs, xsT, dxd, dxdT, bg, bgT, bu, buT, ad, adT, s_g, s_u, m):
+    """The dgrad GEMM dhm = MX(dy) · W_down of the fused MLP with the SwiGLU backward in its epilogue: q, s the
+    MX-tiled codes and scales of dy [m, K]; down the MX down_proj (its dgrad-order operand).  -> (q_dgu
+    [tiled_rows(m), 2N] MX-tiled codes of dg | du, s_dgu its blocked scales, (dxa_p [N/128, m, 3r], dbg_p, dbu_p
+    [ceil(m/256), N, r], dad_p [ceil(m/256), r, N]) fp32 partials).  One launch for torch._scaled_mm + _bwd_kernel
+    (fused_mlp.py:307-314, :112-175); dhm is never stored."""
+    wtf, wtfs = dgrad_rows_operand(down)
+    n, K = wtf.shape
+    r = ad.shape[0]
+    dev = q.device
+    qg = torch.empty((tiled_rows(m), 2 * n), dtype=F8, device=dev)
+    sg = torch.empty(scale_numel(m, 2 * n), dtype=torch.uint8, device=dev)
+    nsb = _cdiv(m, 256)
+    dxa_p = torch.empty((n // 128, m, 3 * r), dtype=torch.float32, device=dev)
+    dbg_p = torch.empty((nsb, n, r), dtype=torch.float32, device=dev)
+    dbu_p = torch.empty((nsb, n, r), dtype=torch.float32, device=dev)
+    dad_p = torch.empty((nsb, r, n), dtype=torch.float32, device=dev)
+    ev = GEMM_EVENTS
+    if ev is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+    _native.gemm_swiglu_bwd(q, s, wtf, wtfs, m, n, K, gu, xs, xsT, dxd, dxdT, bg, bgT, bu, buT,
+                            ad, adT, s_g, s_u, qg, sg, dxa_p, dbg_p, dbu_p, dad_p)
+    if ev is not None:
+        e1.record()
+        ev.append((e0, e1, 2 * m * n * K))
+    return qg, sg.view(E8), (dxa_p, dbg_p, dbu_p, dad_p)
+
+
 # ---------------------------------------------------------------- generic MX linear (mxfp8.py:296-341)
 class _ActivationMemo:
     """The codes of the activation an MX linear quantized last, keyed by (weak reference, version).  Linears that
@@ -334,8 +363,8 @@ _CATS = (("in_proj_qkv", "in_proj_z"), ("q_proj", "k_proj", "v_proj"))
 FUSED_BWD = {"in_proj_qkv", "in_proj_z", "q_proj", "k_proj", "v_proj", "o_proj", "out_proj"}
 FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
 # what enable_mxfp8 attaches to a linear (disable_mxfp8 removes exactly these)
-_MX_ATTRS = ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_cat", "_mx_gu", "_mx_fbwd",
-             "_bf16_cpu", "forward")
+_MX_ATTRS = ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_wtf_tl", "_mx_wtfs", "_mx_cat",
+             "_mx_gu", "_mx_fbwd", "_bf16_cpu", "forward")
 
 
 def _mx_target(name, mod):
@@ -373,6 +402,15 @@ def fused_swiglu_rows(n, device=None):
     half, blk, a = within // 64, (within % 64) // 32, within % 32
     pi = ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3)
     return half * n + 64 * t + 32 * blk + pi
+
+
+def fused_dgrad_rows(n, device=None):
+    """Row order of W_downᵀ [n, K] for the dgrad GEMM with the fused SwiGLU backward (mxfp8_gemm_swiglu_bwd): inside
+    each 32-row block row a is logical row pi_col(a), so that every lane of the epilogue holds 16 contiguous
+    columns of dhm, the columns it also reads of gu."""
+    c = torch.arange(n, device=device)
+    a = c % 32
+    return c - a + ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3)
 
 
 class _GateUp:
@@ -506,6 +544,16 @@ def group_operand(lins):
 def _prep_single(lin):
     lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(lin.weight.data.to(torch.bfloat16))
     lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
+
+
+def dgrad_rows_operand(lin):
+    """(codes, scales) of W_downᵀ in the dgrad row order (fused_dgrad_rows), MX-tiled, for the GEMM with the fused
+    SwiGLU backward; made from the host copy of the bf16 weight on first use and kept with the MX copies."""
+    if "_mx_wtf_tl" not in lin.__dict__:
+        dev = lin._mx_w.device
+        wt = lin._bf16_cpu.to(dev, torch.bfloat16).t()
+        lin._mx_wtf_tl, lin._mx_wtfs = mx_quant_tiled(wt[fused_dgrad_rows(wt.shape[0], dev)].contiguous())
+    return lin._mx_wtf_tl, lin._mx_wtfs
 
 
 def _prep_gate_up(gate, up):
