@@ -167,12 +167,14 @@ int mxfp8_mlp_fwd(const void* gu, const void* xs, const void* bg, const void* bu
  * bgT, buT [r, N], adT [N, r].  Grid: super-blocks of SB rows (SB % 128 == 0) x column groups of CG columns
  * (CG % 128 == 0, N % CG == 0).  Outputs:
  *   q [T, 2N] + s (2N/128 tiles per row): MX(dg) in columns 0..N-1, MX(du) in N..2N-1  (skipped if q == NULL)
- *   dxa_part [N/128, T, 3r] fp32: dxa_g | dxa_u | xS_down partial sums over each 128-column quad (unscaled)
+ *   dxa_part [N/128, T, 3r] fp32: dxa_g | dxa_u | xS_down partial sums over each 128-column quad (unscaled);
+ *     [N/256, T, 3r] over each 256 columns with q_layout bit 2
  *   dbg_part, dbu_part [ceil(Tpad/SB), N, r] fp32 and dad_part [ceil(Tpad/SB), r, N]: per super-block sums of
  *     dgᵀ·xs_g, duᵀ·xs_u and (hᵀ·dxd)ᵀ (unscaled)
  *   dgu_out [T, 2N] bf16 (optional, may be NULL): dg | du themselves, for checks
  *   q_layout bit 0: q MX-tiled with 2N codes per row (see mxfp8_quant_tiled) instead of row-major;
- *   q_layout bit 1: gu and dhm in the FT layout (see mxfp8_gemm_nt) instead of row-major
+ *   q_layout bit 1: gu and dhm in the FT layout (see mxfp8_gemm_nt) instead of row-major;
+ *   q_layout bit 2: 8-wave workgroups, two quads summed in LDS (CG % 256 == 0, dgu_out NULL), one workgroup per CU
  */
 int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, const void* dhm, const void* dxd,
                   const void* dxdT, const void* bg, const void* bu, const void* bgT, const void* buT, const void* ad,

@@ -93,7 +93,7 @@ def test_fused_backward_matches_separate_path(cfg, T, gpu, monkeypatch):
     qd, sd, dxd, dxdT = mxfp8.mx_quant_lora(dy, lw.bdT, scale=s)
     dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=fused_mlp._LAYOUT_FT, m=T)
     q0, s0, p0 = fused_mlp._bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, lw.bg, lw.bu, lw.bgT, lw.buT, lw.ad, lw.adT, s, s,
-                                       True, None, True, gu_ft=True)
+                                       True, None, True, gu_ft=True, wide=False)
     q1, s1, p1 = mxfp8.swiglu_bwd_gemm(qd, sd, down, gu, xs, xsT, dxd, dxdT, lw.bg, lw.bgT, lw.bu, lw.buT, lw.ad,
                                        lw.adT, s, s, T)
     torch.cuda.synchronize()
@@ -113,7 +113,9 @@ def test_fused_backward_autograd_matches_separate_path(gpu):
     recomputes h and xS_down from gu); dB_g, dB_u, dA_d to fp32 rounding of their partial sums."""
     out = []
     for fused in (False, True):
+        # the split path with one dxa partial per 128 columns, the grouping of the fused epilogue
         fused_mlp.FUSED_EPILOGUE[0] = fused_mlp.FUSED_BWD_EPILOGUE[0] = fused
+        fused_mlp.WIDE_BWD[0] = False
         try:
             model, inps = workloads.build_model(3, T=2000, device=gpu)
             mxfp8.enable_mxfp8(model)
@@ -126,7 +128,7 @@ def test_fused_backward_autograd_matches_separate_path(gpu):
             gr = {n: p.grad.detach().clone() for n, p in mod.named_parameters() if p.requires_grad}
             out.append((y.detach(), x.grad.detach(), gr))
         finally:
-            fused_mlp.FUSED_EPILOGUE[0], fused_mlp.FUSED_BWD_EPILOGUE[0] = True, False
+            fused_mlp.FUSED_EPILOGUE[0], fused_mlp.FUSED_BWD_EPILOGUE[0], fused_mlp.WIDE_BWD[0] = True, False, True
     (y0, dx0, g0), (y1, dx1, g1) = out
     assert torch.equal(dx0, dx1)
     a, b = y1.float(), y0.float()
@@ -137,3 +139,39 @@ def test_fused_backward_autograd_matches_separate_path(gpu):
         else:
             err = ((g1[n] - g0[n]).abs().max() / g0[n].abs().max()).item()
             assert err <= 1e-5, (n, err)
+
+
+@pytest.mark.parametrize("cfg,T", [(3, 1100), (5, 600)])
+def test_wide_backward_matches_narrow(cfg, T, gpu):
+    """The 8-wave backward workgroups (one dxa partial per 256 columns, two quads summed in LDS) against the 4-wave
+    ones (one per 128 columns, the pairs added by the finish): MX codes and scales of dg | du bit-identical, each
+    wide dxa partial equal to the sum of its two narrow ones and the dB / dA_d sums equal, to fp32 rounding."""
+    model, inps = workloads.build_model(cfg, T=T, device=gpu)
+    mxfp8.enable_mxfp8(model)
+    fused_linear.new_step()
+    inp, mod = inps[0], model.layers[0].mlp
+    T, N, s = inp["T"], inp["N"], inp["s"]
+    hold, down = mod.gate_proj.base_layer._mx_gu[0], mod.down_proj.base_layer
+    g = lambda m: m.lora_A["default"].weight, lambda m: m.lora_B["default"].weight  # noqa: E731
+    lw = fused_mlp._prep(g[0](mod.gate_proj), g[1](mod.gate_proj), g[0](mod.up_proj), g[1](mod.up_proj),
+                         g[0](mod.down_proj), g[1](mod.down_proj), torch.bfloat16)
+    x, dy = inp["x"].to(gpu), inp["dy"].to(gpu)
+    q, sc, xs, _ = mxfp8.mx_quant_lora(x, lw.S, out_t=False)
+    gu, _, _, _ = mxfp8.swiglu_gemm(q, sc, hold, xs, lw.bg, lw.bu, lw.ad, s, s, T)
+    xsT = fused_mlp._transposed_padded(xs, -(-T // 128) * 128)
+    qd, sd, dxd, dxdT = mxfp8.mx_quant_lora(dy, lw.bdT, scale=s)
+    dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=fused_mlp._LAYOUT_FT, m=T)
+    args = (gu, xs, xsT, dhm, dxd, dxdT, lw.bg, lw.bu, lw.bgT, lw.buT, lw.ad, lw.adT, s, s, True, None, True)
+    q0, s0, p0 = fused_mlp._bwd_launch(*args, gu_ft=True, wide=False)
+    q1, s1, p1 = fused_mlp._bwd_launch(*args, gu_ft=True, wide=True)
+    torch.cuda.synchronize()
+    assert fused_mlp.LAST["bwd"]["wide"] and p1[0].shape[0] * 2 == p0[0].shape[0]
+    assert torch.equal(_tiled_rows(q1, T, 2 * N), _tiled_rows(q0, T, 2 * N)), "codes of dg | du"
+    assert torch.equal(s1.view(torch.uint8), s0.view(torch.uint8)), "scales of dg | du"
+    pairs = p0[0].double().view(-1, 2, T, p0[0].shape[2]).sum(1)
+    err = ((p1[0].double() - pairs).abs().max() / pairs.abs().max()).item()
+    assert err <= 1e-6, err
+    for k, name in ((1, "dB_g"), (2, "dB_u"), (3, "dA_d")):
+        a, b = p1[k].double().sum(0), p0[k].double().sum(0)
+        err = ((a - b).abs().max() / b.abs().max()).item()
+        assert err <= 1e-5, (name, err)

@@ -191,8 +191,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPe
 // zero their values, so they add nothing to dB / dA_d.
 // Register budget: two waves per SIMD (<= 256 VGPRs; with three the kernel spills), i.e. two workgroups per
 // CU (the LDS, 52 KB at r = 16, would allow three).
-template <int R, bool kQuant, bool kDgu>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void bwd_kernel(
+// kQ = 2: 8 waves, two quads side by side (wave w on tile 8o + w of the column group): the dxa products are
+// summed over all 8 waves in LDS, so there is one partial per 256 columns instead of per 128 (half the partial
+// bytes written here and read by the finish); one workgroup per CU (105 KB of LDS at r = 16), still two waves
+// per SIMD.
+template <int R, bool kQuant, bool kDgu, int kQ = 1>
+__global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))) void bwd_kernel(
     const uint16_t* __restrict__ gu, const uint16_t* __restrict__ xs, const uint16_t* __restrict__ xsT,
     const uint16_t* __restrict__ dhm, const uint16_t* __restrict__ dxd, const uint16_t* __restrict__ dxdT,
     const uint16_t* __restrict__ bg, const uint16_t* __restrict__ bu, const uint16_t* __restrict__ bgT,
@@ -200,8 +204,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
     int Tpad, int N, int SB, int CG, float s_g, float s_u, uint8_t* __restrict__ q, uint8_t* __restrict__ s,
     float* __restrict__ dxa_part, float* __restrict__ dbg_part, float* __restrict__ dbu_part,
     float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out, bool q_tiled, bool gu_ft) {
-  __shared__ float red[4][32][3 * R + 1];                              // per-wave dxa | dxa_u | xS products
-  __shared__ __attribute__((aligned(16))) uint16_t trt[4][3][32 * kTrLd];  // per-wave dg, du, h rows
+  constexpr int kW = 4 * kQ, kCols = 128 * kQ;  // waves, columns per pass over the column group
+  __shared__ float red[kW][32][3 * R + 1];                              // per-wave dxa | dxa_u | xS products
+  __shared__ __attribute__((aligned(16))) uint16_t trt[kW][3][32 * kTrLd];  // per-wave dg, du, h rows
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int r0 = blockIdx.x * SB, r1 = min(r0 + SB, Tpad);
   const int c0 = blockIdx.y * CG;
@@ -210,8 +215,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
   struct RowIn {
     uint32_t g[8], u[8], d[8];  // gate, up, dhm of the lane's row and 16 columns
   };
-  for (int oc = 0; oc < CG / 128; ++oc) {
-    const int jb = c0 + oc * 128 + w * 32;  // this wave's tile
+  for (int oc = 0; oc < CG / kCols; ++oc) {
+    const int jb = c0 + oc * kCols + w * 32;  // this wave's tile
     // weights of this tile: LoRA-B rows jb + pi_col(lane % 32) (bg, bu, adᵀ) and, for the products that
     // reduce over the columns, rows ρ of bgᵀ, buᵀ, ad at the lane's columns
     v8bf wbg[R / 16], wbu[R / 16], wad[R / 16], fbg[2], fbu[2], fad[2];
@@ -367,10 +372,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
       // sum the 4 waves' products (fixed order) into the quad's own partial (stores only: a read-modify-write
       // here would wait behind the next row block's prefetch, the memory counter completing in order)
       __syncthreads();
-      float* qpart = dxa_part + ((int64_t)(blockIdx.y * (CG / 128) + oc) * T + rb) * 3 * R;
-      for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 256) {
+      float* qpart = dxa_part + ((int64_t)(blockIdx.y * (CG / kCols) + oc) * T + rb) * 3 * R;
+      for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 256 * kQ) {
         const int mm = idx / (3 * R), cc = idx % (3 * R);
-        if (rb + mm < T) qpart[idx] = ((red[0][mm][cc] + red[1][mm][cc]) + red[2][mm][cc]) + red[3][mm][cc];
+        float v = red[0][mm][cc];
+#pragma unroll
+        for (int u = 1; u < kW; ++u) v += red[u][mm][cc];
+        if (rb + mm < T) qpart[idx] = v;
       }
       __syncthreads();
     };
@@ -511,16 +519,19 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                              const void* ad, const void* adT, int64_t T, int64_t N, int64_t r, float s_g, float s_u,
                              int64_t SB, int64_t CG, void* q, void* s, float* dxa_part, float* dbg_part,
                              float* dbu_part, float* dad_part, void* dgu_out, int64_t q_layout, void* stream) {
-  MX_CHECK_ARG(q_layout >= 0 && q_layout <= 3,
-               "mxfp8_mlp_bwd: q_layout must be 0..3 (bit 0: q MX-tiled, bit 1: gu and dhm in the FT layout)");
+  MX_CHECK_ARG(q_layout >= 0 && q_layout <= 7,
+               "mxfp8_mlp_bwd: q_layout must be 0..7 (bit 0: q MX-tiled, bit 1: gu and dhm in the FT layout, bit 2: "
+               "8-wave workgroups, one dxa partial per 256 columns)");
   MX_CHECK_ARG(gu && xs && xsT && dhm && dxd && dxdT && bg && bu && bgT && buT && ad && adT && dxa_part &&
                    dbg_part && dbu_part && dad_part,
                "mxfp8_mlp_bwd: null pointer");
   MX_CHECK_ARG((q == nullptr) == (s == nullptr), "mxfp8_mlp_bwd: q and s go together");
   MX_CHECK_ARG(T > 0 && N > 0 && N % 128 == 0 && (r == 16 || r == 32), "mxfp8_mlp_bwd: bad shape (N %% 128)");
   MX_CHECK_ARG(T * 2 * N < (1LL << 31), "mxfp8_mlp_bwd: T * 2N must stay below 2^31");
-  MX_CHECK_ARG(SB > 0 && SB % 128 == 0 && CG > 0 && CG % 128 == 0 && N % CG == 0,
-               "mxfp8_mlp_bwd: SB must be a multiple of 128, CG a multiple of 128 dividing N");
+  const bool wide = (q_layout & 4) != 0;
+  MX_CHECK_ARG(SB > 0 && SB % 128 == 0 && CG > 0 && CG % (wide ? 256 : 128) == 0 && N % CG == 0,
+               "mxfp8_mlp_bwd: SB must be a multiple of 128, CG a multiple of 128 (256 with bit 2) dividing N");
+  MX_CHECK_ARG(!wide || !dgu_out, "mxfp8_mlp_bwd: dgu_out takes the 4-wave workgroups");
   MX_CHECK_ARG(mx_aligned(gu, 16) && mx_aligned(dhm, 16) && mx_aligned(xs, 16) && mx_aligned(xsT, 16) &&
                    mx_aligned(dxd, 16) && mx_aligned(dxdT, 16) && mx_aligned(bg, 16) && mx_aligned(bu, 16) &&
                    mx_aligned(bgT, 16) && mx_aligned(buT, 16) && mx_aligned(ad, 16) && mx_aligned(adT, 16) &&
@@ -535,7 +546,15 @@ extern "C" int mxfp8_mlp_bwd(const void* gu, const void* xs, const void* xsT, co
                  (int)CG, s_g, s_u, (uint8_t*)q, (uint8_t*)s, dxa_part, dbg_part, dbu_part, dad_part, (uint16_t*)dgu_out, \
                  (q_layout & 1) != 0, (q_layout & 2) != 0
   MX_CHECK_ARG(!dgu_out || q, "mxfp8_mlp_bwd: dgu_out needs q");
-  if (r == 16) {
+  if (wide) {
+    if (r == 16) {
+      if (q) bwd_kernel<16, true, false, 2><<<grid, 512, 0, stm>>>(BWD_ARGS);
+      else bwd_kernel<16, false, false, 2><<<grid, 512, 0, stm>>>(BWD_ARGS);
+    } else {
+      if (q) bwd_kernel<32, true, false, 2><<<grid, 512, 0, stm>>>(BWD_ARGS);
+      else bwd_kernel<32, false, false, 2><<<grid, 512, 0, stm>>>(BWD_ARGS);
+    }
+  } else if (r == 16) {
     if (dgu_out) bwd_kernel<16, true, true><<<grid, 256, 0, stm>>>(BWD_ARGS);
     else if (q) bwd_kernel<16, true, false><<<grid, 256, 0, stm>>>(BWD_ARGS);
     else bwd_kernel<16, false, false><<<grid, 256, 0, stm>>>(BWD_ARGS);

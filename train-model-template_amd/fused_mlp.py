@@ -37,6 +37,8 @@ _F8, _E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
 ENABLED = [True]  # set False to compare against the unfused path in the same process
 # the SwiGLU forward in the epilogue of the gate|up GEMM (False: the GEMM, then the separate forward kernel)
 FUSED_EPILOGUE = [os.environ.get("MXFP8_FUSED_EPILOGUE", "1") != "0"]
+# 8-wave backward workgroups summing two 128-column quads in LDS (half the dxa partial bytes)
+WIDE_BWD = [os.environ.get("MXFP8_WIDE_BWD", "1") != "0"]
 # the SwiGLU backward in the epilogue of the dhm GEMM (False: the GEMM, then the separate backward kernel)
 FUSED_BWD_EPILOGUE = [os.environ.get("MXFP8_FUSED_BWD_EPILOGUE", "0") == "1"]
 ACTIVE = [False]  # the fused path ran at least once (read by the step engine to shrink per-layer activations)
@@ -66,19 +68,21 @@ def _fwd_groups(T, N, R=16):
     return int(_native.load().mxfp8_mlp_fwd_groups(T, N, R))
 
 
-def _bwd_grid(T, N, R):
-    """(SB, CG) of the backward kernel (SB, CG multiples of 128; two 4-wave workgroups per CU).  Every
-    workgroup of a round runs at the same pace, so the time goes as rounds x (SB/32 row blocks x CG/128 column
-    quads); pick the least of that, then the fewest partial-sum bytes (per super-block dB / dA_d partials; the
-    dxa partials are one per 128-column quad whatever the grid; the trade-off of fused_mlp.py:218-232)."""
+def _bwd_grid(T, N, R, wide=False):
+    """(SB, CG) of the backward kernel (SB a multiple of 128; CG a multiple of 128 with two 4-wave workgroups per
+    CU, or of 256 with one 8-wave workgroup per CU when wide).  Every workgroup of a round runs at the same pace,
+    so the time goes as rounds x (SB/32 row blocks x column passes); pick the least of that, then the fewest
+    partial-sum bytes (per super-block dB / dA_d partials; the dxa partials are one per 128 (wide: 256) columns
+    whatever the grid; the trade-off of fused_mlp.py:218-232)."""
     tpad = _cdiv(T, 128) * 128
-    cap = 2 * _n_cu()
+    cap = _n_cu() * (1 if wide else 2)
+    cols = 256 if wide else 128
     best = None
-    for cg in [128 * d for d in _divisors(N // 128)]:
+    for cg in [cols * d for d in _divisors(N // cols)]:
         ncg = N // cg
         for sb in range(128, tpad + 128, 128):
             nsb = _cdiv(tpad, sb)
-            work = _cdiv(nsb * ncg, cap) * (sb // 32) * (cg // 128)
+            work = _cdiv(nsb * ncg, cap) * (sb // 32) * (cg // cols)
             partial = nsb * N * R * 3 * 4
             key = (work, partial)
             if best is None or key < best[0]:
@@ -110,27 +114,31 @@ def mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, write_q, h_out=None, tiled=False, gu_f
 
 
 def _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, s_g, s_u, need_q, dgu_out, tiled,
-                gu_ft=False):
+                gu_ft=False, wide=None):
     """Run the backward kernel; -> (q, s, (dxa_p, dbg_p, dbu_p, dad_p)) with the partial sums unreduced.
-    gu_ft: gu and dhm in the fused-tile layout (T taken from xs)."""
+    gu_ft: gu and dhm in the fused-tile layout (T taken from xs).  wide: 8-wave workgroups with one dxa partial
+    per 256 columns (None: WIDE_BWD when N allows it and no dgu_out is asked for)."""
     T, N2 = xs.shape[0], gu.shape[1]
     N, R = N2 // 2, ad.shape[0]
     dev = gu.device
     tpad = _cdiv(T, 128) * 128
-    SB, CG = _bwd_grid(T, N, R)
+    if wide is None:
+        wide = WIDE_BWD[0] and N % 256 == 0 and dgu_out is None
+    SB, CG = _bwd_grid(T, N, R, wide)
     nsb, ncg = _cdiv(tpad, SB), N // CG
-    LAST["bwd"] = dict(SB=SB, CG=CG, nsb=nsb, ncg=ncg)
+    LAST["bwd"] = dict(SB=SB, CG=CG, nsb=nsb, ncg=ncg, wide=wide)
     if need_q:
         q = torch.empty((mxfp8.tiled_rows(T) if tiled else T, N2), dtype=_F8, device=dev)
         s = torch.empty(_cdiv(T, 128) * (N2 // 128) * 512, dtype=torch.uint8, device=dev)
     else:
         q = s = None
-    dxa_p = torch.empty((N // 128, T, 3 * R), dtype=torch.float32, device=dev)  # one partial per 128 columns
+    # one dxa partial per 128 (wide: 256) columns
+    dxa_p = torch.empty((N // (256 if wide else 128), T, 3 * R), dtype=torch.float32, device=dev)
     dbg_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
     dbu_p = torch.empty((nsb, N, R), dtype=torch.float32, device=dev)
     dad_p = torch.empty((nsb, R, N), dtype=torch.float32, device=dev)
     _native.mlp_bwd(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, bgT, buT, ad, adT, T, N, R, s_g, s_u, SB, CG, q, s,
-                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out, q_layout=int(tiled) | (2 if gu_ft else 0))
+                    dxa_p, dbg_p, dbu_p, dad_p, dgu_out, q_layout=int(tiled) | (2 if gu_ft else 0) | (4 if wide else 0))
     return q, (s.view(_E8) if need_q else None), (dxa_p, dbg_p, dbu_p, dad_p)
 
 
