@@ -404,8 +404,10 @@ def _kernel_key(name, grid):
         shape = {(4032, "0"): "gate|up", (2016, "0"): "dh", (672, "16"): "down", (672, "32"): "dx"}
         targs = [a.strip() for a in (m.group(2) or "<0").strip("<>").split(",")]
         r = targs[0]
-        if len(targs) > 2 and targs[2] == "true":
+        if len(targs) > 2 and targs[2] == "1":
             k += " gate|up + SwiGLU epilogue"
+        elif len(targs) > 2 and targs[2] == "2":
+            k += " dh + SwiGLU backward epilogue"
         else:
             k += " " + shape.get((wg, r), f"{wg} WGs")
     return k
