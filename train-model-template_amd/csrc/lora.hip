@@ -788,11 +788,12 @@ extern "C" int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, 
 
 extern "C" int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K) {
   if (T <= 0 || K <= 0 || K % 128) return 0;
-  // one workgroup per CU (K / 128 column blocks x chunks of a multiple of 32 tokens): at configuration 3
-  // (T = 10752, K = 2048, 16 chunks) 13.7 / 16.5 us for rp 16 / 32 with x in the last-level cache and 24.0 /
-  // 25.8 us from HBM, against 14.3 / 17.1 and 27.1 / 29.5 us at 32 chunks and more for more chunks (the partials
-  // tn_sum adds grow with the chunk count)
-  const int64_t cols = K / 128, want = (256 + cols - 1) / cols;
+  // K / 128 column blocks x chunks of a multiple of 32 tokens.  While x fits the last-level cache (the rule
+  // of lora_tn_launch), one workgroup per CU: at configuration 3 (T = 10752, K = 2048, 16 chunks) 13.7 / 16.5 us
+  // for rp 16 / 32, against 14.3 / 17.1 us at 32 chunks and more for more chunks (the partials tn_sum adds grow
+  // with the chunk count).  A longer x streams from HBM and needs two workgroups per CU: at configuration 4
+  // (T = 142336) 111 / 136 us at 32 chunks against 182 / 236 us at 16.
+  const int64_t cols = K / 128, wgs = T * K * 2 <= (192LL << 20) ? 256 : 512, want = (wgs + cols - 1) / cols;
   const int64_t blocks = (T + 31) / 32;
   const int64_t per = (blocks + want - 1) / want;
   return (blocks + per - 1) / per;
