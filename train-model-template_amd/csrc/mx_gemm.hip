@@ -86,8 +86,8 @@ struct Lora {
   float alpha;
 };
 
-// Fused SwiGLU forward epilogue (kEpi == kEpiSwiGluFwd): the operands beyond the GEMM's.  The B operand is W_gu = [W_gate; W_up] in
-// the fused row order (fused_swiglu_row in the host code): output tile t (128 columns) holds gate columns
+// Fused SwiGLU forward epilogue (kEpi == kEpiSwiGluFwd): the operands beyond the GEMM's.  The B operand is
+// W_gu = [W_gate; W_up] in the fused row order (fused_swiglu_row in the host code): output tile t (128 columns) holds gate columns
 // 64 t + 0..63 and then up columns 64 t + 0..63, each 32-column block with its weight rows permuted by pi_col,
 // so that acc[b][mt] (gate) and acc[2 + b][mt] (up) hold, in lane l, row m = l % 32 and the 16 CONTIGUOUS
 // columns jb + (l / 32) * 16 + i (jb = 64 t + 32 b): the layout of the fused forward kernel and of the FT blocks.
@@ -693,7 +693,8 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
           dbx[(j0 + i) * 16 + r0] = dbg[jh][i];
           dbx[512 + (j0 + i) * 16 + r0] = dbu[jh][i];
         }
-        *reinterpret_cast<float4*>(dbx + 1024 + r0 * 32 + j0) = make_float4(dad[jh][0], dad[jh][1], dad[jh][2], dad[jh][3]);
+        *reinterpret_cast<float4*>(dbx + 1024 + r0 * 32 + j0) =
+            make_float4(dad[jh][0], dad[jh][1], dad[jh][2], dad[jh][3]);
       }
       lds_barrier();
       for (int f = tid; f < 384; f += 256) {  // 3 x 128 float4 per wave
@@ -961,11 +962,11 @@ extern "C" int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* 
   hipStream_t stm = (hipStream_t)stream;
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   if (r == 16)
-    gemm_kernel<16, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
-                                                                   Lora{}, plan, tiled, sw, SwBwd{});
+    gemm_kernel<16, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(
+        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{});
   else
-    gemm_kernel<32, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs,
-                                                                   Lora{}, plan, tiled, sw, SwBwd{});
+    gemm_kernel<32, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(
+        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{});
   MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_fwd");
   return MXFP8_OK;
 }

@@ -309,7 +309,8 @@ class _MLP(torch.autograd.Function):
         ag_dt, au_dt, bd_dt = ctx.pdt
         part = torch.empty(_native.lora_tn_chunks(T, K) * 2 * R * K, dtype=torch.float32, device=dy2.device)
         dB_d = torch.empty((K, R), dtype=torch.float32 if bd_dt == torch.float32 else dt, device=dy2.device)
-        _native.lora_tn(dy2, xsd, dB_d, part[:part.numel() // 2], scale=s_d, transpose=True)  # bf16(bf16(dyᵀ xsd) s_d)
+        # bf16(bf16(dyᵀ xsd) s_d)
+        _native.lora_tn(dy2, xsd, dB_d, part[:part.numel() // 2], scale=s_d, transpose=True)
         dx = None
         if need_x:
             # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
