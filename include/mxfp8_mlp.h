@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 7
+#define MXFP8_MLP_ABI_VERSION 8
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -33,6 +33,7 @@ extern "C" {
 #define MXFP8_GEMM_B_TILED 2
 #define MXFP8_GEMM_WIDE 4
 #define MXFP8_GEMM_C_FT 8
+#define MXFP8_GEMM_B_PI 16
 
 /* Returns MXFP8_MLP_ABI_VERSION of the built library (the Python loader refuses a mismatch). */
 int mxfp8_abi_version(void);
@@ -106,6 +107,10 @@ int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
  * ((r/32) * (C/32) + c/32) * 1024 elements; element (r, c) inside it at ((c/8) % 2) * 512 +
  * (r%32 + 32 * ((c/16) % 2)) * 8 + c % 8.  It is the order in which the fused kernels' waves read a 32 x 32 tile
  * (two contiguous 1 KB pieces); no reference counterpart (the reference keeps gu and dhm row-major).
+ * MXFP8_GEMM_B_PI = B holds its rows in the pi_col order inside every 32-row block: B row 32b + a is logical
+ * row 32b + pi_col(a), pi_col(a) = ((a >> 2) & 1) * 16 + (a >> 3) * 4 + (a & 3) (mxfp8.fused_dgrad_rows); Q of
+ * the rank-r epilogue stays in row order.  C is the same matrix; each lane then holds 16 contiguous columns and
+ * stores them as two 16-byte pieces instead of four 8-byte ones.
  * workspace (optional, 256-byte aligned, workspace_bytes long; used with MXFP8_GEMM_WIDE only): when it holds
  * at least mxfp8_gemm_workspace_size(M, N, K) bytes, the tiles of a last wave that would leave more than half
  * of the CUs idle are split along K; their fp32 pieces go through the workspace and are added in a fixed order

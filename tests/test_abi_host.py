@@ -68,8 +68,11 @@ def test_argument_checks_reject_before_launch(lib):
     # GEMM epilogue rank not supported
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, p, 8, p, 8, 8, 1.0, 0, None, 0, None) == -1
     # unknown operand layout
-    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 16, None, 0, None) == -1
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 32, None, 0, None) == -1
     assert b"layout" in lib.mxfp8_last_error()
+    # B in the pi_col order stores 16-byte pieces: a row-major C with ldc % 8 != 0 is refused
+    assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 132, None, 0, None, 0, 0, 1.0, 16, None, 0, None) == -1
+    assert b"B_PI" in lib.mxfp8_last_error()
     # workspace given but misaligned
     assert lib.mxfp8_gemm_nt(p, p, 128, p, p, 128, 4, 128, 128, p, 128, None, 0, None, 0, 0, 1.0, 0,
                              ctypes.c_void_p(16), 1 << 20, None) == -1

@@ -7,6 +7,7 @@ step of the reference value (2^-8 relative) plus fp32 reordering slack (1e-3 of 
 import pytest
 import torch
 
+import _native
 import mxfp8
 from oracle import mlp as omlp
 from oracle import mx
@@ -188,3 +189,30 @@ def test_gemm_ft_output(M, N, K, r, gpu):
         # compare the elements of rows < M (the padding rows are not written)
         live = mx.from_ft(np.arange(want.size), mxfp8.ft_rows(M), N)[:M].reshape(-1)
         assert np.array_equal(got[live], want[live]), layout
+
+
+@pytest.mark.parametrize("M,N,K,layout,rank", [(10752, 6144, 2048, 8, 0), (1000, 640, 384, 8, 0), (333, 2048, 1024, 0, 16),
+                                               (700, 640, 384, 0, 32), (512, 1024, 256, 12, 0)])
+def test_b_pi_layout_matches_row_order(M, N, K, layout, rank, gpu):
+    """MXFP8_GEMM_B_PI (B rows in the pi_col order of mxfp8.fused_dgrad_rows, 16-byte stores) gives C bit for
+    bit equal to the GEMM with B in row order, in the row-major and FT output layouts, with and without the rank-r
+    epilogue and in the 8-wave shape."""
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    perm = mxfp8.fused_dgrad_rows(N, gpu)
+    qa, sa = mxfp8.mx_quant_tiled(a)
+    qb, sb = mxfp8.mx_quant_tiled(b)
+    qp, sp = mxfp8.mx_quant_tiled(b[perm].contiguous())
+    lora = lora_p = None
+    if rank:
+        P = (torch.randn(M, rank, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+        Q = (torch.randn(N, rank, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+        lora = lora_p = (P, Q)  # Q stays in row order
+    rows = mxfp8.ft_rows(M) if layout & 8 else M  # rows past M are not written: start both from zeros
+    ref = mxfp8.mx_mm(qa, sa, qb, sb, out=torch.zeros((rows, N), dtype=torch.bfloat16, device=gpu), lora=lora,
+                      alpha=0.5, layout=3 | layout, m=M)
+    got = mxfp8.mx_mm(qa, sa, qp, sp, out=torch.zeros((rows, N), dtype=torch.bfloat16, device=gpu), lora=lora_p,
+                      alpha=0.5, layout=3 | layout | _native.GEMM_B_PI, m=M)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))

@@ -223,7 +223,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   // lane's 16 bytes land at their swizzled LDS position.  MX-tiled operand (tiled_offset in mx_device.h): the
   // slice is one contiguous 1 KB block already in LDS order, lane i copies bytes 16i..16i+15, and a K step
   // advances 1 KB instead of 64 B.
-  const bool a_tiled = tiled & 1, b_tiled = (tiled >> 1) & 1, c_ft = (tiled >> 3) & 1;
+  const bool a_tiled = tiled & 1, b_tiled = (tiled >> 1) & 1, c_ft = (tiled >> 3) & 1, b_pi = (tiled >> 4) & 1;
   const int kst = K / kBK;
   const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);  // (row >> 2) & 3 == (lane >> 4) & 3 for these rows
   auto slice_off = [&](bool op_tiled, int R0, int Rn, int64_t ldd, int rbase) -> uint32_t {
@@ -732,7 +732,8 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   const int64_t ldc = cseg.ld[sg];
   const int ncol0 = cseg.col0[sg];
   // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
-  // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]
+  // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]; with B in the pi_col order (b_pi) the 16 contiguous columns
+  // n0 + wn*128 + nt*32 + (lane/32)*16 + i in acc[nt][mt][i]
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const int m = m0 + wm * 64 + mt * 32 + (lane & 31);
@@ -748,7 +749,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
       const int nb = n0 + wn * 128 + nt * 32;
       v16f o = acc[nt][mt];
       if constexpr (kR > 0) {
-        const int nr = min(nb + (lane & 31), N - 1);
+        const int nr = min(nb + (b_pi ? pi_col(lane & 31) : (lane & 31)), N - 1);
         v16f l = v16f{};
 #pragma unroll
         for (int h = 0; h < kR / 16; ++h) {
@@ -757,6 +758,24 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[i] = round_bf16(o[i]) + lora.alpha * l[i];
+      }
+      if (b_pi) {
+        if (m < M) {  // columns nb + (lane/32)*16 + 0..15 (N % 128 == 0: all inside)
+          uint32_t wv[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) wv[k] = pack_bf16x2(o[2 * k], o[2 * k + 1]);
+          const int n = nb + (lane >> 5) * 16;
+          if (c_ft) {
+            uint16_t* p = C + ft_offset(m, n, N);
+            *reinterpret_cast<uint4*>(p) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            *reinterpret_cast<uint4*>(p + 512) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+          } else {
+            uint16_t* p = C + (int64_t)m * ldc + (n - ncol0);
+            *reinterpret_cast<uint4*>(p) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            *reinterpret_cast<uint4*>(p + 8) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+          }
+        }
+        continue;
       }
       if (m < M) {
 #pragma unroll
@@ -852,9 +871,9 @@ int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const v
                "mxfp8_gemm_nt: need K %% 128 == 0 and N %% 128 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
                (long long)N, (long long)K);
   MX_CHECK_ARG(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "mxfp8_gemm_nt: dimension too large");
-  MX_CHECK_ARG(layout >= 0 && layout <= 15,
-               "mxfp8_gemm_nt: layout must be 0..15 (bit 0: A MX-tiled, bit 1: B MX-tiled, bit 2: 8-wave shape, "
-               "bit 3: C in the FT layout)");
+  MX_CHECK_ARG(layout >= 0 && layout <= 31,
+               "mxfp8_gemm_nt: layout must be 0..31 (bit 0: A MX-tiled, bit 1: B MX-tiled, bit 2: 8-wave shape, "
+               "bit 3: C in the FT layout, bit 4: B rows in the pi_col order)");
   if (layout & 1) lda = K;  // the tiled layouts have no row stride
   if (layout & 2) ldb = K;
   if (layout & MXFP8_GEMM_C_FT) ldc = N;
@@ -866,6 +885,8 @@ int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const v
   MX_CHECK_ARG(mx_aligned(a, 16) && mx_aligned(b, 16) && mx_aligned(sa, 16) && mx_aligned(sb, 16) &&
                    mx_aligned(c, 8),
                "mxfp8_gemm_nt: misaligned buffer");
+  MX_CHECK_ARG(!(layout & MXFP8_GEMM_B_PI) || (mx_aligned(c, 16) && ((layout & MXFP8_GEMM_C_FT) || ldc % 8 == 0)),
+               "mxfp8_gemm_nt: MXFP8_GEMM_B_PI stores 16-byte pieces (C 16-byte aligned, ldc %% 8 == 0)");
   MX_CHECK_ARG(workspace_bytes >= 0 && (workspace_bytes == 0 || (workspace && mx_aligned(workspace, 256))),
                "mxfp8_gemm_nt: workspace must be 256-byte aligned");
   if (lora_p) {
@@ -918,8 +939,8 @@ extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, con
                                  const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
                                  void* stream) {
   MX_CHECK_ARG(n_seg >= 1 && n_seg <= 4 && seg_col0 && seg_c && seg_ldc, "mxfp8_gemm_nt_seg: 1 to 4 segments");
-  MX_CHECK_ARG(!(layout & (MXFP8_GEMM_WIDE | MXFP8_GEMM_C_FT)),
-               "mxfp8_gemm_nt_seg: segments take the 4-wave shape and row-major C");
+  MX_CHECK_ARG(!(layout & (MXFP8_GEMM_WIDE | MXFP8_GEMM_C_FT | MXFP8_GEMM_B_PI)),
+               "mxfp8_gemm_nt_seg: segments take the 4-wave shape, row-major C and B in row order");
   CSeg cs{};
   cs.n = (int)n_seg;
   for (int64_t k = 0; k < n_seg; ++k) {

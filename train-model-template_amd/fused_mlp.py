@@ -37,6 +37,8 @@ _F8, _E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
 ENABLED = [True]  # set False to compare against the unfused path in the same process
 # the SwiGLU forward in the epilogue of the gate|up GEMM (False: the GEMM, then the separate forward kernel)
 FUSED_EPILOGUE = [os.environ.get("MXFP8_FUSED_EPILOGUE", "1") != "0"]
+# the dhm GEMM with W_downᵀ in the dgrad row order (16-byte stores of dhm; False: W_downᵀ in row order)
+DGRAD_B_PI = [os.environ.get("MXFP8_DGRAD_B_PI", "1") != "0"]
 # 8-wave backward workgroups summing two 128-column quads in LDS (half the dxa partial bytes)
 WIDE_BWD = [os.environ.get("MXFP8_WIDE_BWD", "1") != "0"]
 # the SwiGLU backward in the epilogue of the dhm GEMM (False: the GEMM, then the separate backward kernel)
@@ -289,7 +291,13 @@ class _MLP(torch.autograd.Function):
                                                   lw.adT, s_g, s_u, T)
             del qd, sd
         else:
-            dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)  # MX(dy) · W_down, FT
+            # MX(dy) · W_down in the FT layout; with W_downᵀ in the dgrad row order the epilogue stores whole
+            # 16-byte pieces (the same dhm)
+            if DGRAD_B_PI[0]:
+                dhm = mxfp8.mx_mm(qd, sd, *mxfp8.dgrad_rows_operand(down), layout=_LAYOUT_FT | _native.GEMM_B_PI,
+                                  m=T)
+            else:
+                dhm = mxfp8.mx_mm(qd, sd, down._mx_wt_tl, down._mx_wts, layout=_LAYOUT_FT, m=T)
             del qd, sd
             qg, sg, parts = _bwd_launch(gu, xs, xsT, dhm, dxd, dxdT, bg, bu, lw.bgT, lw.buT, ad, lw.adT, s_g, s_u,
                                         need_x, None, True, gu_ft=True)

@@ -207,7 +207,8 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     out = bf16(out + alpha · P · Qᵀ) with lora = (P [M, r], Q [N, r]) (the addmm_ after the GEMM).
     layout bit 0 / 1: q / wq hold MX-tiled codes (mx_quant_tiled, tile_codes); then M = m (q has the rows
     padded to 16).  Bit 2: 8-wave 256 x 256 workgroups (see _native.gemm_nt).  Bit 3: out in the fused-tile
-    layout (pass out with ft_rows(M) rows)."""
+    layout (pass out with ft_rows(M) rows).  Bit 4: wq rows in the pi_col order of fused_dgrad_rows (Q in row
+    order), out the same matrix stored in 16-byte pieces."""
     M, K = q.shape
     if m is not None:
         M = m
@@ -541,18 +542,25 @@ def group_operand(lins):
 
 
 # ---------------------------------------------------------------- enable / disable (mxfp8.py:452-509)
-def _prep_single(lin):
-    lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(lin.weight.data.to(torch.bfloat16))
+def _dgrad_rows(lin, w):
+    wt = w.t()
+    lin._mx_wtf_tl, lin._mx_wtfs = mx_quant_tiled(wt[fused_dgrad_rows(wt.shape[0], w.device)].contiguous())
+
+
+def _prep_single(lin, leaf):
+    w = lin.weight.data.to(torch.bfloat16)
+    lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(w)
     lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
+    if leaf == "down_proj":  # the fused MLP's dhm GEMM operand (dgrad_rows_operand)
+        _dgrad_rows(lin, w)
 
 
 def dgrad_rows_operand(lin):
-    """(codes, scales) of W_downᵀ in the dgrad row order (fused_dgrad_rows), MX-tiled, for the GEMM with the fused
-    SwiGLU backward; made from the host copy of the bf16 weight on first use and kept with the MX copies."""
+    """(codes, scales) of W_downᵀ in the dgrad row order (fused_dgrad_rows), MX-tiled: the B operand of the fused
+    MLP's dhm GEMM (with MXFP8_GEMM_B_PI, or the fused SwiGLU backward).  Made at enable_mxfp8 for down_proj,
+    else from the host copy of the bf16 weight on first use, and kept with the MX copies."""
     if "_mx_wtf_tl" not in lin.__dict__:
-        dev = lin._mx_w.device
-        wt = lin._bf16_cpu.to(dev, torch.bfloat16).t()
-        lin._mx_wtf_tl, lin._mx_wtfs = mx_quant_tiled(wt[fused_dgrad_rows(wt.shape[0], dev)].contiguous())
+        _dgrad_rows(lin, lin._bf16_cpu.to(lin._mx_w.device, torch.bfloat16))
     return lin._mx_wtf_tl, lin._mx_wtfs
 
 
@@ -607,7 +615,7 @@ def enable_mxfp8(model):
             n_pair += 1
     for leaf, lin in found:
         if id(lin) not in prepared:
-            _prep_single(lin)
+            _prep_single(lin, leaf)
         _install(lin, leaf)
     torch.cuda.empty_cache()
     print(f"MXFP8: {len(found)} frozen linears on MX GEMMs (bf16 weights moved to host memory;"
