@@ -37,8 +37,9 @@ _F8, _E8 = torch.float8_e4m3fn, torch.float8_e8m0fnu
 ENABLED = [True]  # set False to compare against the unfused path in the same process
 # the SwiGLU forward in the epilogue of the gate|up GEMM (False: the GEMM, then the separate forward kernel)
 FUSED_EPILOGUE = [os.environ.get("MXFP8_FUSED_EPILOGUE", "1") != "0"]
-# the dhm GEMM with W_downᵀ in the dgrad row order (16-byte stores of dhm; False: W_downᵀ in row order)
-DGRAD_B_PI = [os.environ.get("MXFP8_DGRAD_B_PI", "1") != "0"]
+# the down, dhm and dx GEMMs with their weight operand in the pi_col row order (MXFP8_GEMM_B_PI: 16-byte stores
+# of y, dhm and dx; False: the weights in row order)
+B_PI = [os.environ.get("MXFP8_B_PI", "1") != "0"]
 # 8-wave backward workgroups summing two 128-column quads in LDS (half the dxa partial bytes)
 WIDE_BWD = [os.environ.get("MXFP8_WIDE_BWD", "1") != "0"]
 # the SwiGLU backward in the epilogue of the dhm GEMM (False: the GEMM, then the separate backward kernel)
@@ -255,7 +256,11 @@ class _MLP(torch.autograd.Function):
                 qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True, gu_ft=True)
         if need_out:
             # y = bf16(bf16(MX(h)·W_downᵀ) + s_d · xS_down · B_dᵀ): the addmm_ of fused_mlp.py:284 in the epilogue
-            y = mxfp8.mx_mm(qh, sh, down._mx_w_tl, down._mx_ws, lora=(xsd, bd), alpha=s_d, layout=3, m=T)
+            if B_PI[0] and "_mx_wp_tl" in down.__dict__:
+                y = mxfp8.mx_mm(qh, sh, down._mx_wp_tl, down._mx_wps, lora=(xsd, bd), alpha=s_d,
+                                layout=3 | _native.GEMM_B_PI, m=T)
+            else:
+                y = mxfp8.mx_mm(qh, sh, down._mx_w_tl, down._mx_ws, lora=(xsd, bd), alpha=s_d, layout=3, m=T)
             del qh, sh, xsd
         else:  # graph only (checkpoint recompute / prefix backward): nobody reads y
             STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
@@ -293,7 +298,7 @@ class _MLP(torch.autograd.Function):
         else:
             # MX(dy) · W_down in the FT layout; with W_downᵀ in the dgrad row order the epilogue stores whole
             # 16-byte pieces (the same dhm)
-            if DGRAD_B_PI[0]:
+            if B_PI[0]:
                 dhm = mxfp8.mx_mm(qd, sd, *mxfp8.dgrad_rows_operand(down), layout=_LAYOUT_FT | _native.GEMM_B_PI,
                                   m=T)
             else:
@@ -323,7 +328,11 @@ class _MLP(torch.autograd.Function):
         if need_x:
             # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
             # fused_mlp.py:331 in its epilogue
-            dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
+            if B_PI[0]:
+                dx = mxfp8.mx_mm(qg, sg, hold.wtp_tl, hold.wtps, lora=(dxa, lw.ST), alpha=1.0,
+                                 layout=3 | _native.GEMM_B_PI, m=T)
+            else:
+                dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
         fp32_a = ag_dt == au_dt == torch.float32

@@ -364,8 +364,8 @@ _CATS = (("in_proj_qkv", "in_proj_z"), ("q_proj", "k_proj", "v_proj"))
 FUSED_BWD = {"in_proj_qkv", "in_proj_z", "q_proj", "k_proj", "v_proj", "o_proj", "out_proj"}
 FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
 # what enable_mxfp8 attaches to a linear (disable_mxfp8 removes exactly these)
-_MX_ATTRS = ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_wtf_tl", "_mx_wtfs", "_mx_cat",
-             "_mx_gu", "_mx_fbwd", "_bf16_cpu", "forward")
+_MX_ATTRS = ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_wtf_tl", "_mx_wtfs", "_mx_wp_tl",
+             "_mx_wps", "_mx_cat", "_mx_gu", "_mx_fbwd", "_bf16_cpu", "forward")
 
 
 def _mx_target(name, mod):
@@ -428,6 +428,9 @@ class _GateUp:
         self.w, self.ws, self.wt, self.wts = quant_both(w)
         self.w_tl, self.wt_tl = tile_codes(self.w), tile_codes(self.wt)
         self.wf_tl, self.wfs = mx_quant_tiled(w[fused_swiglu_rows(self.n, w.device)].contiguous())
+        # the dgrad operand W_guᵀ [K, 2N] with its rows in the pi_col order (MXFP8_GEMM_B_PI)
+        wt = w.t()
+        self.wtp_tl, self.wtps = mx_quant_tiled(wt[fused_dgrad_rows(wt.shape[0], w.device)].contiguous())
         self.half_t = [None, None]
 
     def rows(self, i):
@@ -551,8 +554,9 @@ def _prep_single(lin, leaf):
     w = lin.weight.data.to(torch.bfloat16)
     lin._mx_w, lin._mx_ws, lin._mx_wt, lin._mx_wts = quant_both(w)
     lin._mx_w_tl, lin._mx_wt_tl = tile_codes(lin._mx_w), tile_codes(lin._mx_wt)
-    if leaf == "down_proj":  # the fused MLP's dhm GEMM operand (dgrad_rows_operand)
+    if leaf == "down_proj":  # the fused MLP's operands in the pi_col row order (MXFP8_GEMM_B_PI)
         _dgrad_rows(lin, w)
+        lin._mx_wp_tl, lin._mx_wps = mx_quant_tiled(w[fused_dgrad_rows(w.shape[0], w.device)].contiguous())
 
 
 def dgrad_rows_operand(lin):
