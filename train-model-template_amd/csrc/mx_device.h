@@ -166,6 +166,17 @@ __device__ __forceinline__ void load16_rc(const uint16_t* base, int64_t r, int64
   w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
 }
 
+// load16_rc with non-temporal loads (a stream read once: evict-first in the caches)
+__device__ __forceinline__ void load16_rc_nt(const uint16_t* base, int64_t r, int64_t c0, int64_t C, bool ft,
+                                             uint32_t* w) {
+  typedef unsigned int u32x4n __attribute__((ext_vector_type(4)));
+  const uint16_t* p = base + (ft ? ft_offset(r, c0, C) : r * C + c0);
+  const u32x4n a = __builtin_nontemporal_load(reinterpret_cast<const u32x4n*>(p));
+  const u32x4n b = __builtin_nontemporal_load(reinterpret_cast<const u32x4n*>(p + (ft ? 512 : 8)));
+  w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+  w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
+}
+
 // MX-quantize the 16 contiguous values w (8 packed pairs) of row mc, columns k0..k0+15, which with the partner
 // lane's 16 form one 32-block: one 16-byte code store (row-major with Kq codes per row, or MX-tiled), scale
 // byte of row m (0 for padded rows).

@@ -49,6 +49,14 @@
 #include "abi_common.h"
 #include "mx_device.h"
 
+// gu leaves the gate|up epilogue with non-temporal stores: it is read again only by the backward, and
+// streaming it past the last-level cache keeps MX(h) and the xS_down partials there for the down GEMM and the
+// partial sum that follow (with the backward's non-temporal gu loads, MX_BWD_NT_LOAD in mlp_fused.hip: 10-17 us
+// per configuration-3 step faster over five A/B pairs on one box).
+#ifndef MX_NT_GU
+#define MX_NT_GU 1
+#endif
+
 using namespace mxk;
 
 namespace {
@@ -434,10 +442,10 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
         if (live) {  // the lane's columns i = 0..7 and 8..15 are 16 contiguous bytes each in an FT block
           uint16_t* pg = swe.gu + ft_offset(m, jb + lg * 16, 2 * Nf);
           uint16_t* pu = swe.gu + ft_offset(m, Nf + jb + lg * 16, 2 * Nf);
-          *reinterpret_cast<uint4*>(pg) = make_uint4(gw[0], gw[1], gw[2], gw[3]);
-          *reinterpret_cast<uint4*>(pg + 512) = make_uint4(gw[4], gw[5], gw[6], gw[7]);
-          *reinterpret_cast<uint4*>(pu) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-          *reinterpret_cast<uint4*>(pu + 512) = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+          store_codes<MX_NT_GU>(reinterpret_cast<uint8_t*>(pg), make_uint4(gw[0], gw[1], gw[2], gw[3]));
+          store_codes<MX_NT_GU>(reinterpret_cast<uint8_t*>(pg + 512), make_uint4(gw[4], gw[5], gw[6], gw[7]));
+          store_codes<MX_NT_GU>(reinterpret_cast<uint8_t*>(pu), make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          store_codes<MX_NT_GU>(reinterpret_cast<uint8_t*>(pu + 512), make_uint4(hw[4], hw[5], hw[6], hw[7]));
         }
         {
           const v16f d = lora_pi<R>(wg[b], xg[mt]);
