@@ -361,11 +361,13 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
     if not rows:
         raise SystemExit("no gemm_kernel dispatches in the PMC output")
     # algorithmic bytes of each shape: read both MX operands and their scales once, write the bf16 output,
-    # read the rank-r LoRA operands of the epilogue
+    # read the rank-r LoRA operands of the epilogue; the gate|up launch, with the SwiGLU forward in its epilogue,
+    # also reads xs and the LoRA-B / A_down rows and writes MX(h) (codes and scales) and the bf16 xS_down
     alg = {}
     for nm, (M, Nn, Kk, rr) in shapes.items():
         sc = lambda R, C: -(-R // 128) * (C // 128) * 512 // 4  # noqa: E731  (one scale per 32 along K)
         alg[nm] = M * Kk + Nn * Kk + sc(M, Kk) + sc(Nn, Kk) + M * Nn * 2 + (M + Nn) * rr * 2
+    alg["gate|up"] += T * 2 * r * 2 + 3 * N * r * 2 + T * N + sc(T, N) + T * r * 2
     per_launch = sum(x["fetch_bytes"] + x["write_bytes"] for x in rows) / len(rows)
     alg_mean = sum(alg.values()) / len(alg)
     summary = {"config": cfg, "kernel": "mx_gemm (gate|up, down, dh, dx)",
