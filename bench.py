@@ -131,7 +131,10 @@ def _time_graph(fn, min_ms=1.0, reps=5):
     with torch.cuda.graph(g):
         for _ in range(n):
             fn()
-    g.replay()
+    # untimed replays first (>= 10 ms), so the first entry timed in a process does not pay for the clock ramp
+    # from idle (measured: the first of several quantizer timings ran 2% slower than the same kernel later)
+    for _ in range(max(1, int(10.0 / max(one * n, 1e-3)) + 1)):
+        g.replay()
     torch.cuda.synchronize()
     ts = []
     for _ in range(reps):

@@ -216,3 +216,37 @@ def test_b_pi_layout_matches_row_order(M, N, K, layout, rank, gpu):
                       alpha=0.5, layout=3 | layout | _native.GEMM_B_PI, m=M)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_pi_order_weights_give_the_same_mlp_step(gpu):
+    """The _MLP step with the down, dhm and dx GEMMs on the pi_col-ordered weight copies (fused_mlp.B_PI, the
+    default) and on the row-order ones: the same products summed in the same order, stored in other pieces, so y,
+    dx and every LoRA gradient are bit-identical."""
+    import fused_linear
+    import fused_mlp
+    import workloads
+    model, inps = workloads.build_model(3, T=1500, device=gpu)
+    mxfp8.enable_mxfp8(model)
+    mod = model.layers[0].mlp
+    assert "_mx_wp_tl" in mod.down_proj.base_layer.__dict__ and hasattr(mod.gate_proj.base_layer._mx_gu[0], "wtp_tl")
+    out = []
+    try:
+        for pi in (False, True):
+            fused_mlp.B_PI[0] = pi
+            fused_linear.new_step()
+            for p in mod.parameters():
+                p.grad = None
+            x = inps[0]["x"].to(gpu).requires_grad_(True)
+            y = fused_mlp.mlp(mod, x)
+            y.backward(inps[0]["dy"].to(gpu))
+            torch.cuda.synchronize()
+            grads = {n: p.grad.detach().clone() for n, p in mod.named_parameters() if p.requires_grad}
+            out.append((y.detach().clone(), x.grad.detach().clone(), grads))
+    finally:
+        fused_mlp.B_PI[0] = True
+    (y0, dx0, g0), (y1, dx1, g1) = out
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(dx0.view(torch.int16), dx1.view(torch.int16))
+    assert g0.keys() == g1.keys() and len(g0) == 6
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
