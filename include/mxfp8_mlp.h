@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 8
+#define MXFP8_MLP_ABI_VERSION 9
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -269,6 +269,32 @@ int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q,
  * so the backward rebuilds it from the saved xs.  C in {16, 32, 64}.
  */
 int mxfp8_transpose_pad(const void* x, int64_t T, int64_t C, int64_t ld_x, void* out, int64_t Tpad, void* stream);
+
+/*
+ * One copy of mxfp8_pack_bf16: for r < rows, c < cols, dst[r * dst_ld + c] (transpose == 0) or
+ * dst[c * dst_ld + r] (transpose != 0) = bf16(src[r * src_ld + c]), rounded to nearest even (NaN stays NaN);
+ * src fp32 (src_f32 != 0) or bf16, or NULL for zeros.  dst is bf16.
+ */
+typedef struct {
+  const void* src;
+  int64_t src_ld;
+  int64_t src_f32;
+  int64_t rows, cols;
+  void* dst;
+  int64_t dst_ld;
+  int64_t transpose;
+} mxfp8_pack_job;
+
+#define MXFP8_PACK_MAX_JOBS 32
+
+/*
+ * The n_jobs copies of jobs[] (host memory, n_jobs <= MXFP8_PACK_MAX_JOBS) in ONE launch; the destinations of
+ * one call must not overlap.  Replaces the per-step bf16 casts and concatenations of the LoRA weights of a
+ * layer group (/root/reference/scripts/fused_linear.py:55-62, :88-101: B.to(dt), torch.cat of the A rows, and
+ * here also S zero-padded to the rank the kernels take, its transpose and the block-diagonal B of the group's
+ * one forward GEMM), which the reference makes with one torch operation each.
+ */
+int mxfp8_pack_bf16(const mxfp8_pack_job* jobs, int64_t n_jobs, void* stream);
 
 /*
  * The gate|up MX GEMM with the SwiGLU forward fused into its epilogue: one launch replacing

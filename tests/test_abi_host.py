@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 30, names
+    assert len(names) == 31, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -134,6 +134,13 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.mxfp8_quant_tiled(p, 4, 100, 100, p, p, None) == -1
     assert lib.mxfp8_tile_codes(p, 4, 96, 96, p, None) == -1
     assert lib.mxfp8_sum_parts(None, 1, 4, 1.0, p, 0, None) == -1
+    # bf16 pack: job count, a destination row shorter than the job's columns
+    jobs = (_native.PackJob * 2)(_native.PackJob(None, 0, 0, 4, 64, p, 64, 0),
+                                 _native.PackJob(p, 64, 1, 4, 64, p, 32, 0))
+    assert lib.mxfp8_pack_bf16(ctypes.cast(jobs, ctypes.c_void_p), 0, None) == -1
+    assert lib.mxfp8_pack_bf16(ctypes.cast(jobs, ctypes.c_void_p), 33, None) == -1
+    assert lib.mxfp8_pack_bf16(ctypes.cast(jobs, ctypes.c_void_p), 2, None) == -1
+    assert b"bad job 1" in lib.mxfp8_last_error()
 
 
 def test_gemm_workspace_plan(lib):

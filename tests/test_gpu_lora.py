@@ -254,3 +254,27 @@ def test_lora_bwd_codes_on_edge_blocks(mode, gpu):
     mx.quant_into(dy, qr, sr, off * 128, width // 128)
     assert torch.equal(s.cpu(), sr)
     assert torch.equal(q.cpu(), qr)
+
+
+def test_pack_bf16_matches_torch(gpu):
+    """mxfp8_pack_bf16 against torch: fp32 and bf16 sources (row-strided views too), straight and transposed
+    destinations, zero fills, and more jobs than one launch's table takes (two launches)."""
+    g = torch.Generator().manual_seed(3)
+    srcs = [(torch.randn(48, 256, generator=g) * 3).to(gpu),
+            torch.randn(16, 2048, generator=g).to(torch.bfloat16).to(gpu),
+            torch.randn(64, 96, generator=g).to(gpu)[:, 16:80],   # row stride 96
+            (torch.randn(3072, 16, generator=g) * 1e-3).to(gpu)]
+    srcs[0][0, :4] = torch.tensor([float("inf"), -float("inf"), 65504.0, 1e-40])
+    jobs, want = [], []
+    for k in range(12):  # 12 x 3 = 36 jobs
+        src = srcs[k % len(srcs)]
+        r, c = src.shape
+        straight = torch.full((r, c + 8), 7.0, dtype=torch.bfloat16, device=gpu)[:, :c]
+        trans = torch.full((c, r + 8), 7.0, dtype=torch.bfloat16, device=gpu)[:, :r]
+        zero = torch.full((r, c), 7.0, dtype=torch.bfloat16, device=gpu)
+        jobs += [(src, straight, False), (src, trans, True), (None, zero, False)]
+        want += [(straight, src.to(torch.bfloat16)), (trans, src.to(torch.bfloat16).t()), (zero, torch.zeros_like(zero))]
+    _native.pack_bf16(jobs)
+    torch.cuda.synchronize()
+    for got, ref in want:
+        assert torch.equal(got.view(torch.int16), ref.contiguous().view(torch.int16))

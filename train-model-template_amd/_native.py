@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT, GEMM_B_PI = 1, 2, 4, 8, 16  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -44,6 +44,7 @@ SIGNATURES = {
     "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_res_lora": [_ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _f32, _ptr, _ptr],
     "mxfp8_transpose_pad": [_ptr, _i64, _i64, _i64, _ptr, _i64],
+    "mxfp8_pack_bf16": [_ptr, _i64],
     "mxfp8_lora_tn_chunks": [_i64, _i64],
     "mxfp8_swiglu": [_ptr, _ptr, _i64, _ptr, _ptr],
     "mxfp8_swiglu_bwd": [_ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr],
@@ -290,6 +291,38 @@ def lora_tn(x, p, out, part, scale=1.0, transpose=False):
     chunks = part.numel() // (rp * K)
     call("mxfp8_lora_tn", _p(x), T, K, x.stride(0), _p(p), rp, chunks, _p(part), float(scale), int(transpose),
          int(out.dtype == torch.float32), _p(out), like=x)
+
+
+class PackJob(ctypes.Structure):
+    """mxfp8_pack_job of include/mxfp8_mlp.h."""
+    _fields_ = [("src", _ptr), ("src_ld", _i64), ("src_f32", _i64), ("rows", _i64), ("cols", _i64), ("dst", _ptr),
+                ("dst_ld", _i64), ("transpose", _i64)]
+
+
+PACK_MAX_JOBS = 32
+
+
+def pack_bf16(jobs):
+    """Run the bf16 copies `jobs` = [(src, dst, transpose)] in as few launches as the job table allows: src a 2-D
+    fp32 or bf16 tensor [rows, cols] with unit column stride, or None for zeros; dst a 2-D bf16 view, [rows, cols]
+    or, when transpose, [cols, rows], with unit column stride.  Destinations must not overlap."""
+    if not jobs:
+        return
+    like = jobs[0][1]
+    table = []
+    for src, dst, tr in jobs:
+        assert dst.dtype == torch.bfloat16 and dst.dim() == 2 and dst.stride(1) == 1, (dst.dtype, dst.shape)
+        rows, cols = (dst.shape[1], dst.shape[0]) if tr else tuple(dst.shape)
+        if src is not None:
+            assert src.dim() == 2 and src.stride(1) == 1 and tuple(src.shape) == (rows, cols), (src.shape, rows, cols)
+            assert src.dtype in (torch.float32, torch.bfloat16) and src.device == dst.device
+        table.append(PackJob(None if src is None else _p(src), 0 if src is None else src.stride(0),
+                             int(src is not None and src.dtype == torch.float32), rows, cols, _p(dst), dst.stride(0),
+                             int(bool(tr))))
+    for i in range(0, len(table), PACK_MAX_JOBS):
+        chunk = table[i:i + PACK_MAX_JOBS]
+        arr = (PackJob * len(chunk))(*chunk)
+        call("mxfp8_pack_bf16", ctypes.cast(arr, _ptr), len(chunk), like=like)
 
 
 def transpose_pad(x, out):

@@ -748,6 +748,64 @@ extern "C" int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg
   return MXFP8_OK;
 }
 
+namespace {
+
+// The job table of mxfp8_pack_bf16, by value; block b of the grid works on job j where first[j] <= b < first[j + 1],
+// 256 threads x 4 elements of that job (row-major over the job's rows x cols).
+struct PackArgs {
+  mxfp8_pack_job job[MXFP8_PACK_MAX_JOBS];
+  int first[MXFP8_PACK_MAX_JOBS + 1];
+  int n;
+};
+
+__global__ __launch_bounds__(256) void pack_kernel(const PackArgs a) {
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
+  const mxfp8_pack_job& jb = a.job[j];
+  const int64_t n = jb.rows * jb.cols;
+  const int64_t e0 = ((int64_t)(b - a.first[j]) * 256 + threadIdx.x) * 4;
+  uint16_t* dst = static_cast<uint16_t*>(jb.dst);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t e = e0 + u;
+    if (e >= n) break;
+    const int64_t r = e / jb.cols, c = e % jb.cols;
+    uint16_t v = 0;
+    if (jb.src) {
+      v = jb.src_f32 ? (uint16_t)f32_to_bf16_bits(static_cast<const float*>(jb.src)[r * jb.src_ld + c])
+                     : static_cast<const uint16_t*>(jb.src)[r * jb.src_ld + c];
+    }
+    dst[jb.transpose ? c * jb.dst_ld + r : r * jb.dst_ld + c] = v;
+  }
+}
+
+}  // namespace
+
+extern "C" int mxfp8_pack_bf16(const mxfp8_pack_job* jobs, int64_t n_jobs, void* stream) {
+  MX_CHECK_ARG(jobs && n_jobs > 0 && n_jobs <= MXFP8_PACK_MAX_JOBS, "mxfp8_pack_bf16: need 1..%d jobs",
+               MXFP8_PACK_MAX_JOBS);
+  PackArgs a{};
+  int64_t blocks = 0;
+  for (int64_t j = 0; j < n_jobs; ++j) {
+    const mxfp8_pack_job& jb = jobs[j];
+    MX_CHECK_ARG(jb.dst && jb.rows >= 0 && jb.cols > 0 && jb.dst_ld >= (jb.transpose ? jb.rows : jb.cols) &&
+                     (!jb.src || jb.src_ld >= jb.cols),
+                 "mxfp8_pack_bf16: bad job %lld (rows=%lld cols=%lld src_ld=%lld dst_ld=%lld)", (long long)j,
+                 (long long)jb.rows, (long long)jb.cols, (long long)jb.src_ld, (long long)jb.dst_ld);
+    a.job[j] = jb;
+    a.first[j] = (int)blocks;
+    blocks += (jb.rows * jb.cols + 1023) / 1024;
+    MX_CHECK_ARG(blocks < (1LL << 30), "mxfp8_pack_bf16: too large");
+  }
+  a.first[n_jobs] = (int)blocks;
+  a.n = (int)n_jobs;
+  if (blocks == 0) return MXFP8_OK;
+  pack_kernel<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(a);
+  MX_CHECK_LAUNCH("mxfp8_pack_bf16");
+  return MXFP8_OK;
+}
+
 extern "C" int mxfp8_transpose_pad(const void* x, int64_t T, int64_t C, int64_t ld_x, void* out, int64_t Tpad,
                                    void* stream) {
   MX_CHECK_ARG(x && out, "mxfp8_transpose_pad: null pointer");

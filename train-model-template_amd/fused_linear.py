@@ -17,11 +17,14 @@ Layers that cannot be grouped (trainable base weights, DoRA, dropout > 0, severa
 `_part`, `_cast` / `new_step` and `STATS` are also what the fused MLP path reads.
 """
 import dataclasses
+import os
 
 import torch
 from torch import nn
 
 _THIN = 64  # a plain frozen Linear with at most this many outputs joins the thin product (in_proj_b/a: 16)
+# the per-step bf16 weight forms of a group from one mxfp8_pack_bf16 launch (False: one torch operation each)
+PACK_FORMS = [os.environ.get("MXFP8_PACK_FORMS", "1") != "0"]
 STATS = {"gộp": 0, "gọi thẳng": 0}  # path counters, the reference's keys (grouped / called directly)
 
 
@@ -140,7 +143,62 @@ def _s_pad(S, key, rp):
     return _cast(key + ("pad", rp), lambda: torch.cat([S, S.new_zeros(rp - S.shape[0], S.shape[1])]))
 
 
-def _thin_product(x2, S, skey, width, dt):
+def _group_forms(spec, skey, K, dev):
+    """Every per-step bf16 form of the group's weights from ONE launch (mxfp8_pack_bf16), cached per step under
+    skey: S_pad [rp, K] (the A rows and thin weights in column order, zero rows up to rp = _rp(width)), St =
+    S_padᵀ [K, rp] (the backward's dS·S operand), each adapter's B [n, r] in Bs, and Q [Σ n, rp] with the MX
+    layers' B placed block-diagonally at their S columns (the merged forward GEMM's epilogue operand; None
+    for fewer than two MX layers).  The torch path builds these with one operation each."""
+    def make():
+        import types
+
+        import _native
+        rp, width = _rp(spec.width), spec.width
+        a8 = lambda n: _cdiv(n, 8) * 8  # noqa: E731  (16-byte aligned views)
+        sizes = [rp * K, K * rp] + [spec.parts[sl.layer][2].shape[0] * sl.width for sl in spec.adapters]
+        n_q = sum(spec.parts[i][0].out_features for i in spec.mx) if len(spec.mx) >= 2 else 0
+        sizes.append(n_q * rp)
+        buf = torch.empty(sum(a8(n) for n in sizes), dtype=torch.bfloat16, device=dev)
+        views, off = [], 0
+        for n in sizes:
+            views.append(buf[off:off + n])
+            off += a8(n)
+        S_pad, St = views[0].view(rp, K), views[1].view(K, rp)
+        Bs = [v.view(-1, sl.width) for v, sl in zip(views[2:-1], spec.adapters)]
+        Q = views[-1].view(n_q, rp) if n_q else None
+        jobs = []
+        for sl, src in zip(spec.adapters + spec.thin, spec.s_sources()):
+            jobs += [(src.detach(), S_pad[sl.cols], False), (src.detach(), St[:, sl.cols], True)]
+        if rp > width:
+            jobs += [(None, S_pad[width:], False), (None, St[:, width:], True)]
+        for sl, b in zip(spec.adapters, Bs):
+            jobs.append((spec.parts[sl.layer][2].detach(), b, False))
+        row = 0
+        for i in (spec.mx if n_q else ()):
+            n, sl = spec.parts[i][0].out_features, spec.adapter(i)
+            if sl is None:
+                jobs.append((None, Q[row:row + n], False))
+            else:
+                if sl.col:
+                    jobs.append((None, Q[row:row + n, :sl.col], False))
+                jobs.append((spec.parts[i][2].detach(), Q[row:row + n, sl.cols], False))
+                if sl.col + sl.width < rp:
+                    jobs.append((None, Q[row:row + n, sl.col + sl.width:], False))
+            row += n
+        _native.pack_bf16(jobs)
+        return types.SimpleNamespace(S_pad=S_pad, S=S_pad[:width], St=St, Bs=Bs, Q=Q, rp=rp)
+    return _cast(skey + ("forms",), make)
+
+
+def _packable(spec, x2, dt):
+    """The per-step weight forms come from one mxfp8_pack_bf16 launch: the native thin product applies and every
+    source is fp32 or bf16."""
+    return (PACK_FORMS[0] and bool(spec.adapters or spec.thin) and _native_ok(x2, dt, spec.width)
+            and all(t.dtype in (torch.float32, torch.bfloat16) for t in spec.s_sources())
+            and all(spec.parts[sl.layer][2].dtype in (torch.float32, torch.bfloat16) for sl in spec.adapters))
+
+
+def _thin_product(x2, S, skey, width, dt, S_pad=None):
     """bf16(x2 · Sᵀ): one read of x2 on the library's rank-r kernel (S zero-padded to 16/32/64 rows, so xS has
     zero columns past `width`) when it applies, else a torch GEMM."""
     if not _native_ok(x2, dt, width):
@@ -148,7 +206,7 @@ def _thin_product(x2, S, skey, width, dt):
     import _native
     rp = _rp(width)
     xS = torch.empty((x2.shape[0], rp), dtype=dt, device=x2.device)
-    _native.lora_nt(x2, _s_pad(S, skey, rp), xS)
+    _native.lora_nt(x2, _s_pad(S, skey, rp) if S_pad is None else S_pad, xS)
     return xS
 
 
@@ -196,7 +254,11 @@ def _fwd_merged(spec, Bs, xS, codes, T, dt, skey):
             row += n
         return Q
 
-    Q = _cast(skey + ("qcat", tuple(spec.mx), rp), block_diagonal_b)
+    forms = _CAST.get(skey + ("forms",))
+    if forms is not None and forms.Q is not None and forms.rp == rp:
+        Q = forms.Q
+    else:
+        Q = _cast(skey + ("qcat", tuple(spec.mx), rp), block_diagonal_b)
     outs = [torch.empty((T, n), dtype=dt, device=xS.device) for n in widths]
     mxfp8.mx_mm_seg(codes[0], codes[1], op[0], op[1], outs, lora=(xS, Q), alpha=alpha, layout=3, m=T)
     return dict(zip(spec.mx, outs))
@@ -243,12 +305,17 @@ class _Group(torch.autograd.Function):
         if x2.dtype != dt or not x2.is_contiguous():
             x2 = x2.to(dt).contiguous()
         spec = _Spec(parts)
-        Bs = [_cast((id(parts[sl.layer][2]), dt), lambda B=parts[sl.layer][2]: B.detach().to(dt))
-              for sl in spec.adapters]
         src = spec.s_sources()
         skey = (tuple(id(t) for t in src), dt)
-        S = _cast(skey, lambda: torch.cat([t.detach().to(dt) for t in src])) if src else None
-        xS = _thin_product(x2, S, skey, spec.width, dt) if src else None
+        if _packable(spec, x2, dt):
+            forms = _group_forms(spec, skey, K, x2.device)
+            Bs, S = forms.Bs, forms.S
+            xS = _thin_product(x2, S, skey, spec.width, dt, S_pad=forms.S_pad)
+        else:
+            Bs = [_cast((id(parts[sl.layer][2]), dt), lambda B=parts[sl.layer][2]: B.detach().to(dt))
+                  for sl in spec.adapters]
+            S = _cast(skey, lambda: torch.cat([t.detach().to(dt) for t in src])) if src else None
+            xS = _thin_product(x2, S, skey, spec.width, dt) if src else None
         if need_out:
             outs = _forward_outputs(spec, x2, xS, Bs, skey, defer, dt)
         else:  # only the graph for backward is needed (x2, xS saved); nobody reads the outputs
@@ -404,7 +471,11 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
         codes = (q, sbuf.view(mxfp8.E8))
         if native:
             # bf16(bf16(MX GEMM) + dS·S): the reference's dx.addmm_(dS, S) in the GEMM epilogue
-            St = _cast(skey + ("padT", width), lambda: _s_pad(S, skey, width).t().contiguous())
+            forms = _CAST.get(skey + ("forms",))
+            if forms is not None and forms.rp == width:
+                St = forms.St
+            else:
+                St = _cast(skey + ("padT", width), lambda: _s_pad(S, skey, width).t().contiguous())
             dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=(dS, St), alpha=1.0)
         else:
             dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay)
@@ -416,9 +487,12 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
     if spec.adapters:
         if native:
             import _native
-            dA = torch.empty((width, K), dtype=dt, device=dev)
+            # bf16(dSᵀ·x2), held in fp32 when every A is an fp32 parameter: autograd would cast each bf16 slice
+            # to its parameter's dtype anyway (exactly), one kernel per adapter
+            a32 = all(spec.parts[sl.layer][1].dtype == torch.float32 for sl in spec.adapters)
+            dA = torch.empty((width, K), dtype=torch.float32 if a32 else dt, device=dev)
             part = torch.empty(_native.lora_tn_chunks(T, K) * width * K, dtype=torch.float32, device=dev)
-            _native.lora_tn(x2, dS, dA, part)  # bf16(dSᵀ·x2)
+            _native.lora_tn(x2, dS, dA, part)
         else:
             dA = dS[:, :spec.adapter_cols].t() @ x2
         for sl in spec.adapters:
