@@ -219,7 +219,7 @@ int mxfp8_lora_nt(const void* x, int64_t T, int64_t K, int64_t ld_x, const void*
  * layout, ceil(T/16)*16 rows; scales s blocked with K/128 tiles per row, padded rows 0) and
  * mxfp8_lora_nt(x, w, rp, scale, out, outT, Tpad) (out [T, rp] bf16, outT [rp, Tpad] or NULL).  Replaces
  * mx_quant(x2) followed by xs = x2 @ S.t() (/root/reference/scripts/fused_mlp.py:277-279), and mx_quant(dy2)
- * with dxd = (dy2 @ bd).mul_(s_d) (:309-313), each reading the activation once.  K % 128 == 0, rp in {16, 32},
+ * with dxd = (dy2 @ bd).mul_(s_d) (:309-313), each reading the activation once.  K % 128 == 0, rp in {16, 32, 64},
  * Tpad = ceil(T/128)*128.
  */
 int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w, int64_t rp,

@@ -97,7 +97,7 @@ def test_argument_checks_reject_before_launch(lib):
     assert lib.mxfp8_lora_nt(p, 4, 256, 256, p, 8, 1.0, p, None, 0, None) == -1
     # fused quantizer + rank-r product: K % 128, rp in {16, 32}, Tpad = ceil(T/128)*128
     assert lib.mxfp8_quant_lora(p, 4, 200, 200, p, p, p, 16, 1.0, p, None, 128, None) == -1
-    assert lib.mxfp8_quant_lora(p, 4, 256, 256, p, p, p, 64, 1.0, p, None, 128, None) == -1
+    assert lib.mxfp8_quant_lora(p, 4, 256, 256, p, p, p, 48, 1.0, p, None, 128, None) == -1
     assert lib.mxfp8_quant_lora(p, 4, 256, 256, p, p, p, 16, 1.0, p, None, 256, None) == -1
     assert b"Tpad" in lib.mxfp8_last_error()
     assert lib.mxfp8_lora_tn(p, 4, 96, 96, p, 16, 1, ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), 1.0, 0, 0, p,

@@ -118,7 +118,8 @@ def test_bwd_finish_matches_reference_reduction(gpu):
 
 
 @pytest.mark.parametrize("T,K,rp,scale", [(300, 1024, 32, 1.0), (4096, 2048, 16, 2.0), (1, 128, 16, 1.0),
-                                          (8896, 2048, 32, 1.0), (520, 1280, 32, 1.0), (130, 3072, 16, 2.0)])
+                                          (8896, 2048, 32, 1.0), (520, 1280, 32, 1.0), (130, 3072, 16, 2.0),
+                                          (1100, 2048, 64, 1.0), (130, 3072, 64, 2.0), (1, 128, 64, 1.0)])
 def test_quant_lora_matches_quantizer_and_product(T, K, rp, scale, gpu):
     # one read of x: codes and scales bit-identical to mxfp8_quant_tiled; out / outT as lora_nt's contract
     import mxfp8

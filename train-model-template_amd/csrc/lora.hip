@@ -160,9 +160,10 @@ __global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X,
 // ------------------------------------------------------------- MX quantization fused with x · Wᵀ
 // One pass over X [T, K] bf16 giving both its MX operand (codes in the MX-tiled layout and blocked scales:
 // the bytes of mxfp8_quant_tiled) and out = bf16(X · Wᵀ) (then bf16(· scale) when scale != 1), W [RP, K]
-// bf16, RP in {16, 32}, with the zero-padded transposed copy outT.  Grid: Tpad / 32 row blocks (Tpad =
+// bf16, RP in {16, 32, 64}, with the zero-padded transposed copy outT.  Grid: Tpad / 32 row blocks (Tpad =
 // ceil(T/128)*128, so the padded rows of the last scale tiles get scale 0), 4 waves.  The workgroup streams K
-// in 128-column tiles through a 4-stage LDS ring (the X tile and the W tile, 32 rows x 256 B each) filled by
+// in 128-column tiles through an LDS ring (4 stages; 3 at RP = 64) of the X tile (32 rows x 256 B) and the W
+// tile (32 rows, 64 at RP = 64) filled by
 // global_load_lds_dwordx4: lane i of a DMA takes row 4j + i/16 and the 16-byte chunk (i%16) ^ (row%16) of that
 // row's tile piece, so a DMA reads four whole 256-byte row pieces and the LDS reads below, 16 rows at a time at
 // one logical chunk, hit 16 distinct chunk positions.  Wave w takes columns 32w..32w+31 of each tile: lane l
@@ -176,9 +177,12 @@ __global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restr
                                                          uint8_t* __restrict__ s, float scale,
                                                          uint16_t* __restrict__ out, uint16_t* __restrict__ outT,
                                                          int Tpad) {
-  constexpr int kStages = 4, kTileB = 32 * 256, kStageB = 2 * kTileB;
+  // RP = 64: a 16 KB W tile, so 3 stages (72 KB) keep two workgroups on a CU, and a second accumulator for
+  // W rows 32..63
+  constexpr int kStages = RP > 32 ? 3 : 4, kTileB = 32 * 256, kStageB = kTileB + (RP > 32 ? 2 : 1) * kTileB;
   constexpr int kWDma = RP / 16;      // W DMAs per wave (RP rows x 256 B = RP / 4 KB per stage)
   constexpr int kDma = 2 + kWDma;     // X DMAs: 8 KB per stage, two per wave
+  constexpr int kAcc = RP > 32 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int r0 = blockIdx.x * 32, nt = K / 128;
@@ -210,7 +214,9 @@ __global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restr
   const int mc = live ? m : T - 1;
   const int cx = 4 * w + 2 * lg;  // the lane's first logical 16-byte chunk of a tile row
   const int sx0 = ((cx ^ (row & 15)) << 4), sx1 = (((cx + 1) ^ (row & 15)) << 4);
-  v16f acc = v16f{};
+  v16f acc[kAcc];
+#pragma unroll
+  for (int h = 0; h < kAcc; ++h) acc[h] = v16f{};
   // Stages past the end re-load the last tile into the slot just consumed (no later step reads it).  The memory
   // counter also counts this lane's stores (one code store and one scale store per tile), in issue order.  Behind
   // tile t's DMAs come the (kStages - 2) later tiles' DMAs and, from step kStages - 1 on, the stores of the last
@@ -229,24 +235,32 @@ __global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restr
     const uint8_t* st = lds + slot * kStageB;
     const uint4 a = *reinterpret_cast<const uint4*>(st + row * 256 + sx0);
     const uint4 b = *reinterpret_cast<const uint4*>(st + row * 256 + sx1);
-    const uint4 wa = *reinterpret_cast<const uint4*>(st + kTileB + row * 256 + sx0);
-    const uint4 wb = *reinterpret_cast<const uint4*>(st + kTileB + row * 256 + sx1);
     const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     quant16(v, lane, m, live, q, mc, K, true, (int64_t)t * 128 + 32 * w + 16 * lg, s, K / 128);
-    // D[ρ][t] += W[ρ, cols] · X[t, cols] over the lane pair's 32 columns (rows ρ >= RP of the W tile: zero)
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row < RP ? as_bf8(wa) : v8bf{}, as_bf8(a), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(row < RP ? as_bf8(wb) : v8bf{}, as_bf8(b), acc, 0, 0, 0);
+    // D[ρ][t] += W[ρ, cols] · X[t, cols] over the lane pair's 32 columns (rows ρ >= RP of the W tile: zero); W row
+    // 32h + row has the swizzle of row (same row % 16)
+#pragma unroll
+    for (int h = 0; h < kAcc; ++h) {
+      const uint4 wa = *reinterpret_cast<const uint4*>(st + kTileB + (32 * h + row) * 256 + sx0);
+      const uint4 wb = *reinterpret_cast<const uint4*>(st + kTileB + (32 * h + row) * 256 + sx1);
+      const bool wl = 32 * h + row < RP;
+      acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl ? as_bf8(wa) : v8bf{}, as_bf8(a), acc[h], 0, 0, 0);
+      acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl ? as_bf8(wb) : v8bf{}, as_bf8(b), acc[h], 0, 0, 0);
+    }
     slot = slot + 1 == kStages ? 0 : slot + 1;
   }
   wait_vmcnt<0>();       // the tail's repeated DMAs have landed: the ring can be reused
   __syncthreads();
   float(*red)[32][RP + 1] = reinterpret_cast<float(*)[32][RP + 1]>(lds);  // [4 waves][32 rows t][RP]
-  // acc lane l: t = l % 32, ρ = (i/4)*8 + (l/32)*4 + i%4
+  static_assert(4 * 32 * (RP + 1) * 4 <= kStages * kStageB, "reduction tile inside the ring");
+  // acc[h] lane l: t = l % 32, ρ = 32 h + (i/4)*8 + (l/32)*4 + i%4
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int rho = (i >> 2) * 8 + lg * 4 + (i & 3);
-    if (rho < RP) red[w][row][rho] = acc[i];
-  }
+  for (int h = 0; h < kAcc; ++h)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rho = 32 * h + (i >> 2) * 8 + lg * 4 + (i & 3);
+      if (rho < RP) red[w][row][rho] = acc[h][i];
+    }
   __syncthreads();
   for (int idx = threadIdx.x; idx < 32 * RP; idx += 256) {
     const int tt = idx / RP, rho = idx % RP;
@@ -982,8 +996,8 @@ extern "C" int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part
 extern "C" int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w,
                                 int64_t rp, float scale, void* out, void* outT, int64_t Tpad, void* stream) {
   MX_CHECK_ARG(x && q && s && w && out, "mxfp8_quant_lora: null pointer");
-  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32),
-               "mxfp8_quant_lora: need K %% 128 == 0, rp in {16, 32}");
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
+               "mxfp8_quant_lora: need K %% 128 == 0, rp in {16, 32, 64}");
   MX_CHECK_ARG(Tpad == (T + 127) / 128 * 128, "mxfp8_quant_lora: Tpad must be ceil(T / 128) * 128");
   MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(w, 16) && mx_aligned(q, 16) && mx_aligned(s, 16),
                "mxfp8_quant_lora: misaligned buffer");
@@ -993,7 +1007,8 @@ extern "C" int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_
 #define QL_ARGS (const uint16_t*)x, ld_x, (int)T, (int)K, (const uint16_t*)w, (uint8_t*)q, (uint8_t*)s, scale, \
                 (uint16_t*)out, (uint16_t*)outT, (int)Tpad
   if (rp == 16) quant_lora_kernel<16><<<grid, 256, 0, stm>>>(QL_ARGS);
-  else quant_lora_kernel<32><<<grid, 256, 0, stm>>>(QL_ARGS);
+  else if (rp == 32) quant_lora_kernel<32><<<grid, 256, 0, stm>>>(QL_ARGS);
+  else quant_lora_kernel<64><<<grid, 256, 0, stm>>>(QL_ARGS);
 #undef QL_ARGS
   MX_CHECK_LAUNCH("mxfp8_quant_lora");
   return MXFP8_OK;

@@ -264,14 +264,15 @@ def _fwd_merged(spec, Bs, xS, codes, T, dt, skey):
     return dict(zip(spec.mx, outs))
 
 
-def _forward_outputs(spec, x2, xS, Bs, skey, defer, dt):
-    """Every non-thin output of the group (fused_linear.py:104-117)."""
+def _forward_outputs(spec, x2, xS, Bs, skey, defer, dt, codes=None):
+    """Every non-thin output of the group (fused_linear.py:104-117); codes: the MX-tiled codes of x2 when the
+    caller already has them."""
     T = x2.shape[0]
     outs = [None] * len(spec.parts)
-    codes = None
     if spec.mx and T:
         import mxfp8
-        codes = mxfp8.mx_quant_tiled(x2)  # once for the whole group
+        if codes is None:
+            codes = mxfp8.mx_quant_tiled(x2)  # once for the whole group
         if defer is None and dt == torch.bfloat16:
             for i, y in (_fwd_merged(spec, Bs, xS, codes, T, dt, skey) or {}).items():
                 outs[i] = y
@@ -307,17 +308,26 @@ class _Group(torch.autograd.Function):
         spec = _Spec(parts)
         src = spec.s_sources()
         skey = (tuple(id(t) for t in src), dt)
+        codes = None
         if _packable(spec, x2, dt):
             forms = _group_forms(spec, skey, K, x2.device)
             Bs, S = forms.Bs, forms.S
-            xS = _thin_product(x2, S, skey, spec.width, dt, S_pad=forms.S_pad)
+            if spec.mx:
+                # one read of x2 for both the MX layers' codes and xS (mxfp8_quant_lora); also when the outputs
+                # are not needed (a checkpoint's recompute), so xS, which backward reads, has the same bits in
+                # both modes
+                import mxfp8
+                q, sc, xS, _ = mxfp8.mx_quant_lora(x2, forms.S_pad, out_t=False)
+                codes = (q, sc) if need_out else None
+            else:
+                xS = _thin_product(x2, S, skey, spec.width, dt, S_pad=forms.S_pad)
         else:
             Bs = [_cast((id(parts[sl.layer][2]), dt), lambda B=parts[sl.layer][2]: B.detach().to(dt))
                   for sl in spec.adapters]
             S = _cast(skey, lambda: torch.cat([t.detach().to(dt) for t in src])) if src else None
             xS = _thin_product(x2, S, skey, spec.width, dt) if src else None
         if need_out:
-            outs = _forward_outputs(spec, x2, xS, Bs, skey, defer, dt)
+            outs = _forward_outputs(spec, x2, xS, Bs, skey, defer, dt, codes)
         else:  # only the graph for backward is needed (x2, xS saved); nobody reads the outputs
             STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
             outs = [None if i in spec.thin_ids else x2.new_empty(x2.shape[0], p[0].out_features)

@@ -75,7 +75,7 @@ def mx_quant_tiled(x2d):
 
 def mx_quant_lora(x2d, w, scale=1.0, out_t=True):
     """mx_quant_tiled(x2d) and bf16(x2d · wᵀ) (then bf16(· scale)) from one read of x2d, w [rp, K] bf16 with
-    rp in {16, 32}: -> (q, s, out [R, rp], outT [rp, ceil(R/128)*128] zero-padded, or None)."""
+    rp in {16, 32, 64}: -> (q, s, out [R, rp], outT [rp, ceil(R/128)*128] zero-padded, or None)."""
     R, K = x2d.shape
     assert x2d.dtype == torch.bfloat16 and x2d.stride(1) == 1 and K % 128 == 0 and R > 0, (x2d.dtype, x2d.shape)
     rp = w.shape[0]
