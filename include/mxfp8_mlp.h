@@ -263,6 +263,41 @@ int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_dy, void* q,
                    float scale, void* dxa, int64_t ld_dxa, float* db, float* part_dxa, float* part_db, void* stream);
 
 /*
+ * One layer of mxfp8_lora_bwd_batch: dy [T, N] bf16 (row stride ld_dy), its codes at column tile col_tile_off of the
+ * batch's code buffer, xa [T, r] (row stride ld_xa), B [N, r], scale, and the outputs and scratch of
+ * mxfp8_lora_bwd: dxa [T, r] bf16 (row stride ld_dxa), db [N, r] fp32, part_dxa (N/128) * T * r floats, part_db
+ * mxfp8_lora_bwd_batch_chunks(T, ΣN) * N * r floats.
+ */
+typedef struct {
+  const void* dy;
+  int64_t N, ld_dy, col_tile_off;
+  const void* xa;
+  int64_t ld_xa;
+  const void* b;
+  float scale;
+  void* dxa;
+  int64_t ld_dxa;
+  float* db;
+  float* part_dxa;
+  float* part_db;
+} mxfp8_lora_bwd_job;
+
+#define MXFP8_LORA_BWD_MAX_JOBS 8
+
+/* Row chunks of every job of mxfp8_lora_bwd_batch for T tokens and ΣN columns over the jobs; 0 if invalid. */
+int64_t mxfp8_lora_bwd_batch_chunks(int64_t T, int64_t n_total);
+
+/*
+ * mxfp8_lora_bwd of every layer of a group in one launch, plus one launch of their partial sums: the layers'
+ * dy stream side by side, with one row chunking for all (mxfp8_lora_bwd_batch_chunks(T, ΣN)).  q / s (or NULL)
+ * as in mxfp8_lora_bwd, shared by the jobs.  Replaces the per-layer lora_bwd calls of the grouped backward
+ * (/root/reference/scripts/fused_linear.py:219-259).  n_jobs <= MXFP8_LORA_BWD_MAX_JOBS, r in {16, 32}.
+ * d(xa) is the same bits as mxfp8_lora_bwd's; dB is summed over other row chunks (fp32 rounding).
+ */
+int mxfp8_lora_bwd_batch(const mxfp8_lora_bwd_job* jobs, int64_t n_jobs, int64_t T, int64_t r, void* q, int64_t ld_q,
+                         void* s, int64_t s_col_tiles, void* stream);
+
+/*
  * out [C, Tpad] bf16 = xᵀ of x [T, C] bf16 (row stride ld_x, 16-byte aligned rows), zero in columns T..Tpad-1.
  * No counterpart in the reference, which saves xs = x·Sᵀ for the backward (/root/reference/scripts/
  * fused_mlp.py:291) and reads it row-wise: here the backward kernel takes xsᵀ as a matrix-instruction operand,

@@ -279,3 +279,38 @@ def test_pack_bf16_matches_torch(gpu):
     torch.cuda.synchronize()
     for got, ref in want:
         assert torch.equal(got.view(torch.int16), ref.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("T,Ns,R,with_q", [(1000, (2048, 512, 512), 16, True), (300, (128, 256), 32, True),
+                                           (777, (512, 384, 128), 16, False)])
+def test_lora_bwd_batch_matches_per_layer(T, Ns, R, with_q, gpu):
+    """mxfp8_lora_bwd_batch (the layers of a group in one launch) against mxfp8_lora_bwd per layer: codes, scales
+    and d(xa) bit-identical (same products, same column-chunk order), dB within fp32 rounding (other row chunks)."""
+    import mxfp8
+    g = torch.Generator().manual_seed(T + sum(Ns) + R)
+    dys = [(torch.randn(T, n, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for n in Ns]
+    xas = [(torch.randn(T, R, generator=g)).to(torch.bfloat16).to(gpu) for _ in Ns]
+    Bs = [(torch.randn(n, R, generator=g) * 0.05).to(torch.bfloat16).to(gpu) for n in Ns]
+    scales = [2.0, 0.5, 1.0][:len(Ns)]
+    n_tot = sum(Ns)
+    offs = [sum(Ns[:k]) // 128 for k in range(len(Ns))]
+    out = []
+    for batched in (False, True):
+        q = torch.full((T, n_tot), 0x55, dtype=torch.uint8, device=gpu).view(mxfp8.F8) if with_q else None
+        s = torch.full((mxfp8.scale_numel(T, n_tot),), 0x55, dtype=torch.uint8, device=gpu) if with_q else None
+        dxas = [torch.full((T, R), 3.0, dtype=torch.bfloat16, device=gpu) for _ in Ns]
+        if batched:
+            dbs = mxfp8.lora_bwd_batch(dys, xas, Bs, scales, dxas, q=q, s=s, col_tile_offs=offs)
+        else:
+            dbs = [mxfp8.lora_bwd(dy, xa, B, sc, q=q, s=s, col_tile_off=off, dxa_out=dxa)
+                   for dy, xa, B, sc, dxa, off in zip(dys, xas, Bs, scales, dxas, offs)]
+        torch.cuda.synchronize()
+        out.append((q, s, dxas, dbs))
+    (q0, s0, dx0, db0), (q1, s1, dx1, db1) = out
+    if with_q:
+        assert torch.equal(q0.view(torch.uint8), q1.view(torch.uint8)) and torch.equal(s0, s1)
+    for a, b in zip(dx0, dx1):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    for a, b in zip(db0, db1):
+        err = ((a.double() - b.double()).abs().max() / b.double().abs().max()).item()
+        assert err <= 1e-5, err

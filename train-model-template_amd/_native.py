@@ -51,6 +51,8 @@ SIGNATURES = {
     "mxfp8_lora_bwd_chunks": [_i64, _i64],
     "mxfp8_lora_bwd": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _i64,
                        _ptr, _ptr, _ptr],
+    "mxfp8_lora_bwd_batch_chunks": [_i64, _i64],
+    "mxfp8_lora_bwd_batch": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr],
     "mxfp8_lora_tn_noalloc_chunks": [_i64, _i64, _i64],
@@ -59,7 +61,7 @@ SIGNATURES = {
 }
 
 _RESTYPES = {"mxfp8_last_error": ctypes.c_char_p, "mxfp8_gemm_workspace_size": _i64, "mxfp8_mlp_fwd_groups": _i64,
-             "mxfp8_lora_tn_chunks": _i64, "mxfp8_lora_bwd_chunks": _i64,
+             "mxfp8_lora_tn_chunks": _i64, "mxfp8_lora_bwd_chunks": _i64, "mxfp8_lora_bwd_batch_chunks": _i64,
              "mxfp8_lora_tn_noalloc_chunks": _i64}
 
 _lib = None
@@ -291,6 +293,32 @@ def lora_tn(x, p, out, part, scale=1.0, transpose=False):
     chunks = part.numel() // (rp * K)
     call("mxfp8_lora_tn", _p(x), T, K, x.stride(0), _p(p), rp, chunks, _p(part), float(scale), int(transpose),
          int(out.dtype == torch.float32), _p(out), like=x)
+
+
+class LoraBwdJob(ctypes.Structure):
+    """mxfp8_lora_bwd_job of include/mxfp8_mlp.h."""
+    _fields_ = [("dy", _ptr), ("N", _i64), ("ld_dy", _i64), ("col_tile_off", _i64), ("xa", _ptr), ("ld_xa", _i64),
+                ("b", _ptr), ("scale", _f32), ("dxa", _ptr), ("ld_dxa", _i64), ("db", _ptr), ("part_dxa", _ptr),
+                ("part_db", _ptr)]
+
+
+LORA_BWD_MAX_JOBS = 8
+
+
+def lora_bwd_batch_chunks(T, n_total):
+    return int(load().mxfp8_lora_bwd_batch_chunks(T, n_total))
+
+
+def lora_bwd_batch(jobs, T, r, q, s):
+    """jobs: [(dy, col_tile_off, xa, B, scale, dxa, db, part_dxa, part_db)] tensors as for lora_bwd; q [T, ΣN]
+    uint8 codes and s its scales, or None."""
+    table = [LoraBwdJob(_p(dy), dy.shape[1], dy.stride(0), off, _p(xa), xa.stride(0), _p(B), float(sc), _p(dxa),
+                        dxa.stride(0), _p(db), _p(pdx), _p(pdb))
+             for dy, off, xa, B, sc, dxa, db, pdx, pdb in jobs]
+    arr = (LoraBwdJob * len(table))(*table)
+    call("mxfp8_lora_bwd_batch", ctypes.cast(arr, _ptr), len(table), T, r, _p(q) if q is not None else None,
+         q.stride(0) if q is not None else 0, _p(s) if s is not None else None,
+         q.shape[1] // 128 if q is not None else 0, like=jobs[0][0])
 
 
 class PackJob(ctypes.Structure):

@@ -341,14 +341,16 @@ __global__ __launch_bounds__(256) void res_lora_kernel(const uint16_t* __restric
 // once).  For dB each group's 32 x 32 tile goes through a second per-wave tile and is read back transposed
 // (ds_read_b64_tr_b16), with xa, also staged per wave, read transposed: 16x16x32 MFMAs accumulate dB in registers
 // over the wave's blocks; the four waves' dB are added in LDS in a fixed order at the end.
+// The body takes its row chunk bx, column block by and the column block count ny as arguments (blockIdx.x,
+// blockIdx.y and gridDim.y of lora_bwd_kernel; a job's share of the flat grid of lora_bwd_batch_kernel).
 template <int R, bool kQuant, bool kLora>
-__global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __restrict__ dy, int64_t ld_dy, int T,
-                                                          int N, int Tpad, int chunk, uint8_t* __restrict__ q,
-                                                          int64_t ld_q, uint8_t* __restrict__ s, int64_t s_col_tiles,
-                                                          int col_tile_off, const uint16_t* __restrict__ xa,
-                                                          int64_t ld_xa, const uint16_t* __restrict__ B,
-                                                          float* __restrict__ part_dxa, float* __restrict__ part_db,
-                                                          uint16_t* __restrict__ dxa, int64_t ld_dxa, float scale) {
+__device__ __forceinline__ void lora_bwd_body(const uint16_t* __restrict__ dy, int64_t ld_dy, int T, int N, int Tpad,
+                                              int chunk, uint8_t* __restrict__ q, int64_t ld_q,
+                                              uint8_t* __restrict__ s, int64_t s_col_tiles, int col_tile_off,
+                                              const uint16_t* __restrict__ xa, int64_t ld_xa,
+                                              const uint16_t* __restrict__ B, float* __restrict__ part_dxa,
+                                              float* __restrict__ part_db, uint16_t* __restrict__ dxa, int64_t ld_dxa,
+                                              float scale, const int bx, const int by, const int ny) {
   constexpr int kTileB = 32 * 256;         // one block of one wave: 32 rows x 128 bf16
   constexpr int kRedB = kLora ? 4 * 128 * 17 * 4 : 0;  // end-of-kernel dB exchange: [wave][column][16 ρ + 1]
   constexpr int kXaL = kLora ? R / 16 : 0;  // 16-byte xa pieces per lane per block
@@ -357,8 +359,8 @@ __global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __rest
   __shared__ __attribute__((aligned(16))) uint16_t xat[4][kLora ? 32 * R : 8];  // per-wave xa tile
   __shared__ __attribute__((aligned(16))) uint8_t qtile[4][kQuant ? 32 * 128 : 16];  // per-wave block of codes
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
-  const int r0 = blockIdx.x * chunk, r1 = min(r0 + chunk, Tpad);
-  const int c0 = blockIdx.y * 128;
+  const int r0 = bx * chunk, r1 = min(r0 + chunk, Tpad);
+  const int c0 = by * 128;
   const int row = lane & 31;
   const int nblk = (r1 - r0) / 32;
   uint8_t* tile = tiles + w * kTileB;
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __rest
     for (int jh = 0; jh < 2; ++jh)
 #pragma unroll
       for (int h = 0; h < R / 16; ++h) db[g][jh][h] = v4f{};
-  const bool direct = gridDim.y == 1;
+  const bool direct = ny == 1;
   auto lb_block = [&](const int rb) __attribute__((always_inline)) {
     const int m = rb + row;
     const bool live = m < T;
@@ -474,7 +476,7 @@ __global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __rest
 #pragma unroll
         for (int i = 0; i < R / 2; ++i) o[(i >> 2) * 8 + lg * 4 + (i & 3)] = bf(p[i] * scale);
       } else {
-        float* o = part_dxa + ((int64_t)blockIdx.y * T + mc) * R;
+        float* o = part_dxa + ((int64_t)by * T + mc) * R;
 #pragma unroll
         for (int i4 = 0; i4 < R / 8; ++i4)
           *reinterpret_cast<float4*>(o + i4 * 8 + lg * 4) =
@@ -537,13 +539,51 @@ __global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __rest
       __syncthreads();
       for (int idx = threadIdx.x; idx < 128 * 16; idx += 256) {
         const int n = idx >> 4, rr = idx & 15;
-        part_db[((int64_t)blockIdx.x * N + c0 + n) * R + h * 16 + rr] =
+        part_db[((int64_t)bx * N + c0 + n) * R + h * 16 + rr] =
             ((red[0][n][rr] + red[1][n][rr]) + red[2][n][rr]) + red[3][n][rr];
       }
     }
   }
 }
 #undef LB_FETCH
+
+template <int R, bool kQuant, bool kLora>
+__global__ __launch_bounds__(256, 2) void lora_bwd_kernel(const uint16_t* __restrict__ dy, int64_t ld_dy, int T,
+                                                          int N, int Tpad, int chunk, uint8_t* __restrict__ q,
+                                                          int64_t ld_q, uint8_t* __restrict__ s, int64_t s_col_tiles,
+                                                          int col_tile_off, const uint16_t* __restrict__ xa,
+                                                          int64_t ld_xa, const uint16_t* __restrict__ B,
+                                                          float* __restrict__ part_dxa, float* __restrict__ part_db,
+                                                          uint16_t* __restrict__ dxa, int64_t ld_dxa, float scale) {
+  lora_bwd_body<R, kQuant, kLora>(dy, ld_dy, T, N, Tpad, chunk, q, ld_q, s, s_col_tiles, col_tile_off, xa, ld_xa, B,
+                                  part_dxa, part_db, dxa, ld_dxa, scale, blockIdx.x, blockIdx.y, gridDim.y);
+}
+
+// The jobs of mxfp8_lora_bwd_batch in one flat grid: job j owns blocks first[j] .. first[j + 1] - 1, `used` row
+// chunks per column block, so every layer of the group streams its dy at the same time.
+struct LoraBwdBatch {
+  mxfp8_lora_bwd_job job[MXFP8_LORA_BWD_MAX_JOBS];
+  int first[MXFP8_LORA_BWD_MAX_JOBS + 1];
+  int n, T, Tpad, chunk, used;
+  uint8_t* q;
+  int64_t ld_q;
+  uint8_t* s;
+  int64_t s_col_tiles;
+};
+
+template <int R, bool kQuant>
+__global__ __launch_bounds__(256, 2) void lora_bwd_batch_kernel(const LoraBwdBatch a) {
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
+  const mxfp8_lora_bwd_job& jb = a.job[j];
+  const int local = b - a.first[j];
+  lora_bwd_body<R, kQuant, true>(static_cast<const uint16_t*>(jb.dy), jb.ld_dy, a.T, (int)jb.N, a.Tpad, a.chunk, a.q,
+                                 a.ld_q, a.s, a.s_col_tiles, (int)jb.col_tile_off,
+                                 static_cast<const uint16_t*>(jb.xa), jb.ld_xa, static_cast<const uint16_t*>(jb.b),
+                                 jb.part_dxa, jb.part_db, static_cast<uint16_t*>(jb.dxa), jb.ld_dxa, jb.scale,
+                                 local % a.used, local / a.used, (int)(jb.N / 128));
+}
 
 // 16-byte vectors of fp32 partial sums added in ascending partial order, four loads in flight at a time
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
@@ -563,11 +603,10 @@ __device__ __forceinline__ float4 sum_ordered(const float4* __restrict__ p, int6
 // dxa[t, ρ] (row stride ld_dxa) = bf16(scale · Σ_p part_dxa[p, t, ρ]) over the first nx = T·R elements (none when
 // the main kernel wrote d(xa) itself) and dB[n, ρ] = scale · Σ_p part_db[p, n, ρ] (fp32) over the next N·R, partials
 // added in ascending p (mxfp8.py:180-216, _sum_rows / _sum_parts).  Four consecutive elements per thread.
-__global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restrict__ part_dxa, int ncs, int64_t nx,
-                                                           const float* __restrict__ part_db, int nrs, int64_t nb,
-                                                           int R, float scale, uint16_t* __restrict__ dxa,
-                                                           int64_t ld_dxa, float* __restrict__ dB) {
-  int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+__device__ __forceinline__ void lora_bwd_sum_body(const float* __restrict__ part_dxa, int ncs, int64_t nx,
+                                                  const float* __restrict__ part_db, int nrs, int64_t nb, int R,
+                                                  float scale, uint16_t* __restrict__ dxa, int64_t ld_dxa,
+                                                  float* __restrict__ dB, int64_t i) {
   if (i < nx) {
     const float4 v = sum_ordered(reinterpret_cast<const float4*>(part_dxa + i), nx / 4, ncs);
     uint16_t* o = dxa + (i / R) * ld_dxa + i % R;  // R % 4 == 0: the four share a row
@@ -581,6 +620,32 @@ __global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restri
   if (i >= nb) return;
   const float4 v = sum_ordered(reinterpret_cast<const float4*>(part_db + i), nb / 4, nrs);
   *reinterpret_cast<float4*>(dB + i) = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+}
+
+__global__ __launch_bounds__(256) void lora_bwd_sum_kernel(const float* __restrict__ part_dxa, int ncs, int64_t nx,
+                                                           const float* __restrict__ part_db, int nrs, int64_t nb,
+                                                           int R, float scale, uint16_t* __restrict__ dxa,
+                                                           int64_t ld_dxa, float* __restrict__ dB) {
+  lora_bwd_sum_body(part_dxa, ncs, nx, part_db, nrs, nb, R, scale, dxa, ld_dxa, dB,
+                    ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4);
+}
+
+// The sums of mxfp8_lora_bwd_batch's jobs in one flat grid (job j: blocks first[j] .. first[j + 1] - 1).
+struct LoraBwdSumBatch {
+  mxfp8_lora_bwd_job job[MXFP8_LORA_BWD_MAX_JOBS];
+  int first[MXFP8_LORA_BWD_MAX_JOBS + 1];
+  int n, nrs, R, T;
+};
+
+__global__ __launch_bounds__(256) void lora_bwd_sum_batch_kernel(const LoraBwdSumBatch a) {
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
+  const mxfp8_lora_bwd_job& jb = a.job[j];
+  const int64_t nx = jb.N == 128 ? 0 : (int64_t)a.T * a.R;  // one column chunk: d(xa) already written
+  lora_bwd_sum_body(jb.part_dxa, (int)(jb.N / 128), nx, jb.part_db, a.nrs, jb.N * a.R, a.R, jb.scale,
+                    static_cast<uint16_t*>(jb.dxa), jb.ld_dxa, jb.db,
+                    ((int64_t)(b - a.first[j]) * 256 + threadIdx.x) * 4);
 }
 
 // ------------------------------------------------------------------------------------- Pᵀ · X (tn)
@@ -1092,5 +1157,71 @@ extern "C" int mxfp8_lora_bwd(const void* dy, int64_t T, int64_t N, int64_t ld_d
         part_dxa, (int)(N / 128), nx, part_db, (int)used, N * r, (int)r, scale, (uint16_t*)dxa, ld_dxa, db);
     MX_CHECK_LAUNCH("mxfp8_lora_bwd");
   }
+  return MXFP8_OK;
+}
+
+extern "C" int64_t mxfp8_lora_bwd_batch_chunks(int64_t T, int64_t n_total) { return lora_bwd_rows(T, n_total, 512); }
+
+extern "C" int mxfp8_lora_bwd_batch(const mxfp8_lora_bwd_job* jobs, int64_t n_jobs, int64_t T, int64_t r, void* q,
+                                    int64_t ld_q, void* s, int64_t s_col_tiles, void* stream) {
+  MX_CHECK_ARG(jobs && n_jobs > 0 && n_jobs <= MXFP8_LORA_BWD_MAX_JOBS && T > 0 && (r == 16 || r == 32),
+               "mxfp8_lora_bwd_batch: need 1..%d jobs, T > 0, r in {16, 32}", MXFP8_LORA_BWD_MAX_JOBS);
+  const bool quant = q != nullptr;
+  MX_CHECK_ARG(!quant || (s && ld_q % 16 == 0 && mx_aligned(q, 16) && mx_aligned(s, 4)),
+               "mxfp8_lora_bwd_batch: bad code / scale destination");
+  int64_t n_total = 0;
+  for (int64_t j = 0; j < n_jobs; ++j) {
+    const mxfp8_lora_bwd_job& jb = jobs[j];
+    MX_CHECK_ARG(jb.dy && jb.N > 0 && jb.N % 128 == 0 && jb.ld_dy >= jb.N && jb.ld_dy % 8 == 0 &&
+                     T * jb.ld_dy < (1LL << 40) && mx_aligned(jb.dy, 16),
+                 "mxfp8_lora_bwd_batch: job %lld: need N %% 128 == 0 and 16-byte aligned dy rows", (long long)j);
+    MX_CHECK_ARG(!quant || (jb.col_tile_off >= 0 && jb.col_tile_off * 128 + jb.N <= ld_q &&
+                            jb.col_tile_off * 128 + jb.N <= s_col_tiles * 128),
+                 "mxfp8_lora_bwd_batch: job %lld: bad code / scale destination", (long long)j);
+    MX_CHECK_ARG(jb.xa && jb.b && jb.dxa && jb.db && jb.part_dxa && jb.part_db && jb.ld_xa >= r && jb.ld_xa % 8 == 0 &&
+                     jb.ld_dxa >= r && mx_aligned(jb.xa, 16) && mx_aligned(jb.b, 2),
+                 "mxfp8_lora_bwd_batch: job %lld: needs xa, B, dxa, dB and partial buffers", (long long)j);
+    n_total += jb.N;
+  }
+  const int64_t rs = mxfp8_lora_bwd_batch_chunks(T, n_total);
+  const int64_t Tpad = (T + 127) / 128 * 128, blocks = Tpad / 32;
+  const int64_t chunk = (blocks + rs - 1) / rs * 32;
+  const int64_t used = (Tpad + chunk - 1) / chunk;
+  LoraBwdBatch a{};
+  LoraBwdSumBatch b{};
+  int64_t wgs = 0, sum_blocks = 0;
+  for (int64_t j = 0; j < n_jobs; ++j) {
+    a.job[j] = b.job[j] = jobs[j];
+    a.first[j] = (int)wgs;
+    b.first[j] = (int)sum_blocks;
+    wgs += used * (jobs[j].N / 128);
+    const int64_t total = (jobs[j].N == 128 ? 0 : T * r) + jobs[j].N * r;
+    sum_blocks += (total / 4 + 255) / 256;
+  }
+  MX_CHECK_ARG(wgs < (1LL << 31) && sum_blocks < (1LL << 31), "mxfp8_lora_bwd_batch: too large");
+  a.first[n_jobs] = (int)wgs;
+  b.first[n_jobs] = (int)sum_blocks;
+  a.n = b.n = (int)n_jobs;
+  a.T = b.T = (int)T;
+  a.Tpad = (int)Tpad;
+  a.chunk = (int)chunk;
+  a.used = (int)used;
+  a.q = (uint8_t*)q;
+  a.ld_q = ld_q;
+  a.s = (uint8_t*)s;
+  a.s_col_tiles = s_col_tiles;
+  b.nrs = (int)used;
+  b.R = (int)r;
+  hipStream_t stm = (hipStream_t)stream;
+  if (r == 16) {
+    if (quant) lora_bwd_batch_kernel<16, true><<<(unsigned)wgs, 256, 0, stm>>>(a);
+    else lora_bwd_batch_kernel<16, false><<<(unsigned)wgs, 256, 0, stm>>>(a);
+  } else {
+    if (quant) lora_bwd_batch_kernel<32, true><<<(unsigned)wgs, 256, 0, stm>>>(a);
+    else lora_bwd_batch_kernel<32, false><<<(unsigned)wgs, 256, 0, stm>>>(a);
+  }
+  MX_CHECK_LAUNCH("mxfp8_lora_bwd_batch");
+  lora_bwd_sum_batch_kernel<<<(unsigned)sum_blocks, 256, 0, stm>>>(b);
+  MX_CHECK_LAUNCH("mxfp8_lora_bwd_batch");
   return MXFP8_OK;
 }

@@ -427,6 +427,24 @@ def _fused_bwd_plan(spec, flat, dt, need_x):
     return None if wt is None else (wt,)
 
 
+def _lora_bwd_batchable(spec, flat, xS):
+    """The adapter slots of the group's MX layers when their lora_bwd calls can run as one batch: 2..8 MX layers,
+    each with an adapter of one common rank 16 or 32 whose xS columns the kernel reads with 16-byte loads, and
+    row-contiguous, 16-byte aligned dy; else None."""
+    import _native
+    slots = [spec.adapter(i) for i in spec.mx]
+    if not 2 <= len(slots) <= _native.LORA_BWD_MAX_JOBS or any(sl is None for sl in slots):
+        return None
+    if len({sl.width for sl in slots}) != 1 or slots[0].width not in (16, 32):
+        return None
+    if not all(_vec_ok(xS[:, sl.cols]) for sl in slots):
+        return None
+    if not all(flat[i].stride(1) == 1 and flat[i].stride(0) % 8 == 0 and flat[i].data_ptr() % 16 == 0
+               for i in spec.mx):
+        return None
+    return slots
+
+
 def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
     """Grouped backward through mxfp8.lora_bwd (fused_linear.py:219-279): each MX dy is read ONCE (its MX codes
     into a buffer concatenated along the group's N, its d(xa) into dS, its dB), then dx of the group is ONE MX
@@ -449,7 +467,19 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
         q = torch.empty((T, n_mx), dtype=mxfp8.F8, device=dev)
         sbuf = torch.empty(_cdiv(T, 128) * (n_mx // 128) * 512, dtype=torch.uint8, device=dev)
     tile = 0
-    for i in spec.mx:
+    batch = _lora_bwd_batchable(spec, flat, xS)
+    if batch:
+        # every MX layer's lora_bwd in one launch (mxfp8_lora_bwd_batch)
+        offs, t = [], 0
+        for i in spec.mx:
+            offs.append(t)
+            t += flat[i].shape[1] // 128
+        dbs = mxfp8.lora_bwd_batch([flat[i] for i in spec.mx], [xS[:, sl.cols] for sl in batch],
+                                   [Bs[sl.index] for sl in batch], [sl.scale for sl in batch],
+                                   [dS[:, sl.cols] for sl in batch], q=q, s=sbuf, col_tile_offs=offs)
+        for sl, db in zip(batch, dbs):
+            grads[2 * sl.index + 1] = db
+    for i in (() if batch else spec.mx):
         dy = flat[i] if flat[i].stride(1) == 1 else flat[i].contiguous()
         sl = spec.adapter(i)
         if sl is not None and sl.width in (16, 32) and _vec_ok(xS[:, sl.cols]):

@@ -135,6 +135,35 @@ def lora_bwd(dy, xa=None, B=None, scale=1.0, q=None, s=None, col_tile_off=0, dxa
     return db
 
 
+def lora_bwd_batch(dys, xas, Bs, scales, dxa_outs, q=None, s=None, col_tile_offs=None):
+    """lora_bwd of the layers of a group (one shared T and rank r) in one launch and one launch of their partial
+    sums (mxfp8_lora_bwd_batch): every dy streams at once, with one row chunking for all.  Same arguments per
+    layer as lora_bwd; returns the layers' dB (fp32).  d(xa) is the same bits as lora_bwd's; dB adds its row
+    chunks in another grouping (fp32 rounding)."""
+    T, R = dys[0].shape[0], xas[0].shape[1]
+    assert 1 <= len(dys) <= _native.LORA_BWD_MAX_JOBS and R in (16, 32) and T > 0, (len(dys), R, T)
+    if q is not None:
+        assert q.is_contiguous() and q.dim() == 2 and q.shape[0] == T and s is not None
+        assert s.numel() >= scale_numel(T, q.shape[1])
+    rs = _native.lora_bwd_batch_chunks(T, sum(d.shape[1] for d in dys))
+    dev = dys[0].device
+    jobs, dbs = [], []
+    for k, (dy, xa, B, sc, dxa) in enumerate(zip(dys, xas, Bs, scales, dxa_outs)):
+        N = dy.shape[1]
+        assert dy.dtype == xa.dtype == B.dtype == dxa.dtype == torch.bfloat16 and dy.shape[0] == T and N % 128 == 0
+        assert dy.stride(1) == 1 and xa.stride(1) == 1 and B.is_contiguous() and B.shape == (N, R)
+        assert xa.shape == (T, R) and dxa.shape == (T, R) and dxa.stride(1) == 1
+        db = torch.empty((N, R), dtype=torch.float32, device=dev)
+        part_dxa = torch.empty((N // 128, T, R), dtype=torch.float32, device=dev)
+        part_db = torch.empty((rs, N, R), dtype=torch.float32, device=dev)
+        off = col_tile_offs[k] if col_tile_offs is not None else 0
+        jobs.append((dy, off, xa, B, sc, dxa, db, part_dxa, part_db))
+        dbs.append(db)
+    _native.lora_bwd_batch(jobs, T, R, q.view(torch.uint8) if q is not None else None,
+                           s.view(torch.uint8) if q is not None else None)
+    return dbs
+
+
 def tile_codes(q):
     """Row-major codes [R, K] (any row stride) -> the MX-tiled layout ([ceil(R/16)*16, K] bytes)."""
     R, K = q.shape
