@@ -741,59 +741,78 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   const int ncol0 = cseg.col0[sg];
   // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
   // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]; with B in the pi_col order (b_pi) the 16 contiguous columns
-  // n0 + wn*128 + nt*32 + (lane/32)*16 + i in acc[nt][mt][i]
+  // n0 + wn*128 + nt*32 + (lane/32)*16 + i in acc[nt][mt][i].
+  // The rank-r operands: the P rows of both row halves are loaded first, the Q rows of column block nt + 1 while
+  // block nt is finished, so the wave waits for one memory latency, not one per 32 x 32 block.  Rounding to bf16
+  // goes through v_cvt_pk_bf16_f32 (rnd2), pairwise.
+  constexpr int kH = kR > 0 ? kR / 16 : 1;
+  v8bf pf[2][kH], qf[2][kH];
+  auto load_q = [&](int nt, v8bf* dst) {
+    const int nr = min(n0 + wn * 128 + nt * 32 + (b_pi ? pi_col(lane & 31) : (lane & 31)), N - 1);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int m = m0 + wm * 64 + mt * 32 + (lane & 31);
-    v8bf pf[kR > 0 ? kR / 16 : 1];
+    for (int h = 0; h < kH; ++h)
+      dst[h] = *reinterpret_cast<const v8bf*>(lora.q + (int64_t)nr * lora.ld_q + h * 16 + (lane >> 5) * 8);
+  };
+  if constexpr (kR > 0) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int mc = min(m0 + wm * 64 + mt * 32 + (lane & 31), M - 1);
+#pragma unroll
+      for (int h = 0; h < kH; ++h)
+        pf[mt][h] = *reinterpret_cast<const v8bf*>(lora.p + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8);
+    }
+    load_q(0, qf[0]);
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int nb = n0 + wn * 128 + nt * 32;
     if constexpr (kR > 0) {
-      const int mc = min(m, M - 1);
-#pragma unroll
-      for (int h = 0; h < kR / 16; ++h)
-        pf[h] = *reinterpret_cast<const v8bf*>(lora.p + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8);
+      if (nt + 1 < 4) load_q(nt + 1, qf[(nt + 1) & 1]);
     }
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const int nb = n0 + wn * 128 + nt * 32;
-      v16f o = acc[nt][mt];
+    for (int mt = 0; mt < 2; ++mt) {
+      const int m = m0 + wm * 64 + mt * 32 + (lane & 31);
+      const v16f o = acc[nt][mt];
+      uint32_t wv[8];  // packed bf16 pairs of o[2k], o[2k + 1]
       if constexpr (kR > 0) {
-        const int nr = min(nb + (b_pi ? pi_col(lane & 31) : (lane & 31)), N - 1);
         v16f l = v16f{};
 #pragma unroll
-        for (int h = 0; h < kR / 16; ++h) {
-          v8bf qf = *reinterpret_cast<const v8bf*>(lora.q + (int64_t)nr * lora.ld_q + h * 16 + (lane >> 5) * 8);
-          l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf, pf[h], l, 0, 0, 0);
+        for (int h = 0; h < kH; ++h) l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[nt & 1][h], pf[mt][h], l, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // bf16(bf16(acc) + alpha · P·Qᵀ)
+          float a = o[2 * k], b = o[2 * k + 1];
+          rnd2(a, b);
+          a += lora.alpha * l[2 * k];
+          b += lora.alpha * l[2 * k + 1];
+          wv[k] = rnd2(a, b);
         }
+      } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i] = round_bf16(o[i]) + lora.alpha * l[i];
+        for (int k = 0; k < 8; ++k) {
+          float a = o[2 * k], b = o[2 * k + 1];
+          wv[k] = rnd2(a, b);
+        }
       }
-      if (b_pi) {
-        if (m < M) {  // columns nb + (lane/32)*16 + 0..15 (N % 128 == 0: all inside)
-          uint32_t wv[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) wv[k] = pack_bf16x2(o[2 * k], o[2 * k + 1]);
-          const int n = nb + (lane >> 5) * 16;
-          if (c_ft) {
-            uint16_t* p = C + ft_offset(m, n, N);
-            *reinterpret_cast<uint4*>(p) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-            *reinterpret_cast<uint4*>(p + 512) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
-          } else {
-            uint16_t* p = C + (int64_t)m * ldc + (n - ncol0);
-            *reinterpret_cast<uint4*>(p) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-            *reinterpret_cast<uint4*>(p + 8) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
-          }
+      if (m >= M) continue;
+      if (b_pi) {  // columns nb + (lane/32)*16 + 0..15 (N % 128 == 0: all inside)
+        const int n = nb + (lane >> 5) * 16;
+        if (c_ft) {
+          uint16_t* p = C + ft_offset(m, n, N);
+          *reinterpret_cast<uint4*>(p) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+          *reinterpret_cast<uint4*>(p + 512) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
+        } else {
+          uint16_t* p = C + (int64_t)m * ldc + (n - ncol0);
+          *reinterpret_cast<uint4*>(p) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+          *reinterpret_cast<uint4*>(p + 8) = make_uint4(wv[4], wv[5], wv[6], wv[7]);
         }
         continue;
       }
-      if (m < M) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = nb + g * 8 + (lane >> 5) * 4;
-          if (n < N) {
-            uint2 w = make_uint2(pack_bf16x2(o[4 * g], o[4 * g + 1]), pack_bf16x2(o[4 * g + 2], o[4 * g + 3]));
-            *reinterpret_cast<uint2*>(C + (c_ft ? ft_offset(m, n, N) : (int64_t)m * ldc + (n - ncol0))) = w;
-          }
-        }
+      for (int g = 0; g < 4; ++g) {
+        const int n = nb + g * 8 + (lane >> 5) * 4;
+        if (n < N)
+          *reinterpret_cast<uint2*>(C + (c_ft ? ft_offset(m, n, N) : (int64_t)m * ldc + (n - ncol0))) =
+              make_uint2(wv[2 * g], wv[2 * g + 1]);
       }
     }
   }
