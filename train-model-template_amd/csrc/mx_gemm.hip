@@ -436,8 +436,10 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
         uint32_t gw[8], hw[8];  // gate, then g; up, then u, then h (packed bf16 pairs, columns lg*16 + 2k, +1)
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-          gw[k] = pack_bf16x2(acc[b][mt][2 * k], acc[b][mt][2 * k + 1]);
-          hw[k] = pack_bf16x2(acc[2 + b][mt][2 * k], acc[2 + b][mt][2 * k + 1]);
+          float g0 = acc[b][mt][2 * k], g1 = acc[b][mt][2 * k + 1];
+          float u0 = acc[2 + b][mt][2 * k], u1 = acc[2 + b][mt][2 * k + 1];
+          gw[k] = rnd2(g0, g1);
+          hw[k] = rnd2(u0, u1);
         }
         if (live) {  // the lane's columns i = 0..7 and 8..15 are 16 contiguous bytes each in an FT block
           uint16_t* pg = swe.gu + ft_offset(m, jb + lg * 16, 2 * Nf);
