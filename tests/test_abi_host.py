@@ -42,6 +42,23 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(_declared()) == set(_native.SIGNATURES)
 
 
+def _arg_counts():
+    txt = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, args in re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(mxfp8_\w+)\s*\(([^)]*)\)", txt, flags=re.M):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_signatures_match_the_header_argument_counts():
+    # every pointer-sized argument, the trailing stream included, must be typed: an untyped Python int is
+    # passed as a C int
+    counts = _arg_counts()
+    for name, args in _native.SIGNATURES.items():
+        assert len(args) == counts[name], (name, len(args), counts[name])
+
+
 def test_abi_version(lib):
     assert lib.mxfp8_abi_version() == _native.ABI_VERSION
     txt = open(HEADER).read()

@@ -29,7 +29,7 @@ SIGNATURES = {
                       _i64, _f32, _i64, _ptr, _i64, _ptr],
     "mxfp8_gemm_workspace_size": [_i64, _i64, _i64],
     "mxfp8_gemm_swiglu_fwd": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64, _f32, _f32, _ptr,
-                              _ptr, _ptr, _ptr],
+                              _ptr, _ptr, _ptr, _ptr],
     "mxfp8_gemm_swiglu_bwd": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64] + [_ptr] * 11 + [_i64, _f32, _f32] + [_ptr] * 7,
     "mxfp8_gemm_nt_seg": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64,
                           _ptr, _i64, _i64, _f32, _i64, _ptr],
@@ -43,18 +43,18 @@ SIGNATURES = {
     "mxfp8_lora_nt": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_res_lora": [_ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _f32, _ptr, _ptr],
-    "mxfp8_transpose_pad": [_ptr, _i64, _i64, _i64, _ptr, _i64],
-    "mxfp8_pack_bf16": [_ptr, _i64],
+    "mxfp8_transpose_pad": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr],
+    "mxfp8_pack_bf16": [_ptr, _i64, _ptr],
     "mxfp8_lora_tn_chunks": [_i64, _i64],
     "mxfp8_swiglu": [_ptr, _ptr, _i64, _ptr, _ptr],
     "mxfp8_swiglu_bwd": [_ptr, _ptr, _ptr, _i64, _ptr, _ptr, _ptr],
     "mxfp8_lora_bwd_chunks": [_i64, _i64],
     "mxfp8_lora_bwd": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr, _i64,
-                       _ptr, _ptr, _ptr],
+                       _ptr, _ptr, _ptr, _ptr],
     "mxfp8_lora_bwd_batch_chunks": [_i64, _i64],
-    "mxfp8_lora_bwd_batch": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64],
+    "mxfp8_lora_bwd_batch": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
-    "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr],
+    "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc_chunks": [_i64, _i64, _i64],
     "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
                              _ptr, _ptr],
@@ -97,12 +97,19 @@ def _check(rc, name):
         raise NativeError(f"{name} failed with code {rc}: {_lib.mxfp8_last_error().decode()}")
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream  # device index -> the current HIP stream, as an int
+
+
 def _stream(t):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return _raw_stream(t.get_device())
 
 
 def _p(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    """A tensor's device address as an int (the signatures type it as a pointer), or None; an int passes
+    through (an address inside a scratch buffer)."""
+    if t is None or isinstance(t, int):
+        return t
+    return t.data_ptr()
 
 
 def _gpu(t, what):
@@ -110,12 +117,19 @@ def _gpu(t, what):
         raise NativeError(f"{what}: tensors must be on the GPU (the MXFP8 path has no CPU implementation)")
 
 
+_FNS = {}  # entry point name -> typed ctypes function
+
+
 def call(name, *args, like):
     """Call entry point `name` with `args` followed by the current stream of tensor `like`'s device."""
-    L = load()
-    _gpu(like, name)
-    rc = getattr(L, name)(*args, _stream(like))
-    _check(rc, name)
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(load(), name)
+    if not like.is_cuda:
+        _gpu(like, name)
+    rc = fn(*args, _raw_stream(like.get_device()))
+    if rc != 0:
+        _check(rc, name)
 
 
 def quant_rows(x, q, s, ld_q=None, s_col_tiles=None, s_tile0=0):
@@ -154,12 +168,29 @@ def gemm_workspace(M, N, K, device):
     need = load().mxfp8_gemm_workspace_size(M, N, K)
     if need <= 0:
         return None, 0
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, _raw_stream(idx))
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.zeros(need, dtype=torch.uint8, device=device)
         _WORKSPACE[key] = ws
     return ws, ws.numel()
+
+
+_SCRATCH = {}  # (device index, stream) -> float32 scratch of the partial-sum launch pairs
+
+
+def scratch_f32(n, device):
+    """At least n float32 of scratch memory on the current stream of `device`, shared by the launch pairs that
+    pass partial sums from one kernel to the next (lora_bwd, lora_bwd_batch, lora_tn): launches on one stream
+    run in order, so two pairs never use it at once.  Its contents are undefined; grown on demand (the caching
+    allocator reuses a replaced buffer only for later work on the same stream)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, _raw_stream(idx))
+    buf = _SCRATCH.get(key)
+    if buf is None or buf.numel() < n:
+        buf = _SCRATCH[key] = torch.empty(n, dtype=torch.float32, device=device)
+    return buf
 
 
 def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0, split=True, layout=0):
@@ -334,9 +365,13 @@ def pack_bf16(jobs):
     """Run the bf16 copies `jobs` = [(src, dst, transpose)] in as few launches as the job table allows: src a 2-D
     fp32 or bf16 tensor [rows, cols] with unit column stride, or None for zeros; dst a 2-D bf16 view, [rows, cols]
     or, when transpose, [cols, rows], with unit column stride.  Destinations must not overlap."""
-    if not jobs:
-        return
-    like = jobs[0][1]
+    if jobs:
+        pack_run(pack_table(jobs), like=jobs[0][1])
+
+
+def pack_table(jobs):
+    """The job tables of pack_bf16(jobs), built once: a list of (ctypes array, count), at most PACK_MAX_JOBS
+    each.  They hold the tensors' addresses, so they stay valid while those tensors live at the same place."""
     table = []
     for src, dst, tr in jobs:
         assert dst.dtype == torch.bfloat16 and dst.dim() == 2 and dst.stride(1) == 1, (dst.dtype, dst.shape)
@@ -347,10 +382,17 @@ def pack_bf16(jobs):
         table.append(PackJob(None if src is None else _p(src), 0 if src is None else src.stride(0),
                              int(src is not None and src.dtype == torch.float32), rows, cols, _p(dst), dst.stride(0),
                              int(bool(tr))))
+    out = []
     for i in range(0, len(table), PACK_MAX_JOBS):
         chunk = table[i:i + PACK_MAX_JOBS]
-        arr = (PackJob * len(chunk))(*chunk)
-        call("mxfp8_pack_bf16", ctypes.cast(arr, _ptr), len(chunk), like=like)
+        out.append(((PackJob * len(chunk))(*chunk), len(chunk)))
+    return out
+
+
+def pack_run(tables, like):
+    """Launch the job tables of pack_table on the current stream of `like`'s device."""
+    for arr, n in tables:
+        call("mxfp8_pack_bf16", ctypes.addressof(arr), n, like=like)
 
 
 def transpose_pad(x, out):

@@ -143,50 +143,73 @@ def _s_pad(S, key, rp):
     return _cast(key + ("pad", rp), lambda: torch.cat([S, S.new_zeros(rp - S.shape[0], S.shape[1])]))
 
 
+# The layout of a group's weight forms, kept across steps: the buffer, its views and the pack job table, keyed
+# by the addresses, shapes, strides and dtypes of the group's sources (the optimizer updates parameters in
+# place, at the same addresses).  Each step relaunches the pack into the same buffer; the previous step's
+# backward, earlier on the stream, has read it by then.
+_PLANS = {}
+_PLANS_MAX = 256
+
+
+def _build_forms(spec, K, dev):
+    """The buffer and views of the group's weight forms and the pack jobs that fill them."""
+    import types
+    rp, width = _rp(spec.width), spec.width
+    a8 = lambda n: _cdiv(n, 8) * 8  # noqa: E731  (16-byte aligned views)
+    sizes = [rp * K, K * rp] + [spec.parts[sl.layer][2].shape[0] * sl.width for sl in spec.adapters]
+    n_q = sum(spec.parts[i][0].out_features for i in spec.mx) if len(spec.mx) >= 2 else 0
+    sizes.append(n_q * rp)
+    buf = torch.empty(sum(a8(n) for n in sizes), dtype=torch.bfloat16, device=dev)
+    views, off = [], 0
+    for n in sizes:
+        views.append(buf[off:off + n])
+        off += a8(n)
+    S_pad, St = views[0].view(rp, K), views[1].view(K, rp)
+    Bs = [v.view(-1, sl.width) for v, sl in zip(views[2:-1], spec.adapters)]
+    Q = views[-1].view(n_q, rp) if n_q else None
+    jobs = []
+    for sl, src in zip(spec.adapters + spec.thin, spec.s_sources()):
+        jobs += [(src.detach(), S_pad[sl.cols], False), (src.detach(), St[:, sl.cols], True)]
+    if rp > width:
+        jobs += [(None, S_pad[width:], False), (None, St[:, width:], True)]
+    for sl, b in zip(spec.adapters, Bs):
+        jobs.append((spec.parts[sl.layer][2].detach(), b, False))
+    row = 0
+    for i in (spec.mx if n_q else ()):
+        n, sl = spec.parts[i][0].out_features, spec.adapter(i)
+        if sl is None:
+            jobs.append((None, Q[row:row + n], False))
+        else:
+            if sl.col:
+                jobs.append((None, Q[row:row + n, :sl.col], False))
+            jobs.append((spec.parts[i][2].detach(), Q[row:row + n, sl.cols], False))
+            if sl.col + sl.width < rp:
+                jobs.append((None, Q[row:row + n, sl.col + sl.width:], False))
+        row += n
+    return types.SimpleNamespace(S_pad=S_pad, S=S_pad[:width], St=St, Bs=Bs, Q=Q, rp=rp), jobs
+
+
 def _group_forms(spec, skey, K, dev):
     """Every per-step bf16 form of the group's weights from ONE launch (mxfp8_pack_bf16), cached per step under
     skey: S_pad [rp, K] (the A rows and thin weights in column order, zero rows up to rp = _rp(width)), St =
     S_padᵀ [K, rp] (the backward's dS·S operand), each adapter's B [n, r] in Bs, and Q [Σ n, rp] with the MX
     layers' B placed block-diagonally at their S columns (the merged forward GEMM's epilogue operand; None
-    for fewer than two MX layers).  The torch path builds these with one operation each."""
+    for fewer than two MX layers).  The buffer and the job table persist across steps (_PLANS); the torch path
+    builds these with one operation each."""
     def make():
-        import types
-
         import _native
-        rp, width = _rp(spec.width), spec.width
-        a8 = lambda n: _cdiv(n, 8) * 8  # noqa: E731  (16-byte aligned views)
-        sizes = [rp * K, K * rp] + [spec.parts[sl.layer][2].shape[0] * sl.width for sl in spec.adapters]
-        n_q = sum(spec.parts[i][0].out_features for i in spec.mx) if len(spec.mx) >= 2 else 0
-        sizes.append(n_q * rp)
-        buf = torch.empty(sum(a8(n) for n in sizes), dtype=torch.bfloat16, device=dev)
-        views, off = [], 0
-        for n in sizes:
-            views.append(buf[off:off + n])
-            off += a8(n)
-        S_pad, St = views[0].view(rp, K), views[1].view(K, rp)
-        Bs = [v.view(-1, sl.width) for v, sl in zip(views[2:-1], spec.adapters)]
-        Q = views[-1].view(n_q, rp) if n_q else None
-        jobs = []
-        for sl, src in zip(spec.adapters + spec.thin, spec.s_sources()):
-            jobs += [(src.detach(), S_pad[sl.cols], False), (src.detach(), St[:, sl.cols], True)]
-        if rp > width:
-            jobs += [(None, S_pad[width:], False), (None, St[:, width:], True)]
-        for sl, b in zip(spec.adapters, Bs):
-            jobs.append((spec.parts[sl.layer][2].detach(), b, False))
-        row = 0
-        for i in (spec.mx if n_q else ()):
-            n, sl = spec.parts[i][0].out_features, spec.adapter(i)
-            if sl is None:
-                jobs.append((None, Q[row:row + n], False))
-            else:
-                if sl.col:
-                    jobs.append((None, Q[row:row + n, :sl.col], False))
-                jobs.append((spec.parts[i][2].detach(), Q[row:row + n, sl.cols], False))
-                if sl.col + sl.width < rp:
-                    jobs.append((None, Q[row:row + n, sl.col + sl.width:], False))
-            row += n
-        _native.pack_bf16(jobs)
-        return types.SimpleNamespace(S_pad=S_pad, S=S_pad[:width], St=St, Bs=Bs, Q=Q, rp=rp)
+        srcs = spec.s_sources() + [spec.parts[sl.layer][2] for sl in spec.adapters]
+        sig = (K, dev, tuple((sl.col, sl.width) for sl in spec.adapters + spec.thin),
+               tuple(spec.parts[i][0].out_features for i in spec.mx),
+               tuple((t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype) for t in srcs))
+        plan = _PLANS.get(sig)
+        if plan is None:
+            if len(_PLANS) >= _PLANS_MAX:
+                _PLANS.clear()
+            forms, jobs = _build_forms(spec, K, dev)
+            plan = _PLANS[sig] = (forms, _native.pack_table(jobs))
+        _native.pack_run(plan[1], like=plan[0].S_pad)
+        return plan[0]
     return _cast(skey + ("forms",), make)
 
 
@@ -531,7 +554,8 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
             # to its parameter's dtype anyway (exactly), one kernel per adapter
             a32 = all(spec.parts[sl.layer][1].dtype == torch.float32 for sl in spec.adapters)
             dA = torch.empty((width, K), dtype=torch.float32 if a32 else dt, device=dev)
-            part = torch.empty(_native.lora_tn_chunks(T, K) * width * K, dtype=torch.float32, device=dev)
+            n_part = _native.lora_tn_chunks(T, K) * width * K
+            part = _native.scratch_f32(n_part, dev)[:n_part]  # partial sums, read by the launch's sum kernel
             _native.lora_tn(x2, dS, dA, part)
         else:
             dA = dS[:, :spec.adapter_cols].t() @ x2

@@ -128,8 +128,10 @@ def lora_bwd(dy, xa=None, B=None, scale=1.0, q=None, s=None, col_tile_off=0, dxa
         assert B.shape == (N, R) and xa.shape[0] == T and dxa_out is not None and dxa_out.shape == (T, R)
         assert dxa_out.stride(1) == 1 and dxa_out.dtype == torch.bfloat16
         db = torch.empty((N, R), dtype=torch.float32, device=dev)
-        part_dxa = torch.empty((N // 128, T, R), dtype=torch.float32, device=dev)
-        part_db = torch.empty((_native.lora_bwd_chunks(T, N), N, R), dtype=torch.float32, device=dev)
+        # the partial sums [N / 128, T, R] and [row chunks, N, R] live only until the launch's sum kernel
+        n_dxa = _cdiv((N // 128) * T * R, 64) * 64
+        part_dxa = _native.scratch_f32(n_dxa + _native.lora_bwd_chunks(T, N) * N * R, dev).data_ptr()
+        part_db = part_dxa + 4 * n_dxa
     _native.lora_bwd(dy, q.view(torch.uint8) if do_q else None, s.view(torch.uint8) if do_q else None,
                      q.shape[1] // 128 if do_q else 0, col_tile_off, xa, B, scale, dxa_out, db, part_dxa, part_db)
     return db
@@ -145,17 +147,21 @@ def lora_bwd_batch(dys, xas, Bs, scales, dxa_outs, q=None, s=None, col_tile_offs
     if q is not None:
         assert q.is_contiguous() and q.dim() == 2 and q.shape[0] == T and s is not None
         assert s.numel() >= scale_numel(T, q.shape[1])
-    rs = _native.lora_bwd_batch_chunks(T, sum(d.shape[1] for d in dys))
+    Ns = [d.shape[1] for d in dys]
+    rs = _native.lora_bwd_batch_chunks(T, sum(Ns))
     dev = dys[0].device
+    # every job's partial sums ([N / 128, T, R] and [rs, N, R], live only until the sum launch) in the scratch
+    sizes = [_cdiv(n // 128 * T * R, 64) * 64 + _cdiv(rs * n * R, 64) * 64 for n in Ns]
+    addr = _native.scratch_f32(sum(sizes), dev).data_ptr()
     jobs, dbs = [], []
     for k, (dy, xa, B, sc, dxa) in enumerate(zip(dys, xas, Bs, scales, dxa_outs)):
-        N = dy.shape[1]
+        N = Ns[k]
         assert dy.dtype == xa.dtype == B.dtype == dxa.dtype == torch.bfloat16 and dy.shape[0] == T and N % 128 == 0
         assert dy.stride(1) == 1 and xa.stride(1) == 1 and B.is_contiguous() and B.shape == (N, R)
         assert xa.shape == (T, R) and dxa.shape == (T, R) and dxa.stride(1) == 1
         db = torch.empty((N, R), dtype=torch.float32, device=dev)
-        part_dxa = torch.empty((N // 128, T, R), dtype=torch.float32, device=dev)
-        part_db = torch.empty((rs, N, R), dtype=torch.float32, device=dev)
+        part_dxa, part_db = addr, addr + 4 * _cdiv(N // 128 * T * R, 64) * 64
+        addr += 4 * sizes[k]
         off = col_tile_offs[k] if col_tile_offs is not None else 0
         jobs.append((dy, off, xa, B, sc, dxa, db, part_dxa, part_db))
         dbs.append(db)
@@ -394,7 +400,7 @@ FUSED_BWD = {"in_proj_qkv", "in_proj_z", "q_proj", "k_proj", "v_proj", "o_proj",
 FUSE_GU = os.environ.get("MXFP8_FUSE_GU", "1") != "0"
 # what enable_mxfp8 attaches to a linear (disable_mxfp8 removes exactly these)
 _MX_ATTRS = ("_mx_w", "_mx_ws", "_mx_wt", "_mx_wts", "_mx_w_tl", "_mx_wt_tl", "_mx_wtf_tl", "_mx_wtfs", "_mx_wp_tl",
-             "_mx_wps", "_mx_cat", "_mx_gu", "_mx_fbwd", "_bf16_cpu", "forward")
+             "_mx_wps", "_mx_cat", "_mx_gu", "_mx_fbwd", "_mx_ops", "_bf16_cpu", "forward")
 
 
 def _mx_target(name, mod):
@@ -552,15 +558,29 @@ def group_fwd_operand(lins):
     if span is None:
         return None
     cat, k = span
-    c0, c1 = cat.offs[k], cat.offs[k + len(lins)]
-    per_tile_row = (cat.w.shape[1] // 128) * 512
-    return cat.w_tl[c0:c1], cat.ws[c0 // 128 * per_tile_row:c1 // 128 * per_tile_row]
+    memo = cat.__dict__.setdefault("_ops", {})
+    key = ("fwd", k, len(lins))
+    if key not in memo:
+        c0, c1 = cat.offs[k], cat.offs[k + len(lins)]
+        per_tile_row = (cat.w.shape[1] // 128) * 512
+        memo[key] = (cat.w_tl[c0:c1], cat.ws[c0 // 128 * per_tile_row:c1 // 128 * per_tile_row])
+    return memo[key]
 
 
 def group_operand(lins):
     """(B operand [K, ΣN] of mx_mm, scales, layout bit) of dx for `lins` (group_wt): the MX-tiled copy when the
     range is a whole concatenated group or a single layer that has one, else the row-major column view (row
-    stride ΣN of the group)."""
+    stride ΣN of the group).  Kept on the group (or the layer) after the first call: the MX copies are fixed
+    from enable_mxfp8 on."""
+    span = _cat_span(lins)
+    memo = span[0].__dict__.setdefault("_ops", {}) if span is not None else lins[0].__dict__.setdefault("_mx_ops", {})
+    key = ("dx", span[1] if span is not None else 0, len(lins))
+    if key not in memo:
+        memo[key] = _group_operand(lins)
+    return memo[key]
+
+
+def _group_operand(lins):
     g = group_wt(lins)
     if g is None:
         return None
