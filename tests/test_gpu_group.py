@@ -296,3 +296,44 @@ def test_merged_forward_gemm_matches_one_gemm_per_layer(gpu):
     # two consecutive layers of the group (k|v) merge too; a non-consecutive pair (q, v) does not
     assert mxfp8.group_fwd_operand([a.k_proj.base_layer, a.v_proj.base_layer]) is not None
     assert mxfp8.group_fwd_operand([a.q_proj.base_layer, a.v_proj.base_layer]) is None
+
+
+def test_weight_forms_follow_in_place_updates_and_new_parameters(gpu):
+    # the per-step weight forms come from a buffer and job table kept across steps (fused_linear._PLANS): an
+    # optimizer's in-place update and a parameter replaced by a new tensor must both reach the next step, with
+    # the same bits as a plan built from scratch
+    m, _ = _build(gpu, seed=31)
+    a = m.attn
+    mods = [a.q_proj, a.k_proj, a.v_proj]
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    dys = [(torch.randn(T, n, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for n in (NQ, NKV, NKV)]
+
+    def step(fresh):
+        if fresh:
+            fused_linear._PLANS.clear()
+        fused_linear.new_step()
+        for p in m.parameters():
+            p.grad = None
+        xg = x.clone().requires_grad_(True)
+        outs = fused_linear.group_linear(xg, mods)
+        torch.autograd.backward(outs, dys)
+        return [o.detach().clone() for o in outs] + [xg.grad.clone()] + [
+            p.grad.clone() for p in m.parameters() if p.grad is not None]
+
+    def same(u, v):
+        assert len(u) == len(v) and all(torch.equal(s, t) for s, t in zip(u, v))
+
+    first = step(fresh=True)
+    same(step(fresh=False), first)  # the kept plan, unchanged weights
+    with torch.no_grad():  # an optimizer step: in place, same addresses
+        a.q_proj.lora_A["default"].weight.mul_(1.5)
+        a.v_proj.lora_B["default"].weight.add_(0.01)
+    updated = step(fresh=False)
+    assert not torch.equal(updated[0], first[0]) and not torch.equal(updated[2], first[2])
+    same(updated, step(fresh=True))
+    old = a.k_proj.lora_A["default"].weight
+    a.k_proj.lora_A["default"].weight = nn.Parameter(old.detach() * -1.0)  # a new tensor at a new address
+    replaced = step(fresh=False)
+    assert not torch.equal(replaced[1], updated[1])
+    same(replaced, step(fresh=True))
