@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 9
+#define MXFP8_MLP_ABI_VERSION 10
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -131,11 +131,15 @@ int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const void* b, con
  * C only (layout bits 0-1), no workspace.  Lets the q|k|v projections of a group run as one GEMM over their
  * concatenated weight while each returns its own contiguous output (the reference runs one _scaled_mm per layer,
  * /root/reference/scripts/fused_linear.py:72-76, :106-109).
+ * seg_rcol (host array, or NULL for columns [0, r) everywhere): segment k adds the rank-r product over columns
+ * [seg_rcol[k], seg_rcol[k] + r) of P and Q (multiples of 8, within ld_p and ld_q).  A group whose Q is
+ * block-diagonal, each layer's B at that layer's own columns of P, then runs rank r per tile instead of the
+ * whole width, with the same result (the products it skips are zeros).
  */
 int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
                       int64_t M, int64_t N, int64_t K, int64_t n_seg, const int64_t* seg_col0, void* const* seg_c,
                       const int64_t* seg_ldc, const void* lora_p, int64_t ld_p, const void* lora_q, int64_t ld_q,
-                      int64_t r, float alpha, int64_t layout, void* stream);
+                      int64_t r, const int64_t* seg_rcol, float alpha, int64_t layout, void* stream);
 
 /*
  * Bytes of workspace mxfp8_gemm_nt uses for this shape with MXFP8_GEMM_WIDE on the current device (0: no

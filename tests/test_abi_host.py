@@ -124,13 +124,19 @@ def test_argument_checks_reject_before_launch(lib):
     cols = (ctypes.c_int64 * 2)(0, 100)
     ptrs = (ctypes.c_void_p * 2)(16, 16)
     lds = (ctypes.c_int64 * 2)(128, 128)
-    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, None, 0, None, 0, 0, 1.0, 0,
-                                 None) == -1
+    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, None, 0, None, 0, 0, None,
+                                 1.0, 0, None) == -1
     cols = (ctypes.c_int64 * 2)(0, 128)
-    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, None, 0, None, 0, 0, 1.0, 4,
-                                 None) == -1
-    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 5, cols, ptrs, lds, None, 0, None, 0, 0, 1.0, 0,
-                                 None) == -1
+    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, None, 0, None, 0, 0, None,
+                                 1.0, 4, None) == -1
+    assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 5, cols, ptrs, lds, None, 0, None, 0, 0, None,
+                                 1.0, 0, None) == -1
+    # per-segment rank columns: a multiple of 8, inside ld_p and ld_q
+    for bad in ((0, 20), (0, 24)):
+        rc = (ctypes.c_int64 * 2)(*bad)
+        assert lib.mxfp8_gemm_nt_seg(p, p, 128, p, p, 128, 4, 256, 128, 2, cols, ptrs, lds, p, 32, p, 32, 16, rc,
+                                     1.0, 0, None) == -1
+        assert b"rank columns" in lib.mxfp8_last_error()
     # SwiGLU: n % 8, aligned
     assert lib.mxfp8_swiglu(p, p, 12, p, None) == -1
     assert lib.mxfp8_swiglu_bwd(p, p, p, 16, p, ctypes.c_void_p(18), None) == -1

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT, GEMM_B_PI = 1, 2, 4, 8, 16  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -32,7 +32,7 @@ SIGNATURES = {
                               _ptr, _ptr, _ptr, _ptr],
     "mxfp8_gemm_swiglu_bwd": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64] + [_ptr] * 11 + [_i64, _f32, _f32] + [_ptr] * 7,
     "mxfp8_gemm_nt_seg": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr, _ptr, _i64,
-                          _ptr, _i64, _i64, _f32, _i64, _ptr],
+                          _ptr, _i64, _i64, _ptr, _f32, _i64, _ptr],
     "mxfp8_mlp_fwd_groups": [_i64, _i64, _i64],
     "mxfp8_mlp_fwd": [_ptr, _ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _i64, _ptr, _i64,
                       _ptr],
@@ -210,9 +210,10 @@ def gemm_nt(a, sa, lda, b, sb, ldb, M, N, K, c, lora=None, alpha=1.0, split=True
          _p(q), ldq, r, float(alpha), layout, _p(ws), ws_bytes, like=c)
 
 
-def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, layout=0):
+def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, layout=0, lora_cols=None, r=None):
     """gemm_nt with the N output columns split over `outs` (1..4 bf16 [M, n_k] matrices, any row stride; the widths
-    sum to N, each a multiple of 128)."""
+    sum to N, each a multiple of 128).  lora_cols (one per output) with rank r: output k adds the rank-r product
+    over columns lora_cols[k] .. + r of P and Q instead of all of them."""
     n = len(outs)
     col0, c0 = [], 0
     for o in outs:
@@ -226,10 +227,11 @@ def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, lay
         ldp = ldq = r = 0
     else:
         p, q = lora
-        r = p.shape[1]
+        r = p.shape[1] if lora_cols is None else r
         ldp, ldq = p.stride(0), q.stride(0)
+    rcols = None if lora_cols is None else (ctypes.c_int64 * n)(*lora_cols)
     call("mxfp8_gemm_nt_seg", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, n, cols, ptrs, lds, _p(p), ldp, _p(q),
-         ldq, r, float(alpha), layout, like=outs[0])
+         ldq, r, rcols, float(alpha), layout, like=outs[0])
 
 
 def gemm_swiglu_fwd(a, sa, b, sb, M, N, K, xs, bg, bu, ad, s_g, s_u, gu, q_h, s_h, part):

@@ -159,6 +159,7 @@ struct CSeg {
   int col0[4];
   int64_t ld[4];
   uint16_t* ptr[4];
+  int rcol[4];  // first column of P and Q of the segment's rank-r product (0 unless mxfp8_gemm_nt_seg sets it)
 };
 
 // Launch plan (computed on the host, see make_plan).
@@ -741,6 +742,8 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   uint16_t* const C = cseg.ptr[sg];
   const int64_t ldc = cseg.ld[sg];
   const int ncol0 = cseg.col0[sg];
+  const uint16_t* const lp = lora.p + cseg.rcol[sg];  // the segment's rank-r columns of P and Q
+  const uint16_t* const lq = lora.q + cseg.rcol[sg];
   // epilogue: lane holds row m = m0 + wm*64 + mt*32 + lane%32 and columns n0 + wn*128 + nt*32 + g*8 +
   // (lane/32)*4 + 0..3 in acc[nt][mt][4g .. 4g+3]; with B in the pi_col order (b_pi) the 16 contiguous columns
   // n0 + wn*128 + nt*32 + (lane/32)*16 + i in acc[nt][mt][i].
@@ -753,7 +756,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
     const int nr = min(n0 + wn * 128 + nt * 32 + (b_pi ? pi_col(lane & 31) : (lane & 31)), N - 1);
 #pragma unroll
     for (int h = 0; h < kH; ++h)
-      dst[h] = *reinterpret_cast<const v8bf*>(lora.q + (int64_t)nr * lora.ld_q + h * 16 + (lane >> 5) * 8);
+      dst[h] = *reinterpret_cast<const v8bf*>(lq + (int64_t)nr * lora.ld_q + h * 16 + (lane >> 5) * 8);
   };
   if constexpr (kR > 0) {
 #pragma unroll
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
       const int mc = min(m0 + wm * 64 + mt * 32 + (lane & 31), M - 1);
 #pragma unroll
       for (int h = 0; h < kH; ++h)
-        pf[mt][h] = *reinterpret_cast<const v8bf*>(lora.p + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8);
+        pf[mt][h] = *reinterpret_cast<const v8bf*>(lp + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8);
     }
     load_q(0, qf[0]);
   }
@@ -965,8 +968,8 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
 extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, const void* b, const void* sb,
                                  int64_t ldb, int64_t M, int64_t N, int64_t K, int64_t n_seg, const int64_t* seg_col0,
                                  void* const* seg_c, const int64_t* seg_ldc, const void* lora_p, int64_t ld_p,
-                                 const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
-                                 void* stream) {
+                                 const void* lora_q, int64_t ld_q, int64_t r, const int64_t* seg_rcol, float alpha,
+                                 int64_t layout, void* stream) {
   MX_CHECK_ARG(n_seg >= 1 && n_seg <= 4 && seg_col0 && seg_c && seg_ldc, "mxfp8_gemm_nt_seg: 1 to 4 segments");
   MX_CHECK_ARG(!(layout & (MXFP8_GEMM_WIDE | MXFP8_GEMM_C_FT | MXFP8_GEMM_B_PI)),
                "mxfp8_gemm_nt_seg: segments take the 4-wave shape, row-major C and B in row order");
@@ -981,6 +984,12 @@ extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, con
     cs.col0[k] = (int)c0;
     cs.ptr[k] = (uint16_t*)seg_c[k];
     cs.ld[k] = seg_ldc[k];
+    if (seg_rcol && lora_p) {
+      MX_CHECK_ARG(seg_rcol[k] >= 0 && seg_rcol[k] % 8 == 0 && seg_rcol[k] + r <= ld_p && seg_rcol[k] + r <= ld_q,
+                   "mxfp8_gemm_nt_seg: segment %lld: rank columns must be a multiple of 8 within ld_p and ld_q",
+                   (long long)k);
+      cs.rcol[k] = (int)seg_rcol[k];
+    }
   }
   return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, ld_p, lora_q, ld_q, r, alpha, layout, nullptr, 0,
                    stream);

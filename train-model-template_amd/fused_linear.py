@@ -283,7 +283,14 @@ def _fwd_merged(spec, Bs, xS, codes, T, dt, skey):
     else:
         Q = _cast(skey + ("qcat", tuple(spec.mx), rp), block_diagonal_b)
     outs = [torch.empty((T, n), dtype=dt, device=xS.device) for n in widths]
-    mxfp8.mx_mm_seg(codes[0], codes[1], op[0], op[1], outs, lora=(xS, Q), alpha=alpha, layout=3, m=T)
+    # every layer with an adapter of one width: each output tile takes the rank-width window of xS and Q at its
+    # layer's own columns (the rest of its Q row is zero) instead of all rp columns
+    ranks = {sl.width for sl in slots if sl is not None}
+    if all(sl is not None for sl in slots) and len(ranks) == 1 and ranks <= {16, 32, 64}:
+        cols = dict(lora_cols=[sl.col for sl in slots], r=ranks.pop())
+    else:
+        cols = {}
+    mxfp8.mx_mm_seg(codes[0], codes[1], op[0], op[1], outs, lora=(xS, Q), alpha=alpha, layout=3, m=T, **cols)
     return dict(zip(spec.mx, outs))
 
 

@@ -215,9 +215,10 @@ def dequant(q, s, shape):
 GEMM_EVENTS = None  # set to a list to record (start event, end event, flops) around every MX GEMM launch
 
 
-def mx_mm_seg(q, s, wq, ws, outs, lora=None, alpha=1.0, layout=0, m=None):
+def mx_mm_seg(q, s, wq, ws, outs, lora=None, alpha=1.0, layout=0, m=None, lora_cols=None, r=None):
     """mx_mm whose N output columns go to the separate [M, n_k] tensors `outs` (consecutive column ranges, each a
-    multiple of 128 wide); 4-wave shape, row-major outputs."""
+    multiple of 128 wide); 4-wave shape, row-major outputs.  lora_cols / r: output k's rank-r window of the LoRA
+    operands (mxfp8_gemm_nt_seg's seg_rcol)."""
     M, K = q.shape
     if m is not None:
         M = m
@@ -229,7 +230,7 @@ def mx_mm_seg(q, s, wq, ws, outs, lora=None, alpha=1.0, layout=0, m=None):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
         _native.gemm_nt_seg(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, outs, lora=lora, alpha=alpha,
-                            layout=layout)
+                            layout=layout, lora_cols=lora_cols, r=r)
         if ev is not None:
             e1.record()
             ev.append((e0, e1, 2 * M * N * K))
