@@ -132,10 +132,25 @@ __device__ __forceinline__ uint32_t encode4_bf16(uint32_t w0, uint32_t w1, uint3
   return c;
 }
 
-// Unsigned max over a 4-lane group (the 4 lanes that share one 32-element block).
+// The pair {v[l], v[l ^ 32]} (pair32) or {v[l], v[l ^ 16]} (pair16) in every lane l, in either order, from one
+// v_permlane32_swap / v_permlane16_swap of v with itself: it exchanges rows of 16 lanes between its two
+// operands in the VALU, where __shfl_xor goes through LDS (ds_bpermute) and a wait on its return.
+__device__ __forceinline__ void pair32(uint32_t v, uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  a = r[0];
+  b = r[1];
+}
+__device__ __forceinline__ void pair16(uint32_t v, uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  a = r[0];
+  b = r[1];
+}
+
+// Unsigned max over a 4-lane group (the 4 lanes that share one 32-element block), by DPP quad permutations in
+// the VALU (lane l ^ 1: quad_perm 1,0,3,2; lane l ^ 2: quad_perm 2,3,0,1).  Every lane of the wave must be active.
 __device__ __forceinline__ uint32_t quad_umax(uint32_t v) {
-  v = max(v, (uint32_t)__shfl_xor((int)v, 1));
-  v = max(v, (uint32_t)__shfl_xor((int)v, 2));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));
   return v;
 }
 
@@ -225,9 +240,9 @@ __device__ __forceinline__ uint32_t quant16_codes(const uint32_t* w, uint4& c) {
   u16x2 mm = {0, 0};
 #pragma unroll
   for (int k = 0; k < 8; ++k) mm = absmax2(mm, w[k]);
-  uint32_t am = amax_bits(mm);
-  am = max(am, (uint32_t)__shfl_xor((int)am, 32));
-  const uint32_t e = e8m0_from_amax_bits(am);
+  uint32_t a, b;
+  pair32(amax_bits(mm), a, b);  // the partner lane l ^ 32 holds the block's other 16 values
+  const uint32_t e = e8m0_from_amax_bits(max(a, b));
   c = make_uint4(encode4_bf16(w[0], w[1], e), encode4_bf16(w[2], w[3], e), encode4_bf16(w[4], w[5], e),
                  encode4_bf16(w[6], w[7], e));
   return e;

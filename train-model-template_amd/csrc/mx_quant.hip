@@ -90,8 +90,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(6, 8))
       u16x2 m = {0, 0};
 #pragma unroll
       for (int k = 0; k < 8; ++k) m = absmax2(m, word(v[k], p));
-      m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, __shfl_xor(__builtin_bit_cast(int, m), 16)));
-      m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, __shfl_xor(__builtin_bit_cast(int, m), 32)));
+      uint32_t pa, pb;
+      pair16(__builtin_bit_cast(uint32_t, m), pa, pb);
+      m = __builtin_elementwise_max(__builtin_bit_cast(u16x2, pa), __builtin_bit_cast(u16x2, pb));
+      pair32(__builtin_bit_cast(uint32_t, m), pa, pb);
+      m = __builtin_elementwise_max(__builtin_bit_cast(u16x2, pa), __builtin_bit_cast(u16x2, pb));
       const uint32_t e0 = e8m0_from_amax_bits((uint32_t)m.x << 16), e1 = e8m0_from_amax_bits((uint32_t)m.y << 16);
       const uint32_t w0 = word(v[0], p), w1 = word(v[1], p), w2 = word(v[2], p), w3 = word(v[3], p);
       const uint32_t w4 = word(v[4], p), w5 = word(v[5], p), w6 = word(v[6], p), w7 = word(v[7], p);
