@@ -95,7 +95,7 @@ int mxfp8_dequant(const void* q, int64_t rows, int64_t cols, int64_t ld_q, const
  * :283, :309, :329).
  * Optional rank-r epilogue (lora_p != NULL), replacing the addmm_ that follows (fused_mlp.py:284, :331):
  *   C = bf16( bf16(A·Bᵀ) + alpha * P[M, r] · Q[N, r]ᵀ ),  P, Q bf16 with row strides ld_p, ld_q,
- *   r in {16, 32, 64}.
+ *   r in {16, 32, 48, 64}.
  * Requires K % 128 == 0, N % 128 == 0, lda/ldb % 16 == 0, ldc % 4 == 0.
  * layout bits: MXFP8_GEMM_A_TILED = A codes in the MX-tiled layout (mxfp8_quant_tiled / mxfp8_tile_codes,
  * lda ignored), MXFP8_GEMM_B_TILED = the same for B (results are bit-identical to row-major operands; the

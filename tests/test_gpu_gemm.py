@@ -83,19 +83,24 @@ def test_gemm_strided_weight_half(gpu):
     _assert_close(dx, _ref_gemm_f64(qd, sd, qtr, str_, T, K, N))
 
 
-@pytest.mark.parametrize("r", [16, 32])
+@pytest.mark.parametrize("r", [16, 32, 48, 64])
 def test_gemm_lora_epilogue(r, gpu):
-    # C = bf16(bf16(A·Bᵀ) + alpha · P·Qᵀ): the y.addmm_(xsd, bdᵀ, alpha=s_d) of fused_mlp.py:284
+    # C = bf16(bf16(A·Bᵀ) + alpha · P·Qᵀ): the y.addmm_(xsd, bdᵀ, alpha=s_d) of fused_mlp.py:284.  P and Q are the
+    # first r columns of 64-wide buffers whose other columns hold NaN: the epilogue must read exactly r columns
     g = torch.Generator().manual_seed(r)
     M, N, K = 300, 1024, 512
     a = torch.randn(M, K, generator=g).to(torch.bfloat16).to(gpu)
     b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
     P = torch.randn(M, r, generator=g).to(torch.bfloat16)
     Q = (torch.randn(N, r, generator=g) * 0.5).to(torch.bfloat16)
+    Pw = torch.full((M, 64), float("nan"), dtype=torch.bfloat16)
+    Qw = torch.full((N, 64), float("nan"), dtype=torch.bfloat16)
+    Pw[:, :r], Qw[:, :r] = P, Q
     qa, sa = mxfp8.mx_quant(a)
     qb, sb = mxfp8.mx_quant(b)
     c0 = mxfp8.mx_mm(qa, sa, qb, sb)
-    c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P.to(gpu), Q.to(gpu)), alpha=2.0)
+    c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(Pw.to(gpu)[:, :r], Qw.to(gpu)[:, :r]), alpha=2.0)
+    assert bool(torch.isfinite(c).all())
     ref = (c0.float().cpu() + 2.0 * (P.float() @ Q.float().t())).to(torch.bfloat16).float()
     err = (c.float().cpu() - ref).abs()
     assert (err <= ref.abs() * 2.0 ** -7 + 1e-4).all(), err.max()

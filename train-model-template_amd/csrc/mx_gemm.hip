@@ -879,6 +879,7 @@ void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, 
   if (!lo.p) gemm_kernel<0, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 16) gemm_kernel<16, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 32) gemm_kernel<32, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
+  else if (r == 48) gemm_kernel<48, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else gemm_kernel<64, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
 #undef GEMM_ARGS
 }
@@ -922,7 +923,8 @@ int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const v
   MX_CHECK_ARG(workspace_bytes >= 0 && (workspace_bytes == 0 || (workspace && mx_aligned(workspace, 256))),
                "mxfp8_gemm_nt: workspace must be 256-byte aligned");
   if (lora_p) {
-    MX_CHECK_ARG(lora_q && (r == 16 || r == 32 || r == 64), "mxfp8_gemm_nt: epilogue needs P, Q and r in {16, 32, 64}");
+    MX_CHECK_ARG(lora_q && (r == 16 || r == 32 || r == 48 || r == 64),
+                 "mxfp8_gemm_nt: epilogue needs P, Q and r in {16, 32, 48, 64}");
     MX_CHECK_ARG(ld_p >= r && ld_q >= r && ld_p % 8 == 0 && ld_q % 8 == 0 && mx_aligned(lora_p, 16) &&
                      mx_aligned(lora_q, 16),
                  "mxfp8_gemm_nt: bad epilogue strides/alignment");

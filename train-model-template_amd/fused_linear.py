@@ -487,8 +487,12 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
     n_cols = spec.adapter_cols + (sum(sl.width for sl in spec.thin) if need_x else 0)
     native = n_cols > 0 and _native_ok(x2, dt, n_cols) and not spec.plain
     width = _rp(n_cols) if native else n_cols
+    # the dx GEMM's rank-r epilogue reads only the n_cols used columns of dS and St when n_cols is a rank it
+    # takes (q|k|v at r = 16: 48), so the padding of dS stays unwritten; the token reduction's rows past n_cols,
+    # computed from it, are dropped
+    r_dx = n_cols if n_cols in (16, 32, 48, 64) else width
     dS = torch.empty((T, width), dtype=dt, device=dev) if n_cols else None
-    if native and width > n_cols:
+    if native and r_dx > n_cols:
         dS[:, n_cols:].zero_()
     grads = [None] * (2 * len(spec.adapters))
     q = sbuf = None
@@ -546,7 +550,7 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
                 St = forms.St
             else:
                 St = _cast(skey + ("padT", width), lambda: _s_pad(S, skey, width).t().contiguous())
-            dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=(dS, St), alpha=1.0)
+            dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=(dS[:, :r_dx], St[:, :r_dx]), alpha=1.0)
         else:
             dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay)
             for i in spec.plain:  # plain bf16 linears (neither MX nor thin)
