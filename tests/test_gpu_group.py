@@ -337,3 +337,63 @@ def test_weight_forms_follow_in_place_updates_and_new_parameters(gpu):
     replaced = step(fresh=False)
     assert not torch.equal(replaced[1], updated[1])
     same(replaced, step(fresh=True))
+
+
+def test_group_mixed_ranks(gpu):
+    # q and v at rank 16, k at rank 32 (S 64 rows): the merged forward GEMM cannot take one rank window per
+    # layer and runs its block-diagonal epilogue over all 64 columns, bit-identical to one GEMM per layer; the
+    # grouped backward matches the plain per-layer backward within tolerance
+    import mxfp8
+    g = torch.Generator().manual_seed(40)
+    m = _Model.__new__(_Model)
+    nn.Module.__init__(m)
+    m.model = nn.Module()
+    layer = nn.Module()
+    attn = nn.Module()
+
+    def lin(n_out, n_in):
+        x = nn.Linear(n_in, n_out, bias=False)
+        with torch.no_grad():
+            x.weight.copy_(torch.randn(n_out, n_in, generator=g) * 0.03)
+        x.weight.requires_grad_(False)
+        return x
+
+    for name, n, r in (("q_proj", NQ, 16), ("k_proj", NKV, 32), ("v_proj", NKV, 16)):
+        setattr(attn, name, workloads.LoraLinear(lin(n, K), torch.randn(r, K, generator=g) * 0.03,
+                                                 torch.randn(n, r, generator=g) * 0.03, ALPHA))
+        getattr(attn, name).base_layer.to(dtype=torch.bfloat16)
+    layer.self_attn = attn
+    m.model.layers = nn.ModuleList([layer])
+    m = m.to(gpu)
+    mxfp8.enable_mxfp8(m)
+    mods = [attn.q_proj, attn.k_proj, attn.v_proj]
+    x = (torch.randn(T, K, generator=g)).to(torch.bfloat16).to(gpu)
+    dys = [(torch.randn(T, n, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for n in (NQ, NKV, NKV)]
+
+    fused_linear.new_step()
+    merged = [o.clone() for o in fused_linear.group_linear(x, mods)]
+    saved = mxfp8.group_fwd_operand
+    mxfp8.group_fwd_operand = lambda lins: None  # one GEMM per layer
+    try:
+        fused_linear.new_step()
+        single = fused_linear.group_linear(x, mods)
+    finally:
+        mxfp8.group_fwd_operand = saved
+    for u, v in zip(merged, single):
+        assert torch.equal(u, v)
+
+    def run():
+        fused_linear.new_step()
+        for p in m.parameters():
+            p.grad = None
+        xg = x.clone().requires_grad_(True)
+        torch.autograd.backward(fused_linear.group_linear(xg, mods), dys)
+        return xg.grad, [p.grad.clone() for p in m.parameters() if p.requires_grad]
+
+    dxf, gf = run()
+    for mod in mods:
+        mod.base_layer._mx_fbwd = False
+    dxp, gp = run()
+    _close(dxf, dxp.double().cpu(), "dx")
+    for k, (a, b) in enumerate(zip(gf, gp)):
+        _close(a, b.double().cpu(), f"grad {k}")
