@@ -182,19 +182,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPe
 //     dxa_g | dxa_u | xS_down products D[ρ][m] over the tile's columns (MFMA, k = columns), summed over the
 //     quad's 4 waves in LDS (fixed order) and stored (first quad) or added (later quads) into the column
 //     group's [T, 3r] partial;
-//     dB_g, dB_u, dA_dᵀ contributions D[j][ρ] (16x16x32 MFMA, k = rows): the wave writes its dg, du, h rows
-//     to LDS and reads them back column-wise with ds_read_b64_tr_b16; accumulated over the super-block in
-//     registers and stored after it.
+//     dB_g, dB_u, dA_dᵀ contributions D[j][ρ] (16x16x32 MFMA, k = rows): the wave writes its dg, then du,
+//     then h rows to its LDS tile and reads each back column-wise with ds_read_b64_tr_b16; accumulated over
+//     the super-block in registers and stored after it.
 // The large operands of the next row block (gu, dhm) are loaded one row block ahead; the small per-row
 // operands (xs, dxd and their transposed copies, L2-resident) are issued first in each row block, so waiting
 // for them leaves the prefetch in flight.  Rows past T quantize row T - 1 again (the same bytes) and then
 // zero their values, so they add nothing to dB / dA_d.
 // Register budget: two waves per SIMD (<= 256 VGPRs; with three the kernel spills), i.e. two workgroups per
-// CU (the LDS, 52 KB at r = 16, would allow three).
+// CU (58 KB of LDS each at r = 16).
 // kQ = 2: 8 waves, two quads side by side (wave w on tile 8o + w of the column group): the dxa products are
 // summed over all 8 waves in LDS, so there is one partial per 256 columns instead of per 128 (half the partial
-// bytes written here and read by the finish); one workgroup per CU (105 KB of LDS at r = 16), still two waves
-// per SIMD.
+// bytes written here and read by the finish); one workgroup per CU (116 KB of LDS at r = 16), still two waves
+// per SIMD.  With two product buffers (r = 16) one barrier per row block replaces two: 1-4% faster alone
+// (151.9-154.7 against 148.9-152.4 us at configuration 3, three alternating pairs on one box, bit-identical).
 // gu is read once here, with non-temporal loads, so it does not push dhm (written by the GEMM just before) and
 // the MX(dg | du) codes out of the last-level cache (with the gate|up epilogue's non-temporal gu stores, MX_NT_GU
 // in mx_gemm.hip: 10-17 us per configuration-3 step faster over five A/B pairs on one box).
@@ -211,8 +212,13 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
     float* __restrict__ dxa_part, float* __restrict__ dbg_part, float* __restrict__ dbu_part,
     float* __restrict__ dad_part, uint16_t* __restrict__ dgu_out, bool q_tiled, bool gu_ft) {
   constexpr int kW = 4 * kQ, kCols = 128 * kQ;  // waves, columns per pass over the column group
-  __shared__ float red[kW][32][3 * R + 1];                              // per-wave dxa | dxa_u | xS products
-  __shared__ __attribute__((aligned(16))) uint16_t trt[kW][3][32 * kTrLd];  // per-wave dg, du, h rows
+  // kRB buffers of the per-wave products: with two, row block b fills buffer b % 2 while the waves still sum
+  // block b - 1's, so one barrier per row block suffices; taken where they fit the LDS of the workgroups a CU
+  // holds now (one with 8 waves, two with 4)
+  constexpr int kRedBytes = kW * 32 * (3 * R + 1) * 4, kTrBytes = kW * 32 * kTrLd * 2;
+  constexpr int kRB = 2 * kRedBytes + kTrBytes <= (kQ == 2 ? 160 : 80) * 1024 ? 2 : 1;
+  __shared__ float red[kRB][kW][32][3 * R + 1];                        // per-wave dxa | dxa_u | xS products
+  __shared__ __attribute__((aligned(16))) uint16_t trt[kW][32 * kTrLd];  // per-wave dg, then du, then h rows
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int r0 = blockIdx.x * SB, r1 = min(r0 + SB, Tpad);
   const int c0 = blockIdx.y * CG;
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
 #endif
       load16_rc(dhm, mc, jb + lg * 16, N, gu_ft, in.d);
     };
-    auto block = [&](int rb, const RowIn& cur, RowIn& nxt) {
+    auto block = [&](int rb, const RowIn& cur, RowIn& nxt, const int buf) {
       const int m = rb + (lane & 31);
       const bool live = m < T;
       const int mc = live ? m : T - 1;
@@ -345,7 +351,7 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int rr = tile_col(i, lane);
-          if (rr < R) red[w][lane & 31][rr] = p[i];
+          if (rr < R) red[buf][w][lane & 31][rr] = p[i];
         }
         p = v16f{};
 #pragma unroll
@@ -353,7 +359,7 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int rr = tile_col(i, lane);
-          if (rr < R) red[w][lane & 31][R + rr] = p[i];
+          if (rr < R) red[buf][w][lane & 31][R + rr] = p[i];
         }
         p = v16f{};
 #pragma unroll
@@ -361,46 +367,48 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int rr = tile_col(i, lane);
-          if (rr < R) red[w][lane & 31][2 * R + rr] = p[i];
+          if (rr < R) red[buf][w][lane & 31][2 * R + rr] = p[i];
         }
       }
       // dB_g, dB_u, dA_dᵀ: D[j][ρ] += Σ_m dg[m, j] xs_g[m, ρ] etc. over the 32 rows (one k = 32 step)
-      tr_store(trt[w][0], lane, dgw);
-      tr_store(trt[w][1], lane, duw);
-      tr_store(trt[w][2], lane, hw);
+      // one transpose tile per wave, refilled three times: a wave's LDS operations run in order, so each store
+      // follows the reads of the tile's previous contents
+      auto tr_pass = [&](const uint32_t* vals, const v8bf* tf, v4f (*acc)[R / 16]) {
+        tr_store(trt[w], lane, vals);
 #pragma unroll
-      for (int jh = 0; jh < 2; ++jh) {
-        const v8bf ag = tr_operand(trt[w][0], jh * 16, lane);
-        const v8bf au = tr_operand(trt[w][1], jh * 16, lane);
-        const v8bf ah = tr_operand(trt[w][2], jh * 16, lane);
+        for (int jh = 0; jh < 2; ++jh) {
+          const v8bf a = tr_operand(trt[w], jh * 16, lane);
 #pragma unroll
-        for (int h = 0; h < R / 16; ++h) {
-          dbg[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ag, tg[h], dbg[jh][h], 0, 0, 0);
-          dbu[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(au, tu[h], dbu[jh][h], 0, 0, 0);
-          dad[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, td[h], dad[jh][h], 0, 0, 0);
+          for (int h = 0; h < R / 16; ++h) acc[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, tf[h], acc[jh][h], 0, 0, 0);
         }
-      }
-      // sum the 4 waves' products (fixed order) into the quad's own partial (stores only: a read-modify-write
+      };
+      tr_pass(dgw, tg, dbg);
+      tr_pass(duw, tu, dbu);
+      tr_pass(hw, td, dad);
+      // sum the waves' products (fixed order) into the pass's own partial (stores only: a read-modify-write
       // here would wait behind the next row block's prefetch, the memory counter completing in order)
       __syncthreads();
       float* qpart = dxa_part + ((int64_t)(blockIdx.y * (CG / kCols) + oc) * T + rb) * 3 * R;
       for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 256 * kQ) {
         const int mm = idx / (3 * R), cc = idx % (3 * R);
-        float v = red[0][mm][cc];
+        float v = red[buf][0][mm][cc];
 #pragma unroll
-        for (int u = 1; u < kW; ++u) v += red[u][mm][cc];
+        for (int u = 1; u < kW; ++u) v += red[buf][u][mm][cc];
         if (rb + mm < T) qpart[idx] = v;
       }
-      __syncthreads();
+      if (kRB == 1) __syncthreads();  // the next row block refills the same buffer
     };
     RowIn b0, b1;  // alternating buffers: no register copies between row blocks
     fetch(r0, b0);
     int rb = r0;
     for (; rb + 32 < r1; rb += 64) {
-      block(rb, b0, b1);
-      block(rb + 32, b1, b0);
+      block(rb, b0, b1, 0);
+      block(rb + 32, b1, b0, kRB - 1);
     }
-    if (rb < r1) block(rb, b0, b1);
+    if (rb < r1) {
+      block(rb, b0, b1, 0);
+      if (kRB == 2) __syncthreads();  // an odd count: the next pass's first row block refills buffer 0
+    }
     // dB partials of this super-block: D[j][ρ], lane l: ρ = 16 h + l % 16, j = jb + 16 jh + (l / 16) * 4 + i
 #pragma unroll
     for (int jh = 0; jh < 2; ++jh)
