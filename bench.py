@@ -295,6 +295,65 @@ def _grouped_linears(T, K, r, alpha, dev, steps=10):
             "note": "fwd+bwd of q|k|v (one group) and o_proj (deferred, residual_add) on q; seeded upstream grads"}
 
 
+def _unfused_mlp(T, K, N, r, dev, steps=10):
+    """The unfused MLP path (shared_prefix._mlp with fused_mlp off: gate|up as one group_linear, the SwiGLU
+    kernels, down as a group_linear), forward + backward per step on one configuration-3 layer, and the SwiGLU
+    kernels alone on [T, N] (graph timing; algorithmic bytes: g, u read and h written forward, g, u, dh read and
+    dg, du written backward).  FLOPs counted: the MX GEMMs only, 12·T·K·N as for the fused step."""
+    import torch
+
+    import _native
+    import fused_mlp
+    import mxfp8
+    import shared_prefix
+    import workloads
+    g = torch.Generator(device=dev).manual_seed(11)
+    G = torch.randn(T, N, device=dev, generator=g).to(torch.bfloat16)
+    U = torch.randn(T, N, device=dev, generator=g).to(torch.bfloat16)
+    D = (torch.randn(T, N, device=dev, generator=g) * 1e-2).to(torch.bfloat16)
+    H, DG, DU = torch.empty_like(G), torch.empty_like(G), torch.empty_like(G)
+    out = {}
+    for name, fn, by in (("swiglu fwd [T,N]", lambda: _native.swiglu(G, U, H), 6 * T * N),
+                         ("swiglu bwd [T,N]", lambda: _native.swiglu_bwd(G, U, D, DG, DU), 10 * T * N)):
+        ms, n = _time_graph(fn)
+        out[name] = _rate(by, ms, n)
+    del G, U, D, H, DG, DU
+    model, inps = workloads.build_model(3, T=T, layers=1, device=dev)
+    mxfp8.enable_mxfp8(model)
+    mlp = model.layers[0].mlp
+    x = inps[0]["x"].to(dev).requires_grad_(True)
+    dy = inps[0]["dy"].to(dev)
+    params = [p for p in mlp.parameters() if p.requires_grad]
+
+    def step():
+        y = shared_prefix._mlp(mlp, x)
+        y.backward(dy)
+        for p in params:
+            p.grad = None
+        x.grad = None
+
+    fused_mlp.ENABLED[0] = False
+    try:
+        before = fused_mlp.STATS.get("mlp gộp", 0)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        assert fused_mlp.STATS.get("mlp gộp", 0) == before  # the unfused path ran
+    finally:
+        fused_mlp.ENABLED[0] = True
+    ms = e0.elapsed_time(e1) / steps
+    del model, x, dy, params
+    out["unfused step"] = {"ms_per_step": round(ms, 4), "MX_GEMM_TFLOP/s": round(12 * T * K * N / (ms * 1e-3) / 1e12, 1),
+                           "note": "one configuration-3 layer through shared_prefix._mlp with the fused MLP off"}
+    return out
+
+
 def _copy_calib(dev):
     import torch
     src = torch.ones(COPY_CALIB_BYTES // 2, dtype=torch.bfloat16, device=dev)
@@ -595,7 +654,8 @@ def main():
         T, K, N = c["T"], c["K"], c["N"]
         print(json.dumps({"config": workloads.DESCRIPTIONS[cfg],
                           "lora_epilogues": _lora_epilogues(T, K, N, c["r"], dev),
-                          "grouped_linears": _grouped_linears(T, K, c["r"], c["alpha"], dev)}), flush=True)
+                          "grouped_linears": _grouped_linears(T, K, c["r"], c["alpha"], dev),
+                          "unfused_mlp": _unfused_mlp(T, K, N, c["r"], dev)}), flush=True)
         return
     model, inps = workloads.build_model(cfg, layers=c["layers"], device=dev)
     mxfp8.enable_mxfp8(model)
@@ -672,6 +732,7 @@ def main():
         line["quantizer"] = quant
         line["lora_epilogues"] = _lora_epilogues(T, K, N, c["r"], dev)
         line["grouped_linears"] = _grouped_linears(T, K, c["r"], c["alpha"], dev)
+        line["unfused_mlp"] = _unfused_mlp(T, K, N, c["r"], dev)
         tot = ms + wq_ms * c["layers"]
         line["with_requant"] = {"ms_per_step": round(tot, 4), "TFLOP/s": round(fl / (tot * 1e-3) / 1e12, 2),
                                 "weight_prep_ms_per_layer": round(wq_ms, 4)}
