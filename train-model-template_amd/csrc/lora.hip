@@ -589,14 +589,24 @@ __global__ __launch_bounds__(256, 2) void lora_bwd_batch_kernel(const LoraBwdBat
 __device__ __forceinline__ float4 add4(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
+// The partials are read once: streaming (non-temporal) loads.  The backward finish at configuration 3 (graph timing,
+// one box, three alternating pairs, bit-identical): 13.07-13.10 us with plain loads, 12.01-12.03 us with these;
+// lora_bwd's sums unchanged (23.7 / 57.9 us with the main kernel); eight loads in flight instead of four measured
+// the same.  (The forward's sum_parts kernel measured slower with them: 12.8 against 11.6 us.)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_part(const float4* p) {
+  const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(t.x, t.y, t.z, t.w);
+}
 __device__ __forceinline__ float4 sum_ordered(const float4* __restrict__ p, int64_t stride, int n) {
-  float4 v = p[0];
+  float4 v = ld_part(p);
   int c = 1;
   for (; c + 3 < n; c += 4) {
-    const float4 x0 = p[c * stride], x1 = p[(c + 1) * stride], x2 = p[(c + 2) * stride], x3 = p[(c + 3) * stride];
+    const float4 x0 = ld_part(p + c * stride), x1 = ld_part(p + (c + 1) * stride), x2 = ld_part(p + (c + 2) * stride),
+                 x3 = ld_part(p + (c + 3) * stride);
     v = add4(add4(add4(add4(v, x0), x1), x2), x3);
   }
-  for (; c < n; ++c) v = add4(v, p[c * stride]);
+  for (; c < n; ++c) v = add4(v, ld_part(p + c * stride));
   return v;
 }
 
