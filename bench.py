@@ -69,7 +69,7 @@ def _cpu_baseline(cfg, T_sample):
     import workloads
     from oracle import mlp as omlp
 
-    cores = len(os.sched_getaffinity(0))  # every core this process may run on (BASELINE.md §3)
+    cores = len(os.sched_getaffinity(0))  # every core this process may run on
     torch.set_num_threads(cores)
     inp = workloads.make_inputs(cfg, T=T_sample)
     W = omlp.prepare_weights(inp["Wg"], inp["Wu"], inp["Wd"])
