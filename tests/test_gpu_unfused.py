@@ -28,12 +28,13 @@ def _step_ok(got, ref64, frac_min=0.99):
     assert frac >= frac_min, frac
 
 
-def test_swiglu_kernels_match_float64(gpu):
+@pytest.mark.parametrize("shape", [(300, 1024), (37, 200)])  # whole blocks; a partial last block in both kernels
+def test_swiglu_kernels_match_float64(gpu, shape):
     g = torch.Generator().manual_seed(0)
-    G = (torch.randn(300, 1024, generator=g) * 3).to(torch.bfloat16)
+    G = (torch.randn(*shape, generator=g) * 3).to(torch.bfloat16)
     G[0, :8] = torch.tensor([0.0, -0.0, 88.0, -88.0, 100.0, -100.0, 1e-3, -1e-3])  # exp overflow, tiny, zero
-    U = torch.randn(300, 1024, generator=g).to(torch.bfloat16)
-    DH = (torch.randn(300, 1024, generator=g) * 0.1).to(torch.bfloat16)
+    U = torch.randn(*shape, generator=g).to(torch.bfloat16)
+    DH = (torch.randn(*shape, generator=g) * 0.1).to(torch.bfloat16)
     Gd, Ud = G.to(gpu).requires_grad_(True), U.to(gpu).requires_grad_(True)
     h = shared_prefix._SWIGLU(Gd, Ud)
     h.backward(DH.to(gpu))
