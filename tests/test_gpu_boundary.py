@@ -98,6 +98,41 @@ def test_cleared_cache_and_checkpoint_give_identical_gradients(gpu):
             assert torch.equal(a, b), kw
 
 
+def _two_layer_grads(gpu, hooks):
+    """x -> mlp(layer 0) -> mlp(layer 1) -> backward; LoRA gradients of both layers and dx.  hooks=True runs
+    under a saved-tensor hook whose unpack returns a fresh clone at every access, so each layer's backward sees
+    short-lived objects (whose addresses a later layer's clones may take) instead of the tensors forward saved."""
+    model, inps = workloads.build_model(2, T=256, layers=2, device=gpu)
+    mxfp8.enable_mxfp8(model)
+    fused_linear.new_step()
+    x = inps[0]["x"].to(gpu).requires_grad_(True)
+    ctx = (torch.autograd.graph.saved_tensors_hooks(lambda t: t, lambda t: t.clone()) if hooks
+           else torch.autograd.graph.saved_tensors_hooks(lambda t: t, lambda t: t))
+    with ctx:
+        h = fused_mlp.mlp(model.layers[0].mlp, x)
+        y = fused_mlp.mlp(model.layers[1].mlp, h)
+    y.backward(inps[0]["dy"].to(gpu))
+    torch.cuda.synchronize()
+    grads = [x.grad]
+    for layer in model.layers:
+        for name in ("gate_proj", "up_proj", "down_proj"):
+            lin = getattr(layer.mlp, name)
+            grads += [lin.lora_A["default"].weight.grad, lin.lora_B["default"].weight.grad]
+    return grads
+
+
+def test_cloning_unpack_hook_gives_identical_gradients(gpu):
+    """Two layers with distinct adapters: backward under a cloning unpack hook must find each layer's own
+    transposed LoRA forms (the per-step cache keeps its key tensors alive and checks object identity), so every
+    gradient is bit-identical to the run without the hook."""
+    g0 = _two_layer_grads(gpu, hooks=False)
+    g1 = _two_layer_grads(gpu, hooks=True)
+    for k, (a, b) in enumerate(zip(g0, g1)):
+        assert a is not None and torch.equal(a, b), k
+    # the two layers' adapters differ, so a lookup that returned the other layer's forms would change them
+    assert not torch.equal(g0[1], g0[7])
+
+
 def test_enable_disable_round_trip(gpu):
     model, inps = workloads.build_model(2, T=128, device=gpu)
     lins = [m for n, m in model.named_modules() if n.endswith("base_layer")]

@@ -200,7 +200,11 @@ def _forms_key(S, bg, bu, ad, bd, dt):
 def _forms_of_saved(S, bg, bu, ad, bd, dt):
     """The step's bf16 weight forms (_prep) looked up from the five tensors _MLP saves.  The forward registers
     them under the ids of those tensors; when the saved tensors come back as other objects (a saved-tensor
-    hook, e.g. checkpointing) or the cache was cleared, the transposed forms are rebuilt from the saved ones."""
+    hook, e.g. checkpointing) or the cache was cleared, the transposed forms are rebuilt from the saved ones.
+    Every entry keeps its five key tensors alive (`keep`), so no id in a live key can be reused by another
+    tensor within the step, and a hit is accepted only when those are the very objects passed in."""
+    keys = (S, bg, bu, ad, bd)
+
     def make():
         R = ad.shape[0]
         f = lambda t: t.float().contiguous()  # noqa: E731
@@ -209,8 +213,12 @@ def _forms_of_saved(S, bg, bu, ad, bd, dt):
         out = dict(S=e(2 * R, K), ST=e(K, 2 * R), bg=e(N, R), bu=e(N, R), bgT=e(R, N), buT=e(R, N), ad=e(R, N),
                    adT=e(N, R), bd=e(K, R), bdT=e(R, K))
         _native.lora_prep(f(S[:R]), f(S[R:]), f(bg), f(bu), f(ad), f(bd), out)
-        return types.SimpleNamespace(**out)
-    return _cast(_forms_key(S, bg, bu, ad, bd, dt), make)
+        return types.SimpleNamespace(keep=keys, **out)
+
+    lw = _cast(_forms_key(*keys, dt), make)
+    if len(lw.keep) != 5 or any(a is not b for a, b in zip(lw.keep, keys)):
+        return make()  # not reachable while entries hold their keys; never trust an id match alone
+    return lw
 
 
 # GEMM layout of the MLP's own products: both operands MX-tiled, output in the fused-tile layout
@@ -267,6 +275,7 @@ class _MLP(torch.autograd.Function):
             y = x2.new_empty(x2.shape[0], down.out_features)
         # the reference's saved set, the same in both modes (non-reentrant checkpointing compares metadata on
         # recompute); the transposed weight forms stay in the per-step cast cache, keyed by these tensors
+        lw.keep = (S, bg, bu, ad, bd)  # the entry holds its key tensors (see _forms_of_saved)
         _cast(_forms_key(S, bg, bu, ad, bd, dt), lambda: lw)
         ctx.save_for_backward(x2, xs, gu, S, bg, bu, ad, bd)
         ctx.meta = (hold, down, (s_g, s_u, s_d), dt, lead, K, x.dtype)
