@@ -397,3 +397,51 @@ def test_group_mixed_ranks(gpu):
     _close(dxf, dxp.double().cpu(), "dx")
     for k, (a, b) in enumerate(zip(gf, gp)):
         _close(a, b.double().cpu(), f"grad {k}")
+
+
+def _qkv_grads(m, x, dys):
+    return [x.grad] + [getattr(m.attn, n).lora_A["default"].weight.grad for n in ("q_proj", "k_proj", "v_proj")] + \
+        [getattr(m.attn, n).lora_B["default"].weight.grad for n in ("q_proj", "k_proj", "v_proj")]
+
+
+def test_backward_after_next_step_keeps_its_own_weights(gpu):
+    """A graph whose backward runs after the next step's new_step(), in-place parameter update and forward (a
+    retained graph, a deferred prefix backward) must use the weights of its own step, as the reference's per-step
+    bf16 copies do, although the group's weight forms live in a buffer that each step repacks (fused_linear._PLANS:
+    a pending reader makes the next step pack into a fresh buffer).  Reference: the same step 1 with its backward
+    run at once.  Bit-identical gradients."""
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(T, K, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    dys = [(torch.randn(T, n, generator=g) * 1e-2).to(torch.bfloat16).to(gpu) for n in (NQ, NKV, NKV)]
+    names = ("q_proj", "k_proj", "v_proj")
+
+    def forward(m):
+        xx = x.clone().requires_grad_(True)
+        return xx, fused_linear.group_linear(xx, [getattr(m.attn, n) for n in names])
+
+    def bump(m):  # an optimizer step: every adapter parameter changes in place, at the same address
+        with torch.no_grad():
+            for n in names:
+                for p in (getattr(m.attn, n).lora_A["default"].weight, getattr(m.attn, n).lora_B["default"].weight):
+                    p.mul_(1.5).add_(0.01)
+
+    m, _ = _build(gpu, seed=3)
+    xx, outs = forward(m)
+    torch.autograd.backward(list(outs), dys)
+    torch.cuda.synchronize()
+    want = [t.clone() for t in _qkv_grads(m, xx, dys)]
+
+    m, _ = _build(gpu, seed=3)
+    xx, outs = forward(m)       # step 1
+    fused_linear.new_step()
+    bump(m)
+    xx2, outs2 = forward(m)     # step 2 packs its forms while step 1's backward is pending
+    for n in names:
+        for p in (getattr(m.attn, n).lora_A["default"].weight, getattr(m.attn, n).lora_B["default"].weight):
+            p.grad = None
+    torch.autograd.backward(list(outs), dys)  # step 1's backward
+    torch.cuda.synchronize()
+    got = _qkv_grads(m, xx, dys)
+    for k, (a, b) in enumerate(zip(got, want)):
+        assert a is not None and torch.equal(a, b), k
+    del outs2, xx2

@@ -18,6 +18,7 @@ Layers that cannot be grouped (trainable base weights, DoRA, dropout > 0, severa
 """
 import dataclasses
 import os
+import weakref
 
 import torch
 from torch import nn
@@ -138,6 +139,11 @@ def _native_ok(x2, dt, n):
             and _vec_ok(x2))
 
 
+def _same_buffer(a, b):
+    """a and b are views of one allocation."""
+    return a.untyped_storage().data_ptr() == b.untyped_storage().data_ptr()
+
+
 def _s_pad(S, key, rp):
     """S zero-padded to rp rows (cached per step with the S it pads)."""
     return _cast(key + ("pad", rp), lambda: torch.cat([S, S.new_zeros(rp - S.shape[0], S.shape[1])]))
@@ -145,8 +151,12 @@ def _s_pad(S, key, rp):
 
 # The layout of a group's weight forms, kept across steps: the buffer, its views and the pack job table, keyed
 # by the addresses, shapes, strides and dtypes of the group's sources (the optimizer updates parameters in
-# place, at the same addresses).  Each step relaunches the pack into the same buffer; the previous step's
-# backward, earlier on the stream, has read it by then.
+# place, at the same addresses).  Each step relaunches the pack into the same buffer, unless a backward of an
+# earlier step may still read it: every forward saves its own views of the buffer and the plan keeps weak
+# references to them (`readers`); autograd drops saved tensors when that backward has run (or when its graph
+# dies), so a live reader at the next step's pack means a graph whose backward is still to come (a retained
+# graph, a deferred prefix backward, overlapped micro-batches), and that step packs into a fresh buffer
+# instead, leaving the pending backward the weights of its own step, as the reference's per-step copies do.
 _PLANS = {}
 _PLANS_MAX = 256
 
@@ -203,10 +213,15 @@ def _group_forms(spec, skey, K, dev):
                tuple(spec.parts[i][0].out_features for i in spec.mx),
                tuple((t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype) for t in srcs))
         plan = _PLANS.get(sig)
+        if plan is not None:
+            plan[0].readers[:] = [r for r in plan[0].readers if r() is not None]
+            if plan[0].readers:  # an earlier step's backward still reads this buffer: pack into a fresh one
+                plan = None
         if plan is None:
             if len(_PLANS) >= _PLANS_MAX:
                 _PLANS.clear()
             forms, jobs = _build_forms(spec, K, dev)
+            forms.readers = []
             plan = _PLANS[sig] = (forms, _native.pack_table(jobs))
         _native.pack_run(plan[1], like=plan[0].S_pad)
         return plan[0]
@@ -339,6 +354,7 @@ class _Group(torch.autograd.Function):
         src = spec.s_sources()
         skey = (tuple(id(t) for t in src), dt)
         codes = None
+        forms = None
         if _packable(spec, x2, dt):
             forms = _group_forms(spec, skey, K, x2.device)
             Bs, S = forms.Bs, forms.S
@@ -364,6 +380,9 @@ class _Group(torch.autograd.Function):
                     for i, p in enumerate(parts)]
         for sl in spec.thin:
             outs[sl.layer] = xS[:, sl.cols].contiguous()
+        if forms is not None:  # views of the persistent buffer: saved as views of their own, tracked (see _PLANS)
+            S, Bs = S.view(S.shape), [b.view(b.shape) for b in Bs]
+            forms.readers.append(weakref.ref(S))
         ctx.save_for_backward(x2, xS, S, *Bs)
         ctx.spec, ctx.skey, ctx.meta = spec, skey, (lead, K, dt, x.dtype)
         return tuple(y.view(*lead, y.shape[-1]) for y in outs)
@@ -545,11 +564,17 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
         codes = (q, sbuf.view(mxfp8.E8))
         if native:
             # bf16(bf16(MX GEMM) + dS·S): the reference's dx.addmm_(dS, S) in the GEMM epilogue
+            # this step's St only if the saved S is a view of the same buffer: a backward that runs after the next
+            # step's forward has the saved S of its own step (see _PLANS), so it builds St from that S
             forms = _CAST.get(skey + ("forms",))
-            if forms is not None and forms.rp == width:
+            if forms is not None and forms.rp == width and _same_buffer(S, forms.S_pad):
                 St = forms.St
             else:
-                St = _cast(skey + ("padT", width), lambda: _s_pad(S, skey, width).t().contiguous())
+                ent = _CAST.get(skey + ("padT", width))
+                if ent is None or ent[0] is not S:
+                    pad = torch.cat([S, S.new_zeros(width - S.shape[0], S.shape[1])]) if width > S.shape[0] else S
+                    ent = _CAST[skey + ("padT", width)] = (S, pad.t().contiguous())
+                St = ent[1]
             dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=(dS[:, :r_dx], St[:, :r_dx]), alpha=1.0)
         else:
             dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay)

@@ -242,12 +242,7 @@ class _MLP(torch.autograd.Function):
         # one read of x2: its MX operand (MX-tiled codes, the GEMM's operand layout; same codes and scales as
         # mx_quant) and xs = bf16(x2 · Sᵀ) [T, 2R] = xa_gate | xa_up, with the zero-padded transpose the backward
         # kernel reads
-        if 2 * R <= 32:
-            q, sc, xs, _ = mxfp8.mx_quant_lora(x2, S, out_t=False)
-        else:
-            xs = torch.empty((T, 2 * R), dtype=dt, device=x2.device)
-            _native.lora_nt(x2, S, xs)
-            q, sc = mxfp8.mx_quant_tiled(x2)
+        q, sc, xs, _ = mxfp8.mx_quant_lora(x2, S, out_t=False)  # 2R in {32, 64} (r in {16, 32}, _r_ok)
         if need_out and FUSED_EPILOGUE[0]:
             # one launch: gu = gate | up [T, 2N] (fused-tile layout, the saved tensor) and, in the GEMM's epilogue,
             # the LoRA-B of gate and up, h = silu(g)·u, MX(h) and the per-tile xS_down partials
