@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 10
+#define MXFP8_MLP_ABI_VERSION 11
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -230,6 +230,17 @@ int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q,
                      float scale, void* out, void* outT, int64_t Tpad, void* stream);
 
 /*
+ * mxfp8_quant_lora plus, in the same launch, tout [tc, Tpad] bf16 = txᵀ of tx [T, tc] bf16 (row stride ld_tx,
+ * 16-byte aligned rows), zero in columns T..Tpad-1: the bytes of mxfp8_transpose_pad(tx, T, tc, ld_tx, tout,
+ * Tpad), computed by workgroups of its own after the quantizer's.  The backward's first read of dy (mx_quant(dy2)
+ * and dxd, /root/reference/scripts/fused_mlp.py:309-313) with the transposed copy of the saved xs (:291) that the
+ * backward kernel takes as a matrix-instruction operand (see mxfp8_transpose_pad).  tc in {16, 32, 64}.
+ */
+int mxfp8_quant_lora_tp(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w, int64_t rp,
+                        float scale, void* out, void* outT, int64_t Tpad, const void* tx, int64_t ld_tx, int64_t tc,
+                        void* tout, void* stream);
+
+/*
  * out = bf16(x + bf16(y + scale * xa · Bᵀ)): x, y, out [T, N] bf16 (row stride N), xa [T, r] bf16 (row stride
  * ld_xa), B [N, r] bf16.  The LoRA-B addmm_ and the residual add of o_proj / out_proj in one pass; replaces res_lora /
  * _res_lora_kernel (/root/reference/scripts/mxfp8.py:265-293).  N % 128 == 0, r in {16, 32}, T * N < 2^31; x, y,
@@ -388,6 +399,31 @@ int64_t mxfp8_lora_tn_chunks(int64_t T, int64_t K);
  */
 int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, const void* p, int64_t rp, int64_t chunks,
                   float* part, float scale, int64_t transpose, int64_t out_f32, void* out, void* stream);
+
+/* One token reduction of mxfp8_lora_tn_batch: out = bf16(Σ_t p[t, ρ] x[t, k]) (then bf16(· scale)), as in
+ * mxfp8_lora_tn with the same arguments. */
+typedef struct {
+  const void* x;     /* [T, K] bf16, row stride ld_x (>= K, a multiple of 8), 16-byte aligned */
+  int64_t ld_x;
+  const void* p;     /* [T, rp] bf16, 16-byte aligned */
+  int64_t rp;        /* 16 or 32 */
+  float scale;
+  int64_t transpose; /* out [rp, K] (0) or [K, rp] (1) */
+  int64_t out_f32;   /* out holds fp32 values of the bf16 result (1) or bf16 (0) */
+  void* out;
+} mxfp8_lora_tn_job;
+
+#define MXFP8_LORA_TN_MAX_JOBS 4
+
+/*
+ * Up to MXFP8_LORA_TN_MAX_JOBS token reductions over the same T tokens and K columns in one launch, and their
+ * chunk sums in one more: every job's result is bit for bit mxfp8_lora_tn's with the same chunks.  part: scratch
+ * of chunks * (Σ rp over the jobs) * K floats (job j's partials after those of jobs 0..j-1).  Replaces the
+ * backward's dB_d = (dy2.t() @ xS_down).mul_(s_d) and dA = dxa.t() @ x2 (/root/reference/scripts/
+ * fused_mlp.py:316-318, :333), which both read a [T, K] activation after the backward kernel's sums.
+ */
+int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T, int64_t K, int64_t chunks,
+                        float* part, void* stream);
 
 /*
  * Allocation-free variant of mxfp8_lora_tn: same arguments without `chunks` / `part`, same result bit for bit as

@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 33, names
+    assert len(names) == 35, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -242,3 +242,37 @@ def test_outlier_config_contains_edge_blocks():
     k = torch.log2(amax[amax > 0] / 448.0)
     assert bool((k == torch.round(k)).any())  # blocks whose amax is exactly 448 * 2^k
     assert bool(torch.signbit(blocks[(amax == 0)]).any())  # a -0.0 block
+
+
+def test_job_structs_match_the_c_layout(tmp_path):
+    """The ctypes job tables (_native.LoraBwdJob, PackJob, LoraTnJob) against the header's structs as gcc lays them
+    out: every field's offset and the struct size, and the MAX_JOBS constants."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no gcc")
+    structs = {"mxfp8_lora_bwd_job": _native.LoraBwdJob, "mxfp8_pack_job": _native.PackJob,
+               "mxfp8_lora_tn_job": _native.LoraTnJob}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, ct in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in ct._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    for k in ("MXFP8_LORA_BWD_MAX_JOBS", "MXFP8_PACK_MAX_JOBS", "MXFP8_LORA_TN_MAX_JOBS"):
+        lines.append(f'  printf("const {k} %d\\n", {k});')
+    lines.append("  return 0;\n}\n")
+    src, exe = tmp_path / "layout.c", tmp_path / "layout"
+    src.write_text("\n".join(lines))
+    subprocess.run([gcc, "-std=c11", "-o", str(exe), str(src)], check=True)
+    got = {}
+    for ln in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        a, b, v = ln.split()
+        got[(a, b)] = int(v)
+    for cname, ct in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(ct), cname
+        for f, _ in ct._fields_:
+            assert got[(cname, f)] == getattr(ct, f).offset, (cname, f)
+    assert got[("const", "MXFP8_LORA_BWD_MAX_JOBS")] == _native.LORA_BWD_MAX_JOBS
+    assert got[("const", "MXFP8_PACK_MAX_JOBS")] == _native.PACK_MAX_JOBS
+    assert got[("const", "MXFP8_LORA_TN_MAX_JOBS")] == _native.LORA_TN_MAX_JOBS

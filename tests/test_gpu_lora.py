@@ -314,3 +314,54 @@ def test_lora_bwd_batch_matches_per_layer(T, Ns, R, with_q, gpu):
     for a, b in zip(db0, db1):
         err = ((a.double() - b.double()).abs().max() / b.double().abs().max()).item()
         assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("T,K,rp,C,scale", [(10752, 2048, 16, 32, 2.0), (300, 1024, 32, 64, 1.0), (1, 128, 16, 16, 1.0),
+                                            (129, 256, 64, 32, 0.5), (8896, 2048, 16, 32, 2.0)])
+def test_quant_lora_tp_matches_separate_launches(T, K, rp, C, scale, gpu):
+    """mxfp8_quant_lora_tp (the quantizer, its rank-rp product and the zero-padded transpose of another [T, C] tensor
+    from one launch) against mxfp8_quant_lora and mxfp8_transpose_pad run apart: every output byte identical."""
+    import numpy as np
+
+    import mxfp8
+    from oracle import mx
+    g = torch.Generator().manual_seed(T + K + rp + C)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn(rp, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    tx = torch.randn(T, C, generator=g).to(torch.bfloat16).to(gpu)
+    q, s, out, outT = mxfp8.mx_quant_lora(x, w, scale=scale)
+    tpad = -(-T // 128) * 128
+    txT = torch.empty((C, tpad), dtype=torch.bfloat16, device=gpu)
+    _native.transpose_pad(tx, txT)
+    q2, s2, out2, outT2, txT2 = mxfp8.mx_quant_lora_tp(x, w, tx, scale=scale)
+    live = lambda qq: mx.from_tiled(qq.view(torch.uint8).cpu().numpy().reshape(-1), T, K)  # noqa: E731
+    assert np.array_equal(live(q), live(q2))
+    assert torch.equal(s.view(torch.uint8), s2.view(torch.uint8))
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(outT.view(torch.int16), outT2.view(torch.int16))
+    assert torch.equal(txT.view(torch.int16), txT2.view(torch.int16))
+    assert torch.equal(txT2[:, :T].t(), tx) and int(torch.count_nonzero(txT2[:, T:])) == 0
+
+
+@pytest.mark.parametrize("T,K", [(10752, 2048), (300, 1024), (1, 128), (8896, 2048)])
+def test_lora_tn_batch_matches_single_calls(T, K, gpu):
+    """mxfp8_lora_tn_batch (the backward's dB_d and dA reductions in one launch, their chunk sums in one more)
+    against two mxfp8_lora_tn calls with the same chunking: bit-identical outputs, fp32 and bf16 holders, both
+    orientations, a scale and none."""
+    g = torch.Generator().manual_seed(T + K)
+    x0 = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    p0 = (torch.randn(T, 16, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    x1 = torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu)
+    p1 = (torch.randn(T, 32, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    chunks = _native.lora_tn_chunks(T, K)
+    for dt0, dt1 in ((torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32)):
+        a0 = torch.empty((K, 16), dtype=dt0, device=gpu)
+        a1 = torch.empty((32, K), dtype=dt1, device=gpu)
+        _native.lora_tn(x0, p0, a0, torch.empty(chunks * 16 * K, device=gpu), scale=2.0, transpose=True)
+        _native.lora_tn(x1, p1, a1, torch.empty(chunks * 32 * K, device=gpu), scale=1.0, transpose=False)
+        b0 = torch.empty_like(a0)
+        b1 = torch.empty_like(a1)
+        _native.lora_tn_batch([(x0, p0, b0, 2.0, True), (x1, p1, b1, 1.0, False)],
+                              torch.empty(chunks * 48 * K, device=gpu))
+        torch.cuda.synchronize()
+        assert torch.equal(a0, b0) and torch.equal(a1, b1), (dt0, dt1)

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT, GEMM_B_PI = 1, 2, 4, 8, 16  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -42,6 +42,8 @@ SIGNATURES = {
     "mxfp8_lora_prep": [_ptr] * 6 + [_i64, _i64, _i64] + [_ptr] * 10 + [_ptr],
     "mxfp8_lora_nt": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
     "mxfp8_quant_lora": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr],
+    "mxfp8_quant_lora_tp": [_ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr, _i64, _f32, _ptr, _ptr, _i64, _ptr, _i64, _i64,
+                            _ptr, _ptr],
     "mxfp8_res_lora": [_ptr, _ptr, _ptr, _i64, _ptr, _i64, _i64, _i64, _f32, _ptr, _ptr],
     "mxfp8_transpose_pad": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr],
     "mxfp8_pack_bf16": [_ptr, _i64, _ptr],
@@ -54,6 +56,7 @@ SIGNATURES = {
     "mxfp8_lora_bwd_batch_chunks": [_i64, _i64],
     "mxfp8_lora_bwd_batch": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
+    "mxfp8_lora_tn_batch": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc_chunks": [_i64, _i64, _i64],
     "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
@@ -289,6 +292,14 @@ def quant_lora(x, q, s, w, out, scale=1.0, outT=None):
          _p(outT), -(-T // 128) * 128, like=x)
 
 
+def quant_lora_tp(x, q, s, w, out, tx, tout, scale=1.0, outT=None):
+    """quant_lora(x, q, s, w, out, scale, outT) and, in the same launch, tout [C, Tpad] = txᵀ zero-padded
+    (transpose_pad of tx [T, C])."""
+    T, K = x.shape
+    call("mxfp8_quant_lora_tp", _p(x), T, K, x.stride(0), _p(q), _p(s), _p(w), w.shape[0], float(scale), _p(out),
+         _p(outT), -(-T // 128) * 128, _p(tx), tx.stride(0), tx.shape[1], _p(tout), like=x)
+
+
 def res_lora(x, y, xa, b, out, scale):
     """out = bf16(x + bf16(y + scale · xa · bᵀ)); x, y, out [T, N], xa [T, r] (row stride any), b [N, r]."""
     T, N = x.shape
@@ -326,6 +337,29 @@ def lora_tn(x, p, out, part, scale=1.0, transpose=False):
     chunks = part.numel() // (rp * K)
     call("mxfp8_lora_tn", _p(x), T, K, x.stride(0), _p(p), rp, chunks, _p(part), float(scale), int(transpose),
          int(out.dtype == torch.float32), _p(out), like=x)
+
+
+class LoraTnJob(ctypes.Structure):
+    """mxfp8_lora_tn_job of include/mxfp8_mlp.h."""
+    _fields_ = [("x", _ptr), ("ld_x", _i64), ("p", _ptr), ("rp", _i64), ("scale", _f32), ("transpose", _i64),
+                ("out_f32", _i64), ("out", _ptr)]
+
+
+LORA_TN_MAX_JOBS = 4
+
+
+def lora_tn_batch(jobs, part, chunks=None):
+    """lora_tn of every job [(x, p, out, scale, transpose)] (the same [T, K] for all) in one launch, plus one launch
+    of the chunk sums; chunks: token chunks (default lora_tn_chunks(T, K), lora_tn's chunking); part: float
+    scratch of at least chunks * Σ rp * K."""
+    T, K = jobs[0][0].shape
+    chunks = lora_tn_chunks(T, K) if chunks is None else int(chunks)
+    if part.numel() < chunks * sum(p.shape[1] for _, p, _, _, _ in jobs) * K:
+        raise NativeError("lora_tn_batch: partial buffer too small")
+    table = [LoraTnJob(_p(x), x.stride(0), _p(p), p.shape[1], float(sc), int(tr), int(out.dtype == torch.float32),
+                       _p(out)) for x, p, out, sc, tr in jobs]
+    arr = (LoraTnJob * len(table))(*table)
+    call("mxfp8_lora_tn_batch", ctypes.cast(arr, _ptr), len(table), T, K, chunks, _p(part), like=jobs[0][0])
 
 
 class LoraBwdJob(ctypes.Structure):

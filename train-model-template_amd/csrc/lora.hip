@@ -90,9 +90,8 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
 // out [C, Tpad].  One thread per token: it reads its row as C / 8 16-byte pieces and writes one element of each
 // output row, so a wave's stores are 64 consecutive tokens (128 B) of one output row.
 template <int C>
-__global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __restrict__ x, int64_t ldx, int T,
-                                                            int Tpad, uint16_t* __restrict__ out) {
-  const int t = blockIdx.x * 256 + threadIdx.x;
+__device__ __forceinline__ void transpose_pad_body(const uint16_t* __restrict__ x, int64_t ldx, int T, int Tpad,
+                                                   uint16_t* __restrict__ out, int t) {
   if (t >= Tpad) return;
   uint4 v[C / 8];
   const uint4* row = reinterpret_cast<const uint4*>(x + (int64_t)min(t, T - 1) * ldx);
@@ -101,6 +100,28 @@ __global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __re
   const uint16_t* e = reinterpret_cast<const uint16_t*>(v);
 #pragma unroll
   for (int c = 0; c < C; ++c) out[(int64_t)c * Tpad + t] = e[c];
+}
+
+template <int C>
+__global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t* __restrict__ x, int64_t ldx, int T,
+                                                            int Tpad, uint16_t* __restrict__ out) {
+  transpose_pad_body<C>(x, ldx, T, Tpad, out, blockIdx.x * 256 + threadIdx.x);
+}
+
+// A transpose job riding in another kernel's launch (mxfp8_quant_lora_tp): out [C, Tpad] = xᵀ of x [T, C], block b
+// of the job covering tokens 256 b .. 256 b + 255.
+struct TpJob {
+  const uint16_t* x;
+  int64_t ldx;
+  int C;  // 16, 32 or 64; 0: no job
+  uint16_t* out;
+};
+
+__device__ __forceinline__ void transpose_pad_job(const TpJob& j, int T, int Tpad, int b) {
+  const int t = b * 256 + threadIdx.x;
+  if (j.C == 16) transpose_pad_body<16>(j.x, j.ldx, T, Tpad, j.out, t);
+  else if (j.C == 32) transpose_pad_body<32>(j.x, j.ldx, T, Tpad, j.out, t);
+  else transpose_pad_body<64>(j.x, j.ldx, T, Tpad, j.out, t);
 }
 
 // ----------------------------------------------------------------------------------------- x · Wᵀ (nt)
@@ -171,12 +192,17 @@ __global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X,
 // 32-block; it quantizes them (one 16-byte code store, the scale byte) and feeds them, as two k steps in a
 // permuted column order that the W operand follows, to the 32x32x16 MFMA.  The waves' partial products are
 // added in LDS in a fixed order.  Rows past T read row T - 1 (and store its codes again, the same bytes).
+// Workgroups past the Tpad / 32 row blocks run the transpose job tp (mxfp8_quant_lora_tp), if any.
 template <int RP>
 __global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restrict__ X, int64_t ldx, int T, int K,
                                                          const uint16_t* __restrict__ W, uint8_t* __restrict__ q,
                                                          uint8_t* __restrict__ s, float scale,
                                                          uint16_t* __restrict__ out, uint16_t* __restrict__ outT,
-                                                         int Tpad) {
+                                                         int Tpad, const TpJob tp) {
+  if ((int)blockIdx.x >= Tpad / 32) {  // the whole workgroup: before any barrier
+    transpose_pad_job(tp, T, Tpad, (int)blockIdx.x - Tpad / 32);
+    return;
+  }
   // RP = 64: a 16 KB W tile, so 3 stages (72 KB) keep two workgroups on a CU, and a second accumulator for
   // W rows 32..63
   constexpr int kStages = RP > 32 ? 3 : 4, kTileB = 32 * 256, kStageB = kTileB + (RP > 32 ? 2 : 1) * kTileB;
@@ -663,16 +689,17 @@ __global__ __launch_bounds__(256) void lora_bwd_sum_batch_kernel(const LoraBwdSu
 // (K / 128, chunks), 4 waves, wave w on columns blockIdx.x * 128 + 32 w .. + 31.  Per 32-token step the wave
 // writes its X tile and the P tile to LDS and reads both back with k along the tokens (16x16x32 MFMA: A = Xᵀ
 // rows k, B = Pᵀ... as columns ρ); tokens past T are zero.  The next step's tiles are loaded one step ahead.
+// The body takes its column block bx and token chunk by as arguments (blockIdx.x and blockIdx.y of tn_kernel; a
+// job's share of the flat grid of tn_batch_kernel).
 template <int RP, int kD>
-__global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X, int64_t ldx,
-                                                 const uint16_t* __restrict__ P, int T, int K, int chunk,
-                                                 float* __restrict__ part) {
+__device__ __forceinline__ void tn_body(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ P,
+                                        int T, int K, int chunk, float* __restrict__ part, int bx, int by) {
   constexpr int NH = RP / 16;
   __shared__ __attribute__((aligned(16))) uint16_t xt[4][32 * kTrLd];
   __shared__ __attribute__((aligned(16))) uint16_t pt[4][(RP > 32 ? 2 : 1)][32 * kTrLd];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
-  const int kb = blockIdx.x * 128 + w * 32;
-  const int t0 = blockIdx.y * chunk, t1 = min(t0 + chunk, T);
+  const int kb = bx * 128 + w * 32;
+  const int t0 = by * chunk, t1 = min(t0 + chunk, T);
   v4f acc[2][NH];
 #pragma unroll
   for (int jh = 0; jh < 2; ++jh)
@@ -749,15 +776,43 @@ __global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X,
       for (int i = 0; i < 4; ++i) {
         const int rho = h * 16 + (lane & 15);
         const int k = kb + jh * 16 + (lane >> 4) * 4 + i;
-        part[((int64_t)blockIdx.y * RP + rho) * K + k] = acc[jh][h][i];
+        part[((int64_t)by * RP + rho) * K + k] = acc[jh][h][i];
       }
+}
+
+template <int RP, int kD>
+__global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X, int64_t ldx,
+                                                 const uint16_t* __restrict__ P, int T, int K, int chunk,
+                                                 float* __restrict__ part) {
+  tn_body<RP, kD>(X, ldx, P, T, K, chunk, part, blockIdx.x, blockIdx.y);
+}
+
+// The token reductions of mxfp8_lora_tn_batch in one flat grid: job j owns blocks first[j] .. first[j + 1] - 1,
+// `cols` = K / 128 column blocks per token chunk; every job shares T, K and the chunking.
+struct TnBatch {
+  const uint16_t* x[MXFP8_LORA_TN_MAX_JOBS];
+  int64_t ldx[MXFP8_LORA_TN_MAX_JOBS];
+  const uint16_t* p[MXFP8_LORA_TN_MAX_JOBS];
+  float* part[MXFP8_LORA_TN_MAX_JOBS];
+  int rp[MXFP8_LORA_TN_MAX_JOBS];
+  int first[MXFP8_LORA_TN_MAX_JOBS + 1];
+  int n, T, K, chunk, cols;
+};
+
+template <int kD>
+__global__ __launch_bounds__(256) void tn_batch_kernel(const TnBatch a) {
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
+  const int l = b - a.first[j], bx = l % a.cols, by = l / a.cols;
+  if (a.rp[j] == 16) tn_body<16, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by);
+  else tn_body<32, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by);
 }
 
 // out = bf16(Σ_c part[c, ρ, k]) (then bf16(· scale) when scale != 1), written as [RP, K] or transposed
 // [K, RP]; as fp32 holding the bf16 value (out_f32) or as bf16.  The chunks are added in order.
-__global__ __launch_bounds__(256) void tn_sum_kernel(const float* __restrict__ part, int chunks, int RP, int K,
-                                                     float scale, int transpose, int out_f32, void* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__device__ __forceinline__ void tn_sum_body(const float* __restrict__ part, int chunks, int RP, int K, float scale,
+                                            int transpose, int out_f32, void* __restrict__ out, int64_t i) {
   const int64_t n = (int64_t)RP * K;
   if (i >= n) return;
   float v = part[i];
@@ -776,6 +831,31 @@ __global__ __launch_bounds__(256) void tn_sum_kernel(const float* __restrict__ p
   const int64_t o = transpose ? k * RP + rho : i;
   if (out_f32) reinterpret_cast<float*>(out)[o] = v;
   else reinterpret_cast<uint16_t*>(out)[o] = bf(v);
+}
+
+__global__ __launch_bounds__(256) void tn_sum_kernel(const float* __restrict__ part, int chunks, int RP, int K,
+                                                     float scale, int transpose, int out_f32, void* __restrict__ out) {
+  tn_sum_body(part, chunks, RP, K, scale, transpose, out_f32, out, (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// The sums of mxfp8_lora_tn_batch's jobs in one flat grid (job j: blocks first[j] .. first[j + 1] - 1).
+struct TnSumBatch {
+  const float* part[MXFP8_LORA_TN_MAX_JOBS];
+  int rp[MXFP8_LORA_TN_MAX_JOBS];
+  float scale[MXFP8_LORA_TN_MAX_JOBS];
+  int transpose[MXFP8_LORA_TN_MAX_JOBS];
+  int out_f32[MXFP8_LORA_TN_MAX_JOBS];
+  void* out[MXFP8_LORA_TN_MAX_JOBS];
+  int first[MXFP8_LORA_TN_MAX_JOBS + 1];
+  int n, chunks, K;
+};
+
+__global__ __launch_bounds__(256) void tn_sum_batch_kernel(const TnSumBatch a) {
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
+  tn_sum_body(a.part[j], a.chunks, a.rp[j], a.K, a.scale[j], a.transpose[j], a.out_f32[j], a.out[j],
+              (int64_t)(b - a.first[j]) * 256 + threadIdx.x);
 }
 
 // ------------------------------------------------------------------------------- backward partial sums
@@ -992,6 +1072,62 @@ extern "C" int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, 
   return lora_tn_launch(x, T, K, ld_x, p, rp, chunks, part, scale, transpose, out_f32, out, stream);
 }
 
+extern "C" int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T, int64_t K,
+                                   int64_t chunks, float* part, void* stream) {
+  MX_CHECK_ARG(jobs && part && n_jobs >= 1 && n_jobs <= MXFP8_LORA_TN_MAX_JOBS,
+               "mxfp8_lora_tn_batch: 1 to %d jobs and a partial buffer", MXFP8_LORA_TN_MAX_JOBS);
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && T < (1LL << 30) && K < (1LL << 24),
+               "mxfp8_lora_tn_batch: need K %% 128 == 0");
+  MX_CHECK_ARG(chunks > 0 && chunks <= 65535 && mx_aligned(part, 16), "mxfp8_lora_tn_batch: bad chunks or part");
+  const int64_t blocks = (T + 31) / 32;
+  const int64_t chunk = (blocks + chunks - 1) / chunks * 32;
+  const int64_t used = (T + chunk - 1) / chunk;
+  TnBatch a{};
+  TnSumBatch sa{};
+  int64_t off = 0, nb = 0, ns = 0, max_ld = K;
+  for (int64_t j = 0; j < n_jobs; ++j) {
+    const mxfp8_lora_tn_job& jb = jobs[j];
+    MX_CHECK_ARG(jb.x && jb.p && jb.out && (jb.rp == 16 || jb.rp == 32) && jb.ld_x >= K && jb.ld_x % 8 == 0 &&
+                     mx_aligned(jb.x, 16) && mx_aligned(jb.p, 16),
+                 "mxfp8_lora_tn_batch: job %lld: null pointer, rp not in {16, 32} or bad x stride / alignment",
+                 (long long)j);
+    a.x[j] = (const uint16_t*)jb.x;
+    a.ldx[j] = jb.ld_x;
+    a.p[j] = (const uint16_t*)jb.p;
+    a.rp[j] = (int)jb.rp;
+    a.part[j] = part + off;
+    a.first[j] = (int)nb;
+    sa.part[j] = part + off;
+    sa.rp[j] = (int)jb.rp;
+    sa.scale[j] = jb.scale;
+    sa.transpose[j] = (int)jb.transpose;
+    sa.out_f32[j] = (int)jb.out_f32;
+    sa.out[j] = jb.out;
+    sa.first[j] = (int)ns;
+    off += used * jb.rp * K;
+    nb += (K / 128) * used;
+    ns += (jb.rp * K + 255) / 256;
+    max_ld = std::max(max_ld, jb.ld_x);
+  }
+  MX_CHECK_ARG(nb < (1LL << 31), "mxfp8_lora_tn_batch: too many workgroups");
+  a.first[n_jobs] = (int)nb;
+  sa.first[n_jobs] = (int)ns;
+  a.n = sa.n = (int)n_jobs;
+  a.T = (int)T;
+  a.K = sa.K = (int)K;
+  a.chunk = (int)chunk;
+  a.cols = (int)(K / 128);
+  sa.chunks = (int)used;
+  hipStream_t stm = (hipStream_t)stream;
+  // the ring depth rule of lora_tn_launch
+  if (T * max_ld * 2 <= (192LL << 20)) tn_batch_kernel<2><<<(unsigned)nb, 256, 0, stm>>>(a);
+  else tn_batch_kernel<1><<<(unsigned)nb, 256, 0, stm>>>(a);
+  MX_CHECK_LAUNCH("mxfp8_lora_tn_batch");
+  tn_sum_batch_kernel<<<(unsigned)ns, 256, 0, stm>>>(sa);
+  MX_CHECK_LAUNCH("mxfp8_lora_tn_batch");
+  return MXFP8_OK;
+}
+
 // ------------------------------------------------------------------ allocation-free token reduction
 // The chunk partials of mxfp8_lora_tn_noalloc live in this file-scope device array, one copy per GPU, held until
 // the process ends.  Host code never passes `scratch` itself (in host code the name is a stand-in, not a device
@@ -1068,25 +1204,46 @@ extern "C" int mxfp8_mlp_bwd_finish(const float* dxa_part, const float* dbg_part
   return MXFP8_OK;
 }
 
-extern "C" int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w,
-                                int64_t rp, float scale, void* out, void* outT, int64_t Tpad, void* stream) {
+namespace {
+
+int quant_lora_launch(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w, int64_t rp,
+                      float scale, void* out, void* outT, int64_t Tpad, const TpJob& tp, void* stream) {
   MX_CHECK_ARG(x && q && s && w && out, "mxfp8_quant_lora: null pointer");
   MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && ld_x >= K && ld_x % 8 == 0 && (rp == 16 || rp == 32 || rp == 64),
                "mxfp8_quant_lora: need K %% 128 == 0, rp in {16, 32, 64}");
   MX_CHECK_ARG(Tpad == (T + 127) / 128 * 128, "mxfp8_quant_lora: Tpad must be ceil(T / 128) * 128");
   MX_CHECK_ARG(mx_aligned(x, 16) && mx_aligned(w, 16) && mx_aligned(q, 16) && mx_aligned(s, 16),
                "mxfp8_quant_lora: misaligned buffer");
-  MX_CHECK_ARG(Tpad / 32 < (1LL << 31) && T * K < (1LL << 40), "mxfp8_quant_lora: too large");
-  dim3 grid((unsigned)(Tpad / 32));
+  MX_CHECK_ARG(Tpad / 32 < (1LL << 30) && T * K < (1LL << 40), "mxfp8_quant_lora: too large");
+  const int64_t extra = tp.C ? (Tpad + 255) / 256 : 0;  // workgroups of the transpose job
+  dim3 grid((unsigned)(Tpad / 32 + extra));
   hipStream_t stm = (hipStream_t)stream;
 #define QL_ARGS (const uint16_t*)x, ld_x, (int)T, (int)K, (const uint16_t*)w, (uint8_t*)q, (uint8_t*)s, scale, \
-                (uint16_t*)out, (uint16_t*)outT, (int)Tpad
+                (uint16_t*)out, (uint16_t*)outT, (int)Tpad, tp
   if (rp == 16) quant_lora_kernel<16><<<grid, 256, 0, stm>>>(QL_ARGS);
   else if (rp == 32) quant_lora_kernel<32><<<grid, 256, 0, stm>>>(QL_ARGS);
   else quant_lora_kernel<64><<<grid, 256, 0, stm>>>(QL_ARGS);
 #undef QL_ARGS
   MX_CHECK_LAUNCH("mxfp8_quant_lora");
   return MXFP8_OK;
+}
+
+}  // namespace
+
+extern "C" int mxfp8_quant_lora(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w,
+                                int64_t rp, float scale, void* out, void* outT, int64_t Tpad, void* stream) {
+  return quant_lora_launch(x, T, K, ld_x, q, s, w, rp, scale, out, outT, Tpad, TpJob{nullptr, 0, 0, nullptr}, stream);
+}
+
+extern "C" int mxfp8_quant_lora_tp(const void* x, int64_t T, int64_t K, int64_t ld_x, void* q, void* s, const void* w,
+                                   int64_t rp, float scale, void* out, void* outT, int64_t Tpad, const void* tx,
+                                   int64_t ld_tx, int64_t tc, void* tout, void* stream) {
+  MX_CHECK_ARG(tx && tout, "mxfp8_quant_lora_tp: null pointer");
+  MX_CHECK_ARG((tc == 16 || tc == 32 || tc == 64) && ld_tx >= tc && ld_tx % 8 == 0 && mx_aligned(tx, 16) &&
+                   mx_aligned(tout, 2),
+               "mxfp8_quant_lora_tp: need tc in {16, 32, 64} and 16-byte aligned rows of tx");
+  return quant_lora_launch(x, T, K, ld_x, q, s, w, rp, scale, out, outT, Tpad,
+                           TpJob{(const uint16_t*)tx, ld_tx, (int)tc, (uint16_t*)tout}, stream);
 }
 
 extern "C" int mxfp8_res_lora(const void* x, const void* y, const void* xa, int64_t ld_xa, const void* b, int64_t T,

@@ -290,9 +290,9 @@ class _MLP(torch.autograd.Function):
             dy2 = dy2.contiguous()
         T, N = dy2.shape[0], hold.n
         lw = _forms_of_saved(S, bg, bu, ad, bd, dt)
-        xsT = _transposed_padded(xs, _cdiv(T, 128) * 128)  # the backward kernel's operand form of xs
-        # one read of dy2: its MX operand and dxd = bf16(bf16(dy2 · bd) · s_d) [T, R] with its zero-padded transpose
-        qd, sd, dxd, dxdT = mxfp8.mx_quant_lora(dy2, lw.bdT, scale=s_d)
+        # one read of dy2: its MX operand and dxd = bf16(bf16(dy2 · bd) · s_d) [T, R] with its zero-padded transpose,
+        # and, from the same launch, xsT, the backward kernel's operand form of xs (zero-padded transpose)
+        qd, sd, dxd, dxdT, xsT = mxfp8.mx_quant_lora_tp(dy2, lw.bdT, xs, scale=s_d)
         if need_x and R == 16 and FUSED_BWD_EPILOGUE[0]:
             # one launch: dhm = MX(dy) · W_down in registers and, in the GEMM's epilogue, the SwiGLU backward:
             # MX(dg | du) and the dxa / dB / dA_d partials
@@ -322,12 +322,19 @@ class _MLP(torch.autograd.Function):
         # the token reductions: the bf16 values of the reference's bf16 GEMMs (fused_mlp.py:316-318, :333), held
         # in the dtype of the parameter they are the gradient of: autograd casts a bf16 return to an fp32
         # parameter's dtype anyway (bf16 -> fp32 is exact, so .grad is bit-identical), and the kernel writing the
-        # fp32 holder directly saves those cast kernels (about 23 us per step at the headline shape)
+        # fp32 holder directly saves those cast kernels (about 23 us per step at the headline shape).  Both in one
+        # launch (and their chunk sums in one more): dB_d = bf16(bf16(dyᵀ xsd) s_d) and dA = bf16(dxaᵀ · x2)
         ag_dt, au_dt, bd_dt = ctx.pdt
-        part = torch.empty(_native.lora_tn_chunks(T, K) * 2 * R * K, dtype=torch.float32, device=dy2.device)
+        fp32_a = ag_dt == au_dt == torch.float32
+        chunks = _native.lora_tn_chunks(T, K)
+        part = torch.empty(chunks * 3 * R * K, dtype=torch.float32, device=dy2.device)
         dB_d = torch.empty((K, R), dtype=torch.float32 if bd_dt == torch.float32 else dt, device=dy2.device)
-        # bf16(bf16(dyᵀ xsd) s_d)
-        _native.lora_tn(dy2, xsd, dB_d, part[:part.numel() // 2], scale=s_d, transpose=True)
+        dA = torch.empty((2 * R, K), dtype=torch.float32 if fp32_a else dt, device=dy2.device)
+        if 2 * R <= 32:  # the batch takes ranks 16 and 32
+            _native.lora_tn_batch([(dy2, xsd, dB_d, s_d, True), (x2, dxa, dA, 1.0, False)], part)
+        else:
+            _native.lora_tn(dy2, xsd, dB_d, part[:chunks * R * K], scale=s_d, transpose=True)
+            _native.lora_tn(x2, dxa, dA, part[chunks * R * K:])
         dx = None
         if need_x:
             # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
@@ -339,9 +346,6 @@ class _MLP(torch.autograd.Function):
                 dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
-        fp32_a = ag_dt == au_dt == torch.float32
-        dA = torch.empty((2 * R, K), dtype=torch.float32 if fp32_a else dt, device=dy2.device)
-        _native.lora_tn(x2, dxa, dA, part)  # bf16(dxaᵀ · x2)
         grads = [dA[:R], dB_g, dA[R:], dB_u, dA_d, dB_d]
         ws_in = ctx.needs_input_grad[3:]
         return (dx, None, None, *[g if ws_in[k] else None for k, g in enumerate(grads)])

@@ -88,6 +88,24 @@ def mx_quant_lora(x2d, w, scale=1.0, out_t=True):
     return q, s.view(E8), out, outT
 
 
+def mx_quant_lora_tp(x2d, w, tx, scale=1.0):
+    """mx_quant_lora(x2d, w, scale) and, from the same launch, the zero-padded transpose [C, ceil(R/128)*128] of
+    tx [R, C] bf16 (C in {16, 32, 64}): -> (q, s, out, outT, txT)."""
+    R, K = x2d.shape
+    assert x2d.dtype == torch.bfloat16 and x2d.stride(1) == 1 and K % 128 == 0 and R > 0, (x2d.dtype, x2d.shape)
+    assert tx.dtype == torch.bfloat16 and tx.shape[0] == R and tx.stride(1) == 1 and tx.shape[1] in (16, 32, 64)
+    rp = w.shape[0]
+    dev = x2d.device
+    tpad = _cdiv(R, 128) * 128
+    q = torch.empty((tiled_rows(R), K), dtype=F8, device=dev)
+    s = torch.empty(scale_numel(R, K), dtype=torch.uint8, device=dev)
+    out = torch.empty((R, rp), dtype=torch.bfloat16, device=dev)
+    outT = torch.empty((rp, tpad), dtype=torch.bfloat16, device=dev)
+    txT = torch.empty((tx.shape[1], tpad), dtype=torch.bfloat16, device=dev)
+    _native.quant_lora_tp(x2d, q, s, w, out, tx, txT, scale=scale, outT=outT)
+    return q, s.view(E8), out, outT, txT
+
+
 def res_lora(x, y, xa, B, scale):
     """x + (y + scale * xa @ Bᵀ) for x, y [T, N] bf16 contiguous, xa [T, r] (any row stride), B [N, r] contiguous:
     out = bf16(x + bf16(y + scale · xa·Bᵀ)), the LoRA-B addmm_ and the residual add in one pass
