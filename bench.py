@@ -445,12 +445,15 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
     with open(_traffic_path(cfg, "json"), "w") as f:
         json.dump(summary, f, indent=1)
     with open(_traffic_path(cfg, "md"), "w") as f:
-        f.write(f"# HBM traffic of the MX GEMM launches, configuration {cfg} (rocprofv3 FETCH_SIZE / WRITE_SIZE)\n\n")
+        f.write(f"# Memory traffic beyond L2 of the MX GEMM launches, configuration {cfg} (rocprofv3 FETCH_SIZE / "
+                "WRITE_SIZE)\n\n")
         f.write("Commands (GPU box; one counter per run):\n\n```\ncd /tmp && export TMPDIR=/tmp\n"
                 f"{cmd_fetch}\n{cmd_write}\n```\n\n")
         f.write(f"Scaled by the same counters on a plain copy kernel (torch.neg of 1 GiB bf16: reads 1 GiB, writes "
-                f"1 GiB): FETCH x{f_scale:.4f}, WRITE x{w_scale:.4f}.\n\n")
-        f.write("| kernel | grid | HBM read MB | HBM write MB |\n|---|---|---|---|\n")
+                f"1 GiB): FETCH x{f_scale:.4f}, WRITE x{w_scale:.4f}.  FETCH_SIZE counts what the L2 fetches from "
+                "beyond itself, so reads served by the 256 MB last-level cache count as well as HBM reads: the "
+                "columns are an upper bound on HBM bytes.\n\n")
+        f.write("| kernel | grid | beyond-L2 read MB | beyond-L2 write MB |\n|---|---|---|---|\n")
         for x in rows:
             f.write(f"| {x['kernel']} | {x['grid']} | {x['fetch_bytes'] / 1e6:.1f} | {x['write_bytes'] / 1e6:.1f} |\n")
         f.write("\n| shape | algorithmic MB (operands + scales once, bf16 output, LoRA operands) |\n|---|---|\n")
@@ -476,7 +479,8 @@ def _kernel_key(name, grid):
         elif len(targs) > 2 and targs[2] == "2":
             k += " dh + SwiGLU backward epilogue"
         else:
-            k += " " + shape.get((wg, r), f"{wg} WGs")
+            # other grids (configuration 4): at LoRA rank 16 the epilogue rank alone tells the shapes apart
+            k += " " + shape.get((wg, r), {"0": "dh", "16": "down", "32": "dx"}.get(r, f"{wg} WGs"))
     return k
 
 
@@ -484,8 +488,9 @@ def _counters_summary(name, dirs, cmds):
     """Per-kernel medians over the dispatches of the rocprofv3 --pmc passes in `dirs` (one counter set per pass; each dispatch row
     carries its start and end timestamps), with the derived figures: sustained shader clock = GRBM_GUI_ACTIVE / kernel duration; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES
     / (GRBM_GUI_ACTIVE x 256 CUs x 4 SIMDs); FP8 MFMA flops = 512 x SQ_INSTS_VALU_MFMA_MOPS_F8; L2 hit rate =
-    TCC_HIT / (TCC_HIT + TCC_MISS); TA / TD busy = TA_TA_BUSY_sum / TD_TD_BUSY_sum / (GRBM_GUI_ACTIVE x 256); HBM read / write = FETCH_SIZE
-    / WRITE_SIZE scaled by their reading on a 1 GiB copy kernel in the same pass (--copy-calib).
+    TCC_HIT / (TCC_HIT + TCC_MISS); TA / TD busy = TA_TA_BUSY_sum / TD_TD_BUSY_sum / (GRBM_GUI_ACTIVE x 256); beyond-L2 read / write = FETCH_SIZE
+    / WRITE_SIZE scaled by their reading on a 1 GiB copy kernel in the same pass (--copy-calib): bytes the L2
+    moves to and from the last-level cache and HBM, an upper bound on HBM bytes.
     Writes profiles/<name>.md and .json."""
     per = {}  # kernel key -> counter -> [per-dispatch values]
     for d in dirs:
@@ -531,7 +536,7 @@ def _counters_summary(name, dirs, cmds):
             row["fp8_mfma_GFLOP"] = round(512 * m["SQ_INSTS_VALU_MFMA_MOPS_F8"] / 1e9, 1)
         if "TCC_HIT_sum" in m and "TCC_MISS_sum" in m and m["TCC_HIT_sum"] + m["TCC_MISS_sum"] > 0:
             row["l2_hit"] = round(m["TCC_HIT_sum"] / (m["TCC_HIT_sum"] + m["TCC_MISS_sum"]), 4)
-        for c, out_name in (("FETCH_SIZE", "hbm_read_MB"), ("WRITE_SIZE", "hbm_write_MB")):
+        for c, out_name in (("FETCH_SIZE", "beyond_l2_read_MB"), ("WRITE_SIZE", "beyond_l2_write_MB")):
             if c in m:
                 row[out_name] = round(m[c] / 1e6, 1)
         for c, out_name in (("TA_TA_BUSY_sum", "ta_busy"), ("TD_TD_BUSY_sum", "td_busy")):
@@ -559,11 +564,12 @@ def _counters_summary(name, dirs, cmds):
     print(json.dumps(table))
 
 
-def _trace_summary(name, d, steps, cmd):
+def _trace_summary(name, d, steps, cmd, layers=1):
     """rocprofv3 --kernel-trace of a bench run in `d` -> profiles/<name>.md: per kernel (the MX GEMM split into
     its MLP shapes by _kernel_key) the launches from the first MX GEMM on, the median duration, and the share of a
-    step = median x round(launches / steps), where `steps` counts every step the profiled process ran (timed +
-    warmup)."""
+    step = median x round(launches / steps), where `steps` counts every step the profiled process ran (warmup,
+    timed and instrumented); steps = 0 takes it from the trace: the backward kernel runs once per layer and step
+    (the gating forward has no backward), so steps = its launches / layers."""
     files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
         raise SystemExit(f"no *kernel_trace.csv under {d}")
@@ -575,6 +581,11 @@ def _trace_summary(name, d, steps, cmd):
     # host-to-device copies and the weight preparation before it are one-off work
     gemm_starts = [int(r["Start_Timestamp"]) for r in rows_all if "gemm_kernel" in r["Kernel_Name"]]
     t0 = min(gemm_starts) if gemm_starts else 0
+    given = steps
+    if steps <= 0:
+        steps = sum(1 for r in rows_all if re.search(r"\bbwd_kernel<", r["Kernel_Name"])) / max(layers, 1)
+        if steps <= 0:
+            raise SystemExit("no backward-kernel launches to count steps by")
     durs = {}
     for row in rows_all:
         if int(row["Start_Timestamp"]) < t0:
@@ -595,8 +606,11 @@ def _trace_summary(name, d, steps, cmd):
     tot = sum(r[3] for r in rows)
     with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
         f.write(f"# Kernel trace: {name}\n\nCommand (GPU box, repo root as `$GRAFT_REPO_ROOT`):\n\n```\ncd /tmp && "
-                f"export TMPDIR=/tmp\n{cmd}\npython3 bench.py --trace-summary {name} <trace dir> {steps:g}\n```\n\n")
-        f.write(f"The profiled process runs {steps:g} steps (timed + warmup) after one forward for the gating check; "
+                f"export TMPDIR=/tmp\n{cmd}\npython3 bench.py --trace-summary {name} <trace dir> {given:g}"
+                f"{f' --trace-layers {layers}' if layers != 1 else ''}\n```\n\n")
+        f.write(f"The profiled process runs {steps:g} steps (warmup, timed and instrumented"
+                f"{'; counted from the backward-kernel launches' if given <= 0 else ''}) after one forward for the "
+                "gating check; "
                 "dispatches before that forward's first MX GEMM (input generation, host-to-device copies, weight "
                 "preparation) are left out. 'per step' = median duration x round(launches / steps); kernels of the "
                 "gating forward alone show 0.\n\n| kernel | launches | median us | us per step | % |\n"
@@ -604,6 +618,21 @@ def _trace_summary(name, d, steps, cmd):
         for key, n, med, ps in rows:
             f.write(f"| {key} | {n} | {med:.1f} | {ps:.1f} | {100 * ps / tot if tot else 0:.1f} |\n")
         f.write(f"\nSum of kernel time per step: {tot:.1f} us.\n")
+        stats = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+        if stats:  # rocprofv3 --stats of the same run: every dispatch of the process, warmup and gating forward too
+            with open(stats[0]) as fh:
+                srows = list(csv.DictReader(fh))
+            f.write("\nrocprofv3 --stats of the same run (every dispatch of the process by kernel name, the gating "
+                    "forward and the warmup steps included; in the MLP step each MX GEMM shape has its own template "
+                    "arguments: <16, 1, 1> gate|up with the SwiGLU epilogue, <16, 1, 0> down, <0, 1, 0> dh, "
+                    "<32, 1, 0> dx):\n\n| kernel | calls | average us | min us | max us | % |\n"
+                    "|---|---|---|---|---|---|\n")
+            for r in srows[:16]:
+                m = re.search(r"(\w+_kernel)(<[^>]*>)?", r["Name"])
+                kn = (m.group(1) + (m.group(2) or "")) if m else r["Name"][:48]
+                f.write(f"| {kn} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                        f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                        f"{float(r['Percentage']):.1f} |\n")
     print(json.dumps({k: round(ps, 1) for k, _, _, ps in rows}))
 
 
@@ -627,9 +656,11 @@ def main():
     ap.add_argument("--trace-summary", nargs=3, metavar=("NAME", "DIR", "STEPS"),
                     help="summarize a rocprofv3 --kernel-trace run of STEPS steps into profiles/NAME.md")
     ap.add_argument("--trace-command", default="", help="the profiling command, for the summary")
+    ap.add_argument("--trace-layers", type=int, default=1, help="MLP layers per step of the traced run (steps = 0)")
     args = ap.parse_args()
     if args.trace_summary:
-        _trace_summary(args.trace_summary[0], args.trace_summary[1], float(args.trace_summary[2]), args.trace_command)
+        _trace_summary(args.trace_summary[0], args.trace_summary[1], float(args.trace_summary[2]), args.trace_command,
+                       args.trace_layers)
         return
     if args.counters_summary:
         _counters_summary(args.counters_summary[0], args.counters_summary[1:], args.counters_commands)
