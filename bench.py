@@ -262,7 +262,10 @@ def _grouped_linears(T, K, r, alpha, dev, steps=10):
     a = m.model.layers[0].self_attn
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
-    resid = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16).requires_grad_(True)
+    # the residual stream takes no gradient here: its gradient is dy itself (residual_add passes it through), and
+    # a leaf that required it would add a [T, K] copy into .grad per step (autograd copies a gradient that the
+    # other branch still holds), which a decoder's residual stream, whose gradient flows on, never makes
+    resid = torch.randn(T, K, device=dev, generator=g).to(torch.bfloat16)
     dy = (torch.randn(T, K, device=dev, generator=g) * 1e-2).to(torch.bfloat16)
     params = [p for p in m.parameters() if p.requires_grad]
 
@@ -277,7 +280,7 @@ def _grouped_linears(T, K, r, alpha, dev, steps=10):
         torch.autograd.backward([out, k, v], [dy, dk, dv])
         for p in params:
             p.grad = None
-        x.grad = resid.grad = None
+        x.grad = None
 
     for _ in range(3):
         step()
