@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 11
+#define MXFP8_MLP_ABI_VERSION 12
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -424,6 +424,21 @@ typedef struct {
  */
 int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T, int64_t K, int64_t chunks,
                         float* part, void* stream);
+
+/*
+ * mxfp8_gemm_nt (4-wave shape, rank-32 LoRA epilogue, no workspace) and mxfp8_lora_tn_batch in one launch plus
+ * the batch's sums: the token reductions run in workgroups numbered after every GEMM tile, so the dispatcher
+ * starts them only once each tile has started, in the workgroup slots the GEMM's last round of tiles leaves
+ * idle.  Results bit for bit those of the two calls one after the other (jobs, T_tn, K_tn, chunks and part as
+ * in mxfp8_lora_tn_batch).  The jobs must not read c.  Replaces, in the MLP backward, the dx GEMM with its
+ * dxa·S addmm_ and the token GEMMs dB_d, dA (/root/reference/scripts/fused_mlp.py:331, :316-318, :333), which
+ * the reference runs as separate kernels.  r must be 32, layout without MXFP8_GEMM_WIDE, M > 0.
+ */
+int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
+                     int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,
+                     const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
+                     const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T_tn, int64_t K_tn, int64_t chunks,
+                     float* part, void* stream);
 
 /*
  * Allocation-free variant of mxfp8_lora_tn: same arguments without `chunks` / `part`, same result bit for bit as

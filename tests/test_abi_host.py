@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 35, names
+    assert len(names) == 36, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -78,6 +78,15 @@ def test_argument_checks_reject_before_launch(lib):
     # allocation-free token reduction: rp * K * 4 bytes beyond its 16 MiB static scratch (checked first, no GPU call)
     assert lib.mxfp8_lora_tn_noalloc(p, 64, 65536 + 128, 65536 + 128, p, 64, 1.0, 0, 0, p, None) == -1
     assert b"static scratch" in lib.mxfp8_last_error()
+    # GEMM with folded token reductions: only the rank-32 epilogue of the 4-wave shape, and the batch's own checks
+    job = _native.LoraTnJob(16, 2048, 16, 32, 1.0, 0, 0, 16)
+    jobs = (_native.LoraTnJob * 1)(job)
+    gemm = lambda r, layout, jb: lib.mxfp8_gemm_nt_tn(p, p, 2048, p, p, 2048, 256, 2048, 2048, p, 2048, p, 32, p, 32,  # noqa: E731
+                                                      r, 1.0, layout, jb, 1, 256, 2048, 8, p, None)
+    assert gemm(16, 0, jobs) == -1 and b"rank-32" in lib.mxfp8_last_error()
+    assert gemm(32, _native.GEMM_WIDE, jobs) == -1 and b"4-wave" in lib.mxfp8_last_error()
+    bad = (_native.LoraTnJob * 1)(_native.LoraTnJob(16, 2048, 16, 64, 1.0, 0, 0, 16))
+    assert gemm(32, 0, bad) == -1 and b"mxfp8_gemm_nt_tn: job 0" in lib.mxfp8_last_error()
     assert lib.mxfp8_lora_tn_noalloc_chunks(10752, 2048, 32) == lib.mxfp8_lora_tn_chunks(10752, 2048)
     assert lib.mxfp8_lora_tn_noalloc_chunks(10752, 2048, 32) * 32 * 2048 * 4 <= 16 << 20
     # GEMM K not a multiple of 128

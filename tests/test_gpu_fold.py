@@ -1,0 +1,79 @@
+"""GPU checks of mxfp8_gemm_nt_tn: the rank-32 LoRA-epilogue MX GEMM whose launch also runs the token reductions
+of mxfp8_lora_tn_batch in workgroups past its tiles (the MLP backward's dx GEMM with its dB_d / dA reductions,
+/root/reference/scripts/fused_mlp.py:331, :316-318, :333).  The folded launch computes what the two separate
+calls compute, with the same kernels' arithmetic in the same order, so the bar is bit-identical outputs:
+  - the GEMM output and both reductions against mxfp8_gemm_nt followed by mxfp8_lora_tn_batch, at the MLP's
+    configuration-3 dx shape (672 tiles: the reductions run in the last round's idle slots), at a small shape
+    whose few tiles leave most slots free from the start, with T not a multiple of 32 or 128, and at T = 1;
+  - the whole fused MLP step with the fold on and off (fused_mlp.FOLD_TN): output, dx and every LoRA gradient."""
+import pytest
+import torch
+
+import _native
+import fused_linear
+import fused_mlp
+import mxfp8
+import workloads
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N,K,Kt", [(10752, 2048, 12288, 2048), (300, 256, 512, 1024), (1, 128, 256, 128),
+                                      (2000, 1024, 2048, 768)])
+def test_gemm_nt_tn_matches_separate_calls(M, N, K, Kt, gpu):
+    g = torch.Generator().manual_seed(M + N + K)
+    a = (torch.randn(M, K, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    qa, sa = mxfp8.mx_quant_tiled(a)
+    qb, sb = mxfp8.mx_quant_tiled(b)
+    P = (torch.randn(M, 32, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    Q = (torch.randn(N, 32, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    # the MLP's two reductions: dB_d = bf16(bf16(dyᵀ xsd) s) [Kt, 16] transposed, dA = bf16(dxaᵀ x) [32, Kt] fp32
+    x0 = torch.randn(M, Kt, generator=g).to(torch.bfloat16).to(gpu)
+    p0 = (torch.randn(M, 16, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    x1 = torch.randn(M, Kt, generator=g).to(torch.bfloat16).to(gpu)
+    p1 = (torch.randn(M, 32, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    chunks = _native.lora_tn_chunks(M, Kt)
+    part = torch.empty(chunks * 48 * Kt, device=gpu)
+
+    ref_c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P, Q), alpha=2.0, layout=3, m=M)
+    r0 = torch.empty((Kt, 16), dtype=torch.bfloat16, device=gpu)
+    r1 = torch.empty((32, Kt), dtype=torch.float32, device=gpu)
+    _native.lora_tn_batch([(x0, p0, r0, 2.0, True), (x1, p1, r1, 1.0, False)], part)
+    torch.cuda.synchronize()
+
+    o0 = torch.full_like(r0, float("nan"))
+    o1 = torch.full_like(r1, float("nan"))
+    part.fill_(float("nan"))  # the folded launch must write every partial it sums
+    c = mxfp8.mx_mm_tn(qa, sa, qb, sb, (P, Q), 2.0, 3, M, [(x0, p0, o0, 2.0, True), (x1, p1, o1, 1.0, False)], part)
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), ref_c.view(torch.int16))
+    assert torch.equal(o0.view(torch.int16), r0.view(torch.int16))
+    assert torch.equal(o1.view(torch.int32), r1.view(torch.int32))
+
+
+def _grads(m):
+    return [m.gate_proj.lora_A["default"].weight.grad, m.gate_proj.lora_B["default"].weight.grad,
+            m.up_proj.lora_A["default"].weight.grad, m.up_proj.lora_B["default"].weight.grad,
+            m.down_proj.lora_A["default"].weight.grad, m.down_proj.lora_B["default"].weight.grad]
+
+
+@pytest.mark.parametrize("T", [2048, 1000])
+def test_mlp_step_with_and_without_the_fold(T, gpu, monkeypatch):
+    model, inps = workloads.build_model(3, T=T, device=gpu)
+    mxfp8.enable_mxfp8(model)
+    mod = model.layers[0].mlp
+    x, dy = inps[0]["x"].to(gpu), inps[0]["dy"].to(gpu)
+    outs = []
+    for fold in (False, True):
+        monkeypatch.setattr(fused_mlp, "FOLD_TN", [fold])
+        fused_linear.new_step()
+        for p in model.parameters():
+            p.grad = None
+        xi = x.clone().requires_grad_(True)
+        y = fused_mlp.mlp(mod, xi)
+        y.backward(dy)
+        torch.cuda.synchronize()
+        outs.append([y.detach(), xi.grad] + [t.detach().clone() for t in _grads(mod)])
+    for k, (a, b) in enumerate(zip(*outs)):
+        assert torch.equal(a, b), k

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT, GEMM_B_PI = 1, 2, 4, 8, 16  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -57,6 +57,8 @@ SIGNATURES = {
     "mxfp8_lora_bwd_batch": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_batch": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr],
+    "mxfp8_gemm_nt_tn": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
+                         _i64, _f32, _i64, _ptr, _i64, _i64, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc_chunks": [_i64, _i64, _i64],
     "mxfp8_mlp_bwd_finish": [_ptr, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _ptr, _ptr, _ptr, _ptr,
@@ -352,14 +354,30 @@ def lora_tn_batch(jobs, part, chunks=None):
     """lora_tn of every job [(x, p, out, scale, transpose)] (the same [T, K] for all) in one launch, plus one launch
     of the chunk sums; chunks: token chunks (default lora_tn_chunks(T, K), lora_tn's chunking); part: float
     scratch of at least chunks * Σ rp * K."""
+    arr, n, T, K, chunks = _tn_table(jobs, part, chunks)
+    call("mxfp8_lora_tn_batch", ctypes.cast(arr, _ptr), n, T, K, chunks, _p(part), like=jobs[0][0])
+
+
+def _tn_table(jobs, part, chunks):
+    """(ctypes job array, n, T, K, chunks) of mxfp8_lora_tn_batch's jobs [(x, p, out, scale, transpose)]."""
     T, K = jobs[0][0].shape
     chunks = lora_tn_chunks(T, K) if chunks is None else int(chunks)
     if part.numel() < chunks * sum(p.shape[1] for _, p, _, _, _ in jobs) * K:
         raise NativeError("lora_tn_batch: partial buffer too small")
     table = [LoraTnJob(_p(x), x.stride(0), _p(p), p.shape[1], float(sc), int(tr), int(out.dtype == torch.float32),
                        _p(out)) for x, p, out, sc, tr in jobs]
-    arr = (LoraTnJob * len(table))(*table)
-    call("mxfp8_lora_tn_batch", ctypes.cast(arr, _ptr), len(table), T, K, chunks, _p(part), like=jobs[0][0])
+    return (LoraTnJob * len(table))(*table), len(table), T, K, chunks
+
+
+def gemm_nt_tn(a, sa, lda, b, sb, ldb, M, N, K, c, lora, jobs, part, alpha=1.0, layout=0, chunks=None):
+    """gemm_nt (rank-32 lora = (P, Q), 4-wave shape) and lora_tn_batch(jobs, part, chunks) in one launch, plus the
+    batch's sums (include/mxfp8_mlp.h, mxfp8_gemm_nt_tn): the token reductions fill the GEMM's idle tail slots."""
+    p, q = lora
+    arr, n, T, Kt, chunks = _tn_table(jobs, part, chunks)
+    _gpu(c, "mxfp8_gemm_nt_tn")
+    call("mxfp8_gemm_nt_tn", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(p),
+         p.stride(0), _p(q), q.stride(0), p.shape[1], float(alpha), layout, ctypes.cast(arr, _ptr), n, T, Kt, chunks,
+         _p(part), like=c)
 
 
 class LoraBwdJob(ctypes.Structure):

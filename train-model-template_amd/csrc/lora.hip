@@ -18,6 +18,7 @@
 
 #include "abi_common.h"
 #include "mx_device.h"
+#include "tn_device.h"
 
 using namespace mxk;
 
@@ -685,128 +686,20 @@ __global__ __launch_bounds__(256) void lora_bwd_sum_batch_kernel(const LoraBwdSu
 }
 
 // ------------------------------------------------------------------------------------- Pᵀ · X (tn)
-// part[c, ρ, k] = Σ_{t in chunk c} P[t, ρ] X[t, k], P [T, RP] bf16, X [T, K] bf16 (row stride ldx).  Grid
-// (K / 128, chunks), 4 waves, wave w on columns blockIdx.x * 128 + 32 w .. + 31.  Per 32-token step the wave
-// writes its X tile and the P tile to LDS and reads both back with k along the tokens (16x16x32 MFMA: A = Xᵀ
-// rows k, B = Pᵀ... as columns ρ); tokens past T are zero.  The next step's tiles are loaded one step ahead.
-// The body takes its column block bx and token chunk by as arguments (blockIdx.x and blockIdx.y of tn_kernel; a
-// job's share of the flat grid of tn_batch_kernel).
-template <int RP, int kD>
-__device__ __forceinline__ void tn_body(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ P,
-                                        int T, int K, int chunk, float* __restrict__ part, int bx, int by) {
-  constexpr int NH = RP / 16;
-  __shared__ __attribute__((aligned(16))) uint16_t xt[4][32 * kTrLd];
-  __shared__ __attribute__((aligned(16))) uint16_t pt[4][(RP > 32 ? 2 : 1)][32 * kTrLd];
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
-  const int kb = bx * 128 + w * 32;
-  const int t0 = by * chunk, t1 = min(t0 + chunk, T);
-  v4f acc[2][NH];
-#pragma unroll
-  for (int jh = 0; jh < 2; ++jh)
-#pragma unroll
-    for (int h = 0; h < NH; ++h) acc[jh][h] = v4f{};
-  constexpr int PW = RP / 4;  // packed words of P per lane: half of the row (RP / 2 values)
-  struct Step {
-    uint32_t x[8];   // X row t + l % 32, columns kb + lg*16 .. + 15
-    uint32_t p[PW];  // P row t + l % 32, columns lg * RP/2 .. + RP/2 - 1
-    bool ok;         // row t + l % 32 inside the chunk
-  };
-  auto fetch = [&](int t, Step& st) {
-    const int row = t + (lane & 31);
-    st.ok = row < t1;
-    const int rc = min(row, T - 1);
-    load16(X + (int64_t)rc * ldx + kb + lg * 16, st.x);
-    const uint16_t* prow = P + (int64_t)rc * RP + lg * (RP / 2);
-    if constexpr (RP == 16) {
-      const uint4 v = *reinterpret_cast<const uint4*>(prow);
-      st.p[0] = v.x; st.p[1] = v.y; st.p[2] = v.z; st.p[3] = v.w;
-    } else {
-#pragma unroll
-      for (int q = 0; q < PW; q += 8) load16(prow + 2 * q, st.p + q);
-    }
-  };
-  auto consume = [&](Step& cur) {
-    // tokens past the chunk are zero (not 0 * whatever row T - 1 holds); masked here, at the use, so the
-    // loads stay in flight until then
-#pragma unroll
-    for (int k = 0; k < 8; ++k) cur.x[k] = cur.ok ? cur.x[k] : 0u;
-#pragma unroll
-    for (int k = 0; k < PW; ++k) cur.p[k] = cur.ok ? cur.p[k] : 0u;
-    tr_store(xt[w], lane, cur.x);
-    // P tile row l % 32: the lane's RP/2 columns (RP = 64: lane half lg fills tile lg, columns 0..31)
-    {
-      uint32_t* prow = reinterpret_cast<uint32_t*>(pt[w][RP > 32 ? lg : 0] + (lane & 31) * kTrLd) +
-                       (RP > 32 ? 0 : lg * (PW));
-#pragma unroll
-      for (int k = 0; k < PW; k += 2) *reinterpret_cast<uint2*>(prow + k) = make_uint2(cur.p[k], cur.p[k + 1]);
-    }
-    const v8bf a0 = tr_operand(xt[w], 0, lane), a1 = tr_operand(xt[w], 16, lane);
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-      const v8bf b = RP > 32 ? tr_operand(pt[w][h >> 1], (h & 1) * 16, lane) : tr_operand(pt[w][0], h * 16, lane);
-      acc[0][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc[0][h], 0, 0, 0);
-      acc[1][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc[1][h], 0, 0, 0);
-    }
-  };
-  // Register ring of kD 32-token steps: each round but the last consumes a slot and refills it kD steps ahead,
-  // unconditionally (a conditional load would make the counter waits at the loop header drain the ring); the
-  // refills past the chunk reload its last step, never consumed.  kD = 1 loads each step after the previous one
-  // is consumed.
-  const int nsteps = (t1 - t0 + 31) / 32;
-  Step ring[kD];
-#pragma unroll
-  for (int j = 0; j < kD; ++j) fetch(t0 + 32 * min(j, nsteps - 1), ring[j]);
-  int s0 = 0;
-  for (; s0 + kD < nsteps; s0 += kD) {
-#pragma unroll
-    for (int j = 0; j < kD; ++j) {
-      consume(ring[j]);
-      fetch(t0 + 32 * min(s0 + j + kD, nsteps - 1), ring[j]);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < kD; ++j)
-    if (s0 + j < nsteps) consume(ring[j]);
-  // acc[jh][h] lane l: ρ = 16 h + l % 16, k = kb + 16 jh + (l / 16) * 4 + i
-#pragma unroll
-  for (int jh = 0; jh < 2; ++jh)
-#pragma unroll
-    for (int h = 0; h < NH; ++h)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rho = h * 16 + (lane & 15);
-        const int k = kb + jh * 16 + (lane >> 4) * 4 + i;
-        part[((int64_t)by * RP + rho) * K + k] = acc[jh][h][i];
-      }
-}
-
+// The body (tn_body, tn_device.h) with its per-wave tiles in this kernel's own LDS; grid (K / 128, chunks).
 template <int RP, int kD>
 __global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X, int64_t ldx,
                                                  const uint16_t* __restrict__ P, int T, int K, int chunk,
                                                  float* __restrict__ part) {
-  tn_body<RP, kD>(X, ldx, P, T, K, chunk, part, blockIdx.x, blockIdx.y);
+  __shared__ __attribute__((aligned(16))) uint16_t lds[tn_lds_elems<RP>()];
+  tn_body<RP, kD>(X, ldx, P, T, K, chunk, part, blockIdx.x, blockIdx.y, lds);
 }
 
-// The token reductions of mxfp8_lora_tn_batch in one flat grid: job j owns blocks first[j] .. first[j + 1] - 1,
-// `cols` = K / 128 column blocks per token chunk; every job shares T, K and the chunking.
-struct TnBatch {
-  const uint16_t* x[MXFP8_LORA_TN_MAX_JOBS];
-  int64_t ldx[MXFP8_LORA_TN_MAX_JOBS];
-  const uint16_t* p[MXFP8_LORA_TN_MAX_JOBS];
-  float* part[MXFP8_LORA_TN_MAX_JOBS];
-  int rp[MXFP8_LORA_TN_MAX_JOBS];
-  int first[MXFP8_LORA_TN_MAX_JOBS + 1];
-  int n, T, K, chunk, cols;
-};
-
+// The token reductions of mxfp8_lora_tn_batch in one flat grid (TnBatch, tn_device.h).
 template <int kD>
 __global__ __launch_bounds__(256) void tn_batch_kernel(const TnBatch a) {
-  const int b = blockIdx.x;
-  int j = 0;
-  while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
-  const int l = b - a.first[j], bx = l % a.cols, by = l / a.cols;
-  if (a.rp[j] == 16) tn_body<16, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by);
-  else tn_body<32, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by);
+  __shared__ __attribute__((aligned(16))) uint16_t lds[kTnBatchLdsElems];
+  tn_batch_block<kD>(a, blockIdx.x, lds);
 }
 
 // out = bf16(Σ_c part[c, ρ, k]) (then bf16(· scale) when scale != 1), written as [RP, K] or transposed
@@ -838,18 +731,7 @@ __global__ __launch_bounds__(256) void tn_sum_kernel(const float* __restrict__ p
   tn_sum_body(part, chunks, RP, K, scale, transpose, out_f32, out, (int64_t)blockIdx.x * 256 + threadIdx.x);
 }
 
-// The sums of mxfp8_lora_tn_batch's jobs in one flat grid (job j: blocks first[j] .. first[j + 1] - 1).
-struct TnSumBatch {
-  const float* part[MXFP8_LORA_TN_MAX_JOBS];
-  int rp[MXFP8_LORA_TN_MAX_JOBS];
-  float scale[MXFP8_LORA_TN_MAX_JOBS];
-  int transpose[MXFP8_LORA_TN_MAX_JOBS];
-  int out_f32[MXFP8_LORA_TN_MAX_JOBS];
-  void* out[MXFP8_LORA_TN_MAX_JOBS];
-  int first[MXFP8_LORA_TN_MAX_JOBS + 1];
-  int n, chunks, K;
-};
-
+// The sums of mxfp8_lora_tn_batch's jobs in one flat grid (TnSumBatch, tn_device.h).
 __global__ __launch_bounds__(256) void tn_sum_batch_kernel(const TnSumBatch a) {
   const int b = blockIdx.x;
   int j = 0;
@@ -1072,25 +954,26 @@ extern "C" int mxfp8_lora_tn(const void* x, int64_t T, int64_t K, int64_t ld_x, 
   return lora_tn_launch(x, T, K, ld_x, p, rp, chunks, part, scale, transpose, out_f32, out, stream);
 }
 
-extern "C" int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T, int64_t K,
-                                   int64_t chunks, float* part, void* stream) {
+namespace mxk {
+
+int tn_batch_tables(const char* who, const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T, int64_t K,
+                    int64_t chunks, float* part, TnBatch& a, TnSumBatch& sa, int64_t& nb, int64_t& ns) {
   MX_CHECK_ARG(jobs && part && n_jobs >= 1 && n_jobs <= MXFP8_LORA_TN_MAX_JOBS,
-               "mxfp8_lora_tn_batch: 1 to %d jobs and a partial buffer", MXFP8_LORA_TN_MAX_JOBS);
-  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && T < (1LL << 30) && K < (1LL << 24),
-               "mxfp8_lora_tn_batch: need K %% 128 == 0");
-  MX_CHECK_ARG(chunks > 0 && chunks <= 65535 && mx_aligned(part, 16), "mxfp8_lora_tn_batch: bad chunks or part");
+               "%s: 1 to %d jobs and a partial buffer", who, MXFP8_LORA_TN_MAX_JOBS);
+  MX_CHECK_ARG(T > 0 && K > 0 && K % 128 == 0 && T < (1LL << 30) && K < (1LL << 24), "%s: need K %% 128 == 0", who);
+  MX_CHECK_ARG(chunks > 0 && chunks <= 65535 && mx_aligned(part, 16), "%s: bad chunks or part", who);
   const int64_t blocks = (T + 31) / 32;
   const int64_t chunk = (blocks + chunks - 1) / chunks * 32;
   const int64_t used = (T + chunk - 1) / chunk;
-  TnBatch a{};
-  TnSumBatch sa{};
-  int64_t off = 0, nb = 0, ns = 0, max_ld = K;
+  a = TnBatch{};
+  sa = TnSumBatch{};
+  int64_t off = 0, max_ld = K;
+  nb = ns = 0;
   for (int64_t j = 0; j < n_jobs; ++j) {
     const mxfp8_lora_tn_job& jb = jobs[j];
     MX_CHECK_ARG(jb.x && jb.p && jb.out && (jb.rp == 16 || jb.rp == 32) && jb.ld_x >= K && jb.ld_x % 8 == 0 &&
                      mx_aligned(jb.x, 16) && mx_aligned(jb.p, 16),
-                 "mxfp8_lora_tn_batch: job %lld: null pointer, rp not in {16, 32} or bad x stride / alignment",
-                 (long long)j);
+                 "%s: job %lld: null pointer, rp not in {16, 32} or bad x stride / alignment", who, (long long)j);
     a.x[j] = (const uint16_t*)jb.x;
     a.ldx[j] = jb.ld_x;
     a.p[j] = (const uint16_t*)jb.p;
@@ -1109,7 +992,7 @@ extern "C" int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs
     ns += (jb.rp * K + 255) / 256;
     max_ld = std::max(max_ld, jb.ld_x);
   }
-  MX_CHECK_ARG(nb < (1LL << 31), "mxfp8_lora_tn_batch: too many workgroups");
+  MX_CHECK_ARG(nb < (1LL << 31), "%s: too many workgroups", who);
   a.first[n_jobs] = (int)nb;
   sa.first[n_jobs] = (int)ns;
   a.n = sa.n = (int)n_jobs;
@@ -1117,15 +1000,32 @@ extern "C" int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs
   a.K = sa.K = (int)K;
   a.chunk = (int)chunk;
   a.cols = (int)(K / 128);
-  sa.chunks = (int)used;
-  hipStream_t stm = (hipStream_t)stream;
   // the ring depth rule of lora_tn_launch
-  if (T * max_ld * 2 <= (192LL << 20)) tn_batch_kernel<2><<<(unsigned)nb, 256, 0, stm>>>(a);
+  a.kd = T * max_ld * 2 <= (192LL << 20) ? 2 : 1;
+  sa.chunks = (int)used;
+  return MXFP8_OK;
+}
+
+int tn_sum_batch_launch(const TnSumBatch& sa, int64_t ns, hipStream_t stm, const char* who) {
+  tn_sum_batch_kernel<<<(unsigned)ns, 256, 0, stm>>>(sa);
+  MX_CHECK_LAUNCH(who);
+  return MXFP8_OK;
+}
+
+}  // namespace mxk
+
+extern "C" int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T, int64_t K,
+                                   int64_t chunks, float* part, void* stream) {
+  TnBatch a;
+  TnSumBatch sa;
+  int64_t nb = 0, ns = 0;
+  const int rc = tn_batch_tables("mxfp8_lora_tn_batch", jobs, n_jobs, T, K, chunks, part, a, sa, nb, ns);
+  if (rc != MXFP8_OK) return rc;
+  hipStream_t stm = (hipStream_t)stream;
+  if (a.kd == 2) tn_batch_kernel<2><<<(unsigned)nb, 256, 0, stm>>>(a);
   else tn_batch_kernel<1><<<(unsigned)nb, 256, 0, stm>>>(a);
   MX_CHECK_LAUNCH("mxfp8_lora_tn_batch");
-  tn_sum_batch_kernel<<<(unsigned)ns, 256, 0, stm>>>(sa);
-  MX_CHECK_LAUNCH("mxfp8_lora_tn_batch");
-  return MXFP8_OK;
+  return tn_sum_batch_launch(sa, ns, stm, "mxfp8_lora_tn_batch");
 }
 
 // ------------------------------------------------------------------ allocation-free token reduction

@@ -48,6 +48,7 @@
 
 #include "abi_common.h"
 #include "mx_device.h"
+#include "tn_device.h"
 
 // gu leaves the gate|up epilogue with non-temporal stores: it is read again only by the backward, and
 // streaming it past the last-level cache keeps MX(h) and the xS_down partials there for the down GEMM and the
@@ -182,6 +183,13 @@ __device__ __forceinline__ void tile_coords(int t, int tm, int tn, int& mt, int&
   nt = r / rows;
 }
 
+// The instance that can run token reductions past its tiles (mxfp8_gemm_nt_tn): the plain 4-wave GEMM with the
+// rank-32 LoRA epilogue, the fused MLP's dx GEMM at r = 16 (its tiles fill the slots 1.3 times at configuration
+// 3).  Other instances do not compile the reduction.
+template <int kR, int kNW, int kEpi>
+constexpr bool kFoldTn = kR == 32 && kNW == 1 && kEpi == 0;
+static_assert(kTnBatchLdsElems * 2 <= 3 * 26 * 1024, "the folded token reduction borrows the 4-wave ring's LDS");
+
 // 32 bytes of one operand row for the stage's 64-wide K step: chunk c0 (k 16*(l/32)..) and c0 + 2 (k 32 + ..)
 __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw) {
   uint4 lo = *reinterpret_cast<const uint4*>(base + row * kBK + ((c0 ^ sw) << 4));
@@ -196,13 +204,26 @@ template <int kR, int kNW, int kEpi>
 __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, int64_t lda, const uint8_t* __restrict__ B,
     const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, CSeg cseg, Lora lora, Plan plan, int tiled,
-    SwEpi swe, SwBwd swb) {
+    SwEpi swe, SwBwd swb, const TnBatch tnb) {
   using S = Shape<kNW>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[S::kStages * S::kStageBytes];
   __shared__ int arrived;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wn = wave >> 2, wm = wave & 3;  // compute sub-tile: n rows wn*128 + [0,128), m rows wm*64 + [0,64)
+
+  // ---- workgroups past the tiles: the folded token reductions (mxfp8_gemm_nt_tn), in the ring's LDS.  They are
+  // numbered after every tile, so the dispatcher starts them only once each tile has started, in the slots the
+  // last round of tiles leaves free.
+  if constexpr (kFoldTn<kR, kNW, kEpi>) {
+    const int first = 8 * (plan.per_full + plan.per_split);
+    if ((int)blockIdx.x >= first) {
+      uint16_t* tl = reinterpret_cast<uint16_t*>(lds);
+      if (tnb.kd == 2) tn_batch_block<2>(tnb, blockIdx.x - first, tl);
+      else tn_batch_block<1>(tnb, blockIdx.x - first, tl);
+      return;
+    }
+  }
 
   // ---- which tile (and which K piece) this workgroup computes
   const int ns_all = K / kBK;  // even: K % 128 == 0
@@ -872,10 +893,10 @@ int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
 template <int kNW>
 void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, const uint8_t* SB, int64_t ldb,
             int M, int N, int K, const CSeg& cseg, const Lora& lo, int r, const Plan& plan, int layout,
-            hipStream_t stm) {
+            const TnBatch& tnb, int64_t tn_blocks, hipStream_t stm) {
   using S = Shape<kNW>;
-  dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split));
-#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}, SwBwd{}
+  dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split + tn_blocks));
+#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}, SwBwd{}, tnb
   if (!lo.p) gemm_kernel<0, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 16) gemm_kernel<16, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 32) gemm_kernel<32, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
@@ -896,7 +917,8 @@ namespace {
 
 int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb, int64_t M,
               int64_t N, int64_t K, CSeg cseg, const void* lora_p, int64_t ld_p, const void* lora_q, int64_t ld_q,
-              int64_t r, float alpha, int64_t layout, void* workspace, int64_t workspace_bytes, void* stream) {
+              int64_t r, float alpha, int64_t layout, void* workspace, int64_t workspace_bytes, void* stream,
+              const TnBatch& tnb = TnBatch{}, int64_t tn_blocks = 0) {
   void* const c = cseg.ptr[0];
   int64_t ldc = cseg.ld[0];
   MX_CHECK_ARG(a && sa && b && sb && c, "mxfp8_gemm_nt: null pointer");
@@ -946,9 +968,11 @@ int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const v
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   const int tiled = (int)(layout & ~MXFP8_GEMM_WIDE);
   if (wide)
-    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, (hipStream_t)stream);
+    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, tnb, 0,
+              (hipStream_t)stream);
   else
-    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, (hipStream_t)stream);
+    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, tnb, tn_blocks,
+              (hipStream_t)stream);
   MX_CHECK_LAUNCH("mxfp8_gemm_nt");
   return MXFP8_OK;
 }
@@ -965,6 +989,30 @@ extern "C" int mxfp8_gemm_nt(const void* a, const void* sa, int64_t lda, const v
   cs.ld[0] = ldc;
   return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, ld_p, lora_q, ld_q, r, alpha, layout, workspace,
                    workspace_bytes, stream);
+}
+
+extern "C" int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, const void* b, const void* sb,
+                                int64_t ldb, int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p,
+                                int64_t ld_p, const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
+                                const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T_tn, int64_t K_tn,
+                                int64_t chunks, float* part, void* stream) {
+  MX_CHECK_ARG(M > 0 && lora_p && r == 32 && !(layout & MXFP8_GEMM_WIDE),
+               "mxfp8_gemm_nt_tn: needs M > 0, the rank-32 LoRA epilogue and the 4-wave shape (r=%lld layout=%lld)",
+               (long long)r, (long long)layout);
+  TnBatch tnb;
+  TnSumBatch sa_tn;
+  int64_t nb = 0, ns = 0;
+  int rc = tn_batch_tables("mxfp8_gemm_nt_tn", jobs, n_jobs, T_tn, K_tn, chunks, part, tnb, sa_tn, nb, ns);
+  if (rc != MXFP8_OK) return rc;
+  MX_CHECK_ARG(nb + (M + kBM - 1) / kBM * (N / 128) + 8 < (1LL << 31), "mxfp8_gemm_nt_tn: too many workgroups");
+  CSeg cs{};
+  cs.n = 1;
+  cs.ptr[0] = (uint16_t*)c;
+  cs.ld[0] = ldc;
+  rc = gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, ld_p, lora_q, ld_q, r, alpha, layout, nullptr, 0, stream,
+                 tnb, nb);
+  if (rc != MXFP8_OK) return rc;
+  return tn_sum_batch_launch(sa_tn, ns, (hipStream_t)stream, "mxfp8_gemm_nt_tn");
 }
 
 extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, const void* b, const void* sb,
@@ -1024,10 +1072,10 @@ extern "C" int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* 
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   if (r == 16)
     gemm_kernel<16, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(
-        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{});
+        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{}, TnBatch{});
   else
     gemm_kernel<32, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(
-        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{});
+        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{}, TnBatch{});
   MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_fwd");
   return MXFP8_OK;
 }
@@ -1065,7 +1113,7 @@ extern "C" int mxfp8_gemm_swiglu_bwd(const void* a, const void* sa, const void* 
   const int tiled = MXFP8_GEMM_A_TILED | MXFP8_GEMM_B_TILED;
   gemm_kernel<16, 1, kEpiSwiGluBwd><<<grid, Shape<1>::kThreads, 0, (hipStream_t)stream>>>(
       (const uint8_t*)a, (const uint8_t*)sa, K, (const uint8_t*)b, (const uint8_t*)sb, K, (int)M, (int)N, (int)K, cs,
-      Lora{}, plan, tiled, SwEpi{}, sw);
+      Lora{}, plan, tiled, SwEpi{}, sw, TnBatch{});
   MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_bwd");
   return MXFP8_OK;
 }

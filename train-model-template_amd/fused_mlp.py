@@ -42,6 +42,9 @@ FUSED_EPILOGUE = [os.environ.get("MXFP8_FUSED_EPILOGUE", "1") != "0"]
 B_PI = [os.environ.get("MXFP8_B_PI", "1") != "0"]
 # 8-wave backward workgroups summing two 128-column quads in LDS (half the dxa partial bytes)
 WIDE_BWD = [os.environ.get("MXFP8_WIDE_BWD", "1") != "0"]
+# the backward's token reductions (dB_d, dA) folded into the dx GEMM's launch, in the slots its last round of tiles
+# leaves idle (mxfp8_gemm_nt_tn; False: their own launch before the GEMM)
+FOLD_TN = [os.environ.get("MXFP8_FOLD_TN", "1") != "0"]
 # the SwiGLU backward in the epilogue of the dhm GEMM (False: the GEMM, then the separate backward kernel)
 FUSED_BWD_EPILOGUE = [os.environ.get("MXFP8_FUSED_BWD_EPILOGUE", "0") == "1"]
 ACTIVE = [False]  # the fused path ran at least once (read by the step engine to shrink per-layer activations)
@@ -330,20 +333,23 @@ class _MLP(torch.autograd.Function):
         part = torch.empty(chunks * 3 * R * K, dtype=torch.float32, device=dy2.device)
         dB_d = torch.empty((K, R), dtype=torch.float32 if bd_dt == torch.float32 else dt, device=dy2.device)
         dA = torch.empty((2 * R, K), dtype=torch.float32 if fp32_a else dt, device=dy2.device)
-        if 2 * R <= 32:  # the batch takes ranks 16 and 32
-            _native.lora_tn_batch([(dy2, xsd, dB_d, s_d, True), (x2, dxa, dA, 1.0, False)], part)
-        else:
+        tn_jobs = [(dy2, xsd, dB_d, s_d, True), (x2, dxa, dA, 1.0, False)]
+        fold = need_x and 2 * R == 32 and FOLD_TN[0]  # else the reductions run here, before the dx GEMM
+        if not fold and 2 * R <= 32:  # the batch takes ranks 16 and 32
+            _native.lora_tn_batch(tn_jobs, part)
+        elif not fold:
             _native.lora_tn(dy2, xsd, dB_d, part[:chunks * R * K], scale=s_d, transpose=True)
             _native.lora_tn(x2, dxa, dA, part[chunks * R * K:])
         dx = None
         if need_x:
             # dx = bf16(bf16(MX(dg | du) · W_gu) + dxa · S): one K = 2N GEMM with the addmm_ of
             # fused_mlp.py:331 in its epilogue
-            if B_PI[0]:
-                dx = mxfp8.mx_mm(qg, sg, hold.wtp_tl, hold.wtps, lora=(dxa, lw.ST), alpha=1.0,
-                                 layout=3 | _native.GEMM_B_PI, m=T)
+            w, ws, lay = ((hold.wtp_tl, hold.wtps, 3 | _native.GEMM_B_PI) if B_PI[0] else
+                          (hold.wt_tl, hold.wts, 3))
+            if fold:
+                dx = mxfp8.mx_mm_tn(qg, sg, w, ws, (dxa, lw.ST), 1.0, lay, T, tn_jobs, part)
             else:
-                dx = mxfp8.mx_mm(qg, sg, hold.wt_tl, hold.wts, lora=(dxa, lw.ST), alpha=1.0, layout=3, m=T)
+                dx = mxfp8.mx_mm(qg, sg, w, ws, lora=(dxa, lw.ST), alpha=1.0, layout=lay, m=T)
             del qg, sg
             dx = dx.view(*lead, K).to(xdt)
         grads = [dA[:R], dB_g, dA[R:], dB_u, dA_d, dB_d]

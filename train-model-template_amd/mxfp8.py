@@ -284,6 +284,29 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     return out
 
 
+def mx_mm_tn(q, s, wq, ws, lora, alpha, layout, m, tn_jobs, part):
+    """mx_mm with the rank-32 LoRA epilogue, and the token reductions _native.lora_tn_batch(tn_jobs, part) run in
+    the same launch (in the workgroup slots the GEMM's last round of tiles leaves idle), plus their sums: the
+    MLP backward's dx GEMM and its dB_d / dA reductions (/root/reference/scripts/fused_mlp.py:331, :316-318,
+    :333).  Same results as mx_mm then lora_tn_batch."""
+    M, K = q.shape
+    M = m
+    N = wq.shape[0]
+    assert wq.shape[1] == K and q.stride(1) == 1 and wq.stride(1) == 1, (q.shape, wq.shape)
+    assert not (layout & 1) or q.shape[0] == tiled_rows(M), (q.shape, M)
+    out = torch.empty((ft_rows(M) if layout & 8 else M, N), dtype=torch.bfloat16, device=q.device)
+    ev = GEMM_EVENTS
+    if ev is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+    _native.gemm_nt_tn(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, out, lora, tn_jobs, part, alpha=alpha,
+                       layout=layout)
+    if ev is not None:
+        e1.record()
+        ev.append((e0, e1, 2 * M * N * K))
+    return out
+
+
 def swiglu_gemm(q, s, hold, xs, bg, bu, ad, s_g, s_u, m):
     """The gate|up MX GEMM of the fused MLP with the SwiGLU forward in its epilogue: q, s the MX-tiled codes and
     scales of x [m, K]; hold the _GateUp copy (its fused-order operand).  -> (gu [ft_rows(m), 2N] bf16 in the
