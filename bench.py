@@ -777,7 +777,9 @@ def main():
                    "frac_of_mxfp8_peak": round(value / PEAK_MXFP8_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tf / PEAK_MXFP8_TFLOPS, 4), "traffic": _traffic_from_profiles(cfg),
-                     "kernel": "mx_gemm (4 launches per layer: gate|up, down, dh, dx)",
+                     "kernel": "mx_gemm (4 launches per layer: gate|up, down, dh, dx)" +
+                               (" ; the dx launch also runs the backward's token reductions (mxfp8_gemm_nt_tn), "
+                                "timed as GEMM time" if fused_mlp.FOLD_TN[0] else ""),
                      "launches": len(ev), "kernel_ms_per_step": round(gemm_ms / args.steps, 4),
                      "instrumented_ms_per_step": round(wall_ev * 1e3 / args.steps, 4)},
     }
