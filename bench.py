@@ -470,13 +470,14 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
 def _kernel_key(name, grid):
     """A short kernel name: the template head of the demangled name, and for the MX GEMM the MLP shape its grid
     and epilogue rank identify at configuration 3 (4032 / 2016 / 672 workgroups of 256 threads; the dx GEMM with
-    the backward's token reductions folded into its launch has 672 + 512)."""
+    the backward's token reductions folded into its launch has 672 + 512, the down GEMM with the xS_down sum
+    168 + 672)."""
     m = re.search(r"(\w+_kernel)(<[^>]*>)?", name)
     k = (m.group(1) + (m.group(2) or "")) if m else name[:48]
     if m and m.group(1) == "gemm_kernel":
         wg = int(grid) // 256 if grid else 0
         shape = {(4032, "0"): "gate|up", (2016, "0"): "dh", (672, "16"): "down", (672, "32"): "dx",
-                 (1184, "32"): "dx + token reductions"}
+                 (1184, "32"): "dx + token reductions", (840, "16"): "down + xS_down sum"}
         targs = [a.strip() for a in (m.group(2) or "<0").strip("<>").split(",")]
         r = targs[0]
         if len(targs) > 2 and targs[2] == "1":
@@ -629,8 +630,9 @@ def _trace_summary(name, d, steps, cmd, layers=1):
                 srows = list(csv.DictReader(fh))
             f.write("\nrocprofv3 --stats of the same run (every dispatch of the process by kernel name, the gating "
                     "forward and the warmup steps included; in the MLP step each MX GEMM shape has its own template "
-                    "arguments: <16, 1, 1> gate|up with the SwiGLU epilogue, <16, 1, 0> down, <0, 1, 0> dh, "
-                    "<32, 1, 0> dx, with the token reductions in its launch by default):\n\n| kernel | calls | average us | min us | max us | % |\n"
+                    "arguments: <16, 1, 1> gate|up with the SwiGLU epilogue, <16, 1, 0> down (with the xS_down "
+                    "sum in its launch by default), <0, 1, 0> dh, <32, 1, 0> dx (with the token reductions in its "
+                    "launch by default)):\n\n| kernel | calls | average us | min us | max us | % |\n"
                     "|---|---|---|---|---|---|\n")
             for r in srows[:16]:
                 m = re.search(r"(\w+_kernel)(<[^>]*>)?", r["Name"])
@@ -778,8 +780,11 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tf, 2), "peak": PEAK_MXFP8_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tf / PEAK_MXFP8_TFLOPS, 4), "traffic": _traffic_from_profiles(cfg),
                      "kernel": "mx_gemm (4 launches per layer: gate|up, down, dh, dx)" +
-                               (" ; the dx launch also runs the backward's token reductions (mxfp8_gemm_nt_tn), "
-                                "timed as GEMM time" if fused_mlp.FOLD_TN[0] else ""),
+                               ("; the dx launch also runs the backward's token reductions (mxfp8_gemm_nt_tn)"
+                                if fused_mlp.FOLD_TN[0] else "") +
+                               ("; the down launch also sums xS_down (mxfp8_gemm_nt_sum)"
+                                if fused_mlp.FOLD_SUM[0] else "") +
+                               ("; timed as GEMM time" if fused_mlp.FOLD_TN[0] or fused_mlp.FOLD_SUM[0] else ""),
                      "launches": len(ev), "kernel_ms_per_step": round(gemm_ms / args.steps, 4),
                      "instrumented_ms_per_step": round(wall_ev * 1e3 / args.steps, 4)},
     }

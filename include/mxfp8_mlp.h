@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 12
+#define MXFP8_MLP_ABI_VERSION 13
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -439,6 +439,23 @@ int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, const void* b, 
                      const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
                      const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T_tn, int64_t K_tn, int64_t chunks,
                      float* part, void* stream);
+
+/*
+ * mxfp8_gemm_nt (4-wave shape, rank-16 LoRA epilogue, no workspace) whose epilogue operand P is summed in the same
+ * launch: P [M, r] (lora_p, row stride r, written) = bf16(part_scale · Σ_p part[p]) over the n_parts fp32 partials
+ * part [n_parts, M, r], p ascending, exactly as mxfp8_sum_parts computes it.  Workgroups numbered before the
+ * GEMM's tiles compute P and publish each block of rows; a tile waits for its rows only at its epilogue.  A tile
+ * whose wait runs past wait_limit polls sums its own rows of P from part instead (the same bits); wait_limit < 0
+ * takes the default, 0 makes every tile do so (for tests).  Results bit for bit those of mxfp8_sum_parts then
+ * mxfp8_gemm_nt.  Replaces, in the MLP forward, part.sum(0) of the xS_down partials and the down projection's
+ * _scaled_mm + addmm_ (/root/reference/scripts/fused_mlp.py:214, :283-284), separate kernels there.  r must be 16,
+ * M > 0, M · r ≤ 2^26; part and lora_p 16-byte aligned.  Launches that overlap on one GPU stay correct but may
+ * fall back to the per-tile sums.
+ */
+int mxfp8_gemm_nt_sum(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
+                      int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const float* part, int64_t n_parts,
+                      float part_scale, void* lora_p, const void* lora_q, int64_t ld_q, int64_t r, float alpha,
+                      int64_t layout, int64_t wait_limit, void* stream);
 
 /*
  * Allocation-free variant of mxfp8_lora_tn: same arguments without `chunks` / `part`, same result bit for bit as

@@ -33,7 +33,7 @@ def lib():
 def test_header_declares_the_abi():
     names = _declared()
     assert "mxfp8_quant_rows" in names and "mxfp8_gemm_nt" in names and "mxfp8_mlp_bwd" in names
-    assert len(names) == 36, names
+    assert len(names) == 37, names
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -87,6 +87,12 @@ def test_argument_checks_reject_before_launch(lib):
     assert gemm(32, _native.GEMM_WIDE, jobs) == -1 and b"4-wave" in lib.mxfp8_last_error()
     bad = (_native.LoraTnJob * 1)(_native.LoraTnJob(16, 2048, 16, 64, 1.0, 0, 0, 16))
     assert gemm(32, 0, bad) == -1 and b"mxfp8_gemm_nt_tn: job 0" in lib.mxfp8_last_error()
+    # GEMM with its epilogue operand summed in the launch: rank 16 and the 4-wave shape only, aligned buffers
+    gsum = lambda r, layout, part: lib.mxfp8_gemm_nt_sum(p, p, 2048, p, p, 2048, 256, 2048, 2048, p, 2048, part, 96,  # noqa: E731
+                                                         1.0, p, p, 16, r, 1.0, layout, -1, None)
+    assert gsum(32, 0, p) == -1 and b"r == 16" in lib.mxfp8_last_error()
+    assert gsum(16, _native.GEMM_WIDE, p) == -1 and b"4-wave" in lib.mxfp8_last_error()
+    assert gsum(16, 0, ctypes.c_void_p(8)) == -1 and b"misaligned" in lib.mxfp8_last_error()
     assert lib.mxfp8_lora_tn_noalloc_chunks(10752, 2048, 32) == lib.mxfp8_lora_tn_chunks(10752, 2048)
     assert lib.mxfp8_lora_tn_noalloc_chunks(10752, 2048, 32) * 32 * 2048 * 4 <= 16 << 20
     # GEMM K not a multiple of 128

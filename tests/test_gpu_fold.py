@@ -77,3 +77,53 @@ def test_mlp_step_with_and_without_the_fold(T, gpu, monkeypatch):
         outs.append([y.detach(), xi.grad] + [t.detach().clone() for t in _grads(mod)])
     for k, (a, b) in enumerate(zip(*outs)):
         assert torch.equal(a, b), k
+
+
+@pytest.mark.parametrize("M,N,K,n_parts", [(10752, 2048, 6144, 96), (1000, 256, 128, 7), (1, 128, 256, 3),
+                                           (4097, 1024, 512, 24)])
+@pytest.mark.parametrize("wait_limit", [-1, 0])
+def test_gemm_nt_sum_matches_separate_calls(M, N, K, n_parts, wait_limit, gpu):
+    """mxfp8_gemm_nt_sum against mxfp8_sum_parts then mxfp8_gemm_nt: P and the GEMM output bit-identical, with the
+    tiles waiting for the summing workgroups (K = 128: the tiles reach their epilogue almost at once) and with
+    wait_limit 0, where every tile sums its own rows of P from the partials; three launches into one P buffer, so a
+    tile that read an earlier launch's P (a stale cache line) or flag would fail."""
+    g = torch.Generator().manual_seed(M + N + K + n_parts)
+    a = (torch.randn(M, K, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    qa, sa = mxfp8.mx_quant_tiled(a)
+    qb, sb = mxfp8.mx_quant_tiled(b)
+    Q = (torch.randn(N, 16, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    p_out = torch.full((M, 16), float("nan"), dtype=torch.bfloat16, device=gpu)
+    # three launches into the same P buffer with new partials each time: a later launch finds the earlier ones'
+    # flags and P values, and must read neither
+    for it in range(3):
+        part = torch.randn(n_parts, M, 16, generator=g).to(gpu)
+        p_ref = torch.empty((M, 16), dtype=torch.bfloat16, device=gpu)
+        _native.sum_parts(part, n_parts, M * 16, p_ref)
+        ref_c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(p_ref, Q), alpha=2.0, layout=3, m=M)
+        torch.cuda.synchronize()
+        c = mxfp8.mx_mm_sum(qa, sa, qb, sb, part, p_out, Q, 2.0, 3, M, wait_limit=wait_limit)
+        torch.cuda.synchronize()
+        assert torch.equal(p_out.view(torch.int16), p_ref.view(torch.int16)), it
+        assert torch.equal(c.view(torch.int16), ref_c.view(torch.int16)), it
+
+
+@pytest.mark.parametrize("T", [2048, 1000])
+def test_mlp_step_with_and_without_the_forward_sum_fold(T, gpu, monkeypatch):
+    model, inps = workloads.build_model(3, T=T, device=gpu)
+    mxfp8.enable_mxfp8(model)
+    mod = model.layers[0].mlp
+    x, dy = inps[0]["x"].to(gpu), inps[0]["dy"].to(gpu)
+    outs = []
+    for fold in (False, True):
+        monkeypatch.setattr(fused_mlp, "FOLD_SUM", [fold])
+        fused_linear.new_step()
+        for p in model.parameters():
+            p.grad = None
+        xi = x.clone().requires_grad_(True)
+        y = fused_mlp.mlp(mod, xi)
+        y.backward(dy)
+        torch.cuda.synchronize()
+        outs.append([y.detach(), xi.grad] + [t.detach().clone() for t in _grads(mod)])
+    for k, (a, b) in enumerate(zip(*outs)):
+        assert torch.equal(a, b), k

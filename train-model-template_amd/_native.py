@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT, GEMM_B_PI = 1, 2, 4, 8, 16  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -57,6 +57,8 @@ SIGNATURES = {
     "mxfp8_lora_bwd_batch": [_ptr, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "mxfp8_lora_tn": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _f32, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_batch": [_ptr, _i64, _i64, _i64, _i64, _ptr, _ptr],
+    "mxfp8_gemm_nt_sum": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _f32, _ptr,
+                          _ptr, _i64, _i64, _f32, _i64, _i64, _ptr],
     "mxfp8_gemm_nt_tn": [_ptr, _ptr, _i64, _ptr, _ptr, _i64, _i64, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _i64,
                          _i64, _f32, _i64, _ptr, _i64, _i64, _i64, _i64, _ptr, _ptr],
     "mxfp8_lora_tn_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _f32, _i64, _i64, _ptr, _ptr],
@@ -237,6 +239,18 @@ def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, lay
     rcols = None if lora_cols is None else (ctypes.c_int64 * n)(*lora_cols)
     call("mxfp8_gemm_nt_seg", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, n, cols, ptrs, lds, _p(p), ldp, _p(q),
          ldq, r, rcols, float(alpha), layout, like=outs[0])
+
+
+def gemm_nt_sum(a, sa, lda, b, sb, ldb, M, N, K, c, part, p_out, q, alpha=1.0, layout=0, part_scale=1.0,
+                wait_limit=-1):
+    """gemm_nt with the rank-16 epilogue whose P = p_out [M, 16] is summed from part [n, M, 16] in the same launch
+    (include/mxfp8_mlp.h, mxfp8_gemm_nt_sum): p_out = bf16(part_scale · Σ part) as sum_parts writes it, then
+    c = bf16(bf16(A·Bᵀ) + alpha · p_out · qᵀ).  wait_limit 0: every tile sums its own rows (tests)."""
+    _gpu(c, "mxfp8_gemm_nt_sum")
+    assert part.dtype == torch.float32 and part.is_contiguous() and p_out.is_contiguous() and p_out.shape == (M, 16)
+    call("mxfp8_gemm_nt_sum", _p(a), _p(sa), lda, _p(b), _p(sb), ldb, M, N, K, _p(c), c.stride(0), _p(part),
+         part.shape[0], float(part_scale), _p(p_out), _p(q), q.stride(0), 16, float(alpha), layout, int(wait_limit),
+         like=c)
 
 
 def gemm_swiglu_fwd(a, sa, b, sb, M, N, K, xs, bg, bu, ad, s_g, s_u, gu, q_h, s_h, part):

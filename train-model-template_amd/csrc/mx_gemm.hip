@@ -44,10 +44,14 @@
 // pieces run as separate workgroups after the full tiles; each piece writes its fp32 accumulators to the
 // caller's workspace, and the piece that arrives last (agent-scope counter) adds the pieces in part order,
 // which makes the result independent of arrival order, runs the epilogue and resets its counter to zero.
+#include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "abi_common.h"
 #include "mx_device.h"
+#include "presum_device.h"
 #include "tn_device.h"
 
 // gu leaves the gate|up epilogue with non-temporal stores: it is read again only by the backward, and
@@ -188,6 +192,10 @@ __device__ __forceinline__ void tile_coords(int t, int tm, int tn, int& mt, int&
 // 3).  Other instances do not compile the reduction.
 template <int kR, int kNW, int kEpi>
 constexpr bool kFoldTn = kR == 32 && kNW == 1 && kEpi == 0;
+// The instance whose epilogue operand P can be summed in its own launch (mxfp8_gemm_nt_sum): the plain 4-wave GEMM
+// with the rank-16 epilogue, the fused MLP's down GEMM at r = 16.
+template <int kR, int kNW, int kEpi>
+constexpr bool kFoldSum = kR == 16 && kNW == 1 && kEpi == 0;
 static_assert(kTnBatchLdsElems * 2 <= 3 * 26 * 1024, "the folded token reduction borrows the 4-wave ring's LDS");
 
 // 32 bytes of one operand row for the stage's 64-wide K step: chunk c0 (k 16*(l/32)..) and c0 + 2 (k 32 + ..)
@@ -204,7 +212,7 @@ template <int kR, int kNW, int kEpi>
 __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
     const uint8_t* __restrict__ A, const uint8_t* __restrict__ SA, int64_t lda, const uint8_t* __restrict__ B,
     const uint8_t* __restrict__ SB, int64_t ldb, int M, int N, int K, CSeg cseg, Lora lora, Plan plan, int tiled,
-    SwEpi swe, SwBwd swb, const TnBatch tnb) {
+    SwEpi swe, SwBwd swb, const TnBatch tnb, const PreSum pre) {
   using S = Shape<kNW>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[S::kStages * S::kStageBytes];
   __shared__ int arrived;
@@ -212,15 +220,25 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int wn = wave >> 2, wm = wave & 3;  // compute sub-tile: n rows wn*128 + [0,128), m rows wm*64 + [0,64)
 
+  // ---- workgroups before the tiles: the sum of the epilogue operand P (mxfp8_gemm_nt_sum, presum_device.h)
+  int bid = blockIdx.x;
+  if constexpr (kFoldSum<kR, kNW, kEpi>) {
+    if (bid < pre.blocks) {
+      presum_block(pre, bid);
+      return;
+    }
+    bid -= pre.blocks;  // a multiple of 8: the tiles keep their XCDs
+  }
+
   // ---- workgroups past the tiles: the folded token reductions (mxfp8_gemm_nt_tn), in the ring's LDS.  They are
   // numbered after every tile, so the dispatcher starts them only once each tile has started, in the slots the
   // last round of tiles leaves free.
   if constexpr (kFoldTn<kR, kNW, kEpi>) {
     const int first = 8 * (plan.per_full + plan.per_split);
-    if ((int)blockIdx.x >= first) {
+    if (bid >= first) {
       uint16_t* tl = reinterpret_cast<uint16_t*>(lds);
-      if (tnb.kd == 2) tn_batch_block<2>(tnb, blockIdx.x - first, tl);
-      else tn_batch_block<1>(tnb, blockIdx.x - first, tl);
+      if (tnb.kd == 2) tn_batch_block<2>(tnb, bid - first, tl);
+      else tn_batch_block<1>(tnb, bid - first, tl);
       return;
     }
   }
@@ -229,7 +247,7 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
   const int ns_all = K / kBK;  // even: K % 128 == 0
   int tile, part = -1, s_begin = 0, s_end = ns_all;
   {
-    const int i = blockIdx.x, x = i & 7, j = i >> 3;
+    const int i = bid, x = i & 7, j = i >> 3;
     if (i < 8 * plan.per_full) {
       tile = x * plan.per_full + j;
       if (tile >= plan.full) return;
@@ -780,12 +798,24 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
       dst[h] = *reinterpret_cast<const v8bf*>(lq + (int64_t)nr * lora.ld_q + h * 16 + (lane >> 5) * 8);
   };
   if constexpr (kR > 0) {
+    bool p_ready = true;  // P summed in this launch: its rows published, or this tile sums them (presum_device.h)
+    if constexpr (kFoldSum<kR, kNW, kEpi>) {
+      if (pre.blocks) p_ready = presum_wait(pre, m0, min(m0 + kBM, M), &arrived);
+    }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const int mc = min(m0 + wm * 64 + mt * 32 + (lane & 31), M - 1);
 #pragma unroll
-      for (int h = 0; h < kH; ++h)
+      for (int h = 0; h < kH; ++h) {
+        if constexpr (kFoldSum<kR, kNW, kEpi>) {
+          if (pre.blocks) {
+            pf[mt][h] = p_ready ? presum_load8(lp + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8)
+                                : presum_row8(pre, mc, h * 16 + (lane >> 5) * 8, kR);
+            continue;
+          }
+        }
         pf[mt][h] = *reinterpret_cast<const v8bf*>(lp + (int64_t)mc * lora.ld_p + h * 16 + (lane >> 5) * 8);
+      }
     }
     load_q(0, qf[0]);
   }
@@ -893,10 +923,10 @@ int64_t make_plan(int64_t M, int64_t N, int64_t K, int cus, Plan& p) {
 template <int kNW>
 void launch(const uint8_t* A, const uint8_t* SA, int64_t lda, const uint8_t* B, const uint8_t* SB, int64_t ldb,
             int M, int N, int K, const CSeg& cseg, const Lora& lo, int r, const Plan& plan, int layout,
-            const TnBatch& tnb, int64_t tn_blocks, hipStream_t stm) {
+            const TnBatch& tnb, int64_t tn_blocks, const PreSum& pre, hipStream_t stm) {
   using S = Shape<kNW>;
-  dim3 grid((unsigned)(8 * plan.per_full + 8 * plan.per_split + tn_blocks));
-#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}, SwBwd{}, tnb
+  dim3 grid((unsigned)(pre.blocks + 8 * plan.per_full + 8 * plan.per_split + tn_blocks));
+#define GEMM_ARGS A, SA, lda, B, SB, ldb, M, N, K, cseg, lo, plan, layout, SwEpi{}, SwBwd{}, tnb, pre
   if (!lo.p) gemm_kernel<0, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 16) gemm_kernel<16, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
   else if (r == 32) gemm_kernel<32, kNW, kEpiPlain><<<grid, S::kThreads, 0, stm>>>(GEMM_ARGS);
@@ -918,7 +948,7 @@ namespace {
 int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb, int64_t M,
               int64_t N, int64_t K, CSeg cseg, const void* lora_p, int64_t ld_p, const void* lora_q, int64_t ld_q,
               int64_t r, float alpha, int64_t layout, void* workspace, int64_t workspace_bytes, void* stream,
-              const TnBatch& tnb = TnBatch{}, int64_t tn_blocks = 0) {
+              const TnBatch& tnb = TnBatch{}, int64_t tn_blocks = 0, const PreSum& pre = PreSum{}) {
   void* const c = cseg.ptr[0];
   int64_t ldc = cseg.ld[0];
   MX_CHECK_ARG(a && sa && b && sb && c, "mxfp8_gemm_nt: null pointer");
@@ -968,10 +998,10 @@ int gemm_impl(const void* a, const void* sa, int64_t lda, const void* b, const v
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   const int tiled = (int)(layout & ~MXFP8_GEMM_WIDE);
   if (wide)
-    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, tnb, 0,
+    launch<2>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, tnb, 0, PreSum{},
               (hipStream_t)stream);
   else
-    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, tnb, tn_blocks,
+    launch<1>(A, SA, lda, B, SB, ldb, (int)M, (int)N, (int)K, cseg, lo, (int)r, plan, tiled, tnb, tn_blocks, pre,
               (hipStream_t)stream);
   MX_CHECK_LAUNCH("mxfp8_gemm_nt");
   return MXFP8_OK;
@@ -1013,6 +1043,80 @@ extern "C" int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, cons
                  tnb, nb);
   if (rc != MXFP8_OK) return rc;
   return tn_sum_batch_launch(sa_tn, ns, (hipStream_t)stream, "mxfp8_gemm_nt_tn");
+}
+
+// ------------------------------------------------------------------ the epilogue operand summed in the launch
+// The publication flags of mxfp8_gemm_nt_sum's summing workgroups: one file-scope device array per GPU, held
+// until the process ends.  Host code uses its device address (hipGetSymbolAddress, looked up once per device with
+// that device current), never the array's name.  Flags hold launch ids, unique per process, so they need no
+// clearing; launches that overlap on one GPU may overwrite each other's flags, and then a tile sums its rows
+// itself after its polls run out (same results, slower).
+constexpr int64_t kPreSumMaxBlocks = 1 << 16;
+static __device__ __align__(256) unsigned long long presum_flags[kPreSumMaxBlocks];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex presum_mu;
+unsigned long long* presum_flags_dev[kMaxDevices] = {};
+std::atomic<unsigned long long> presum_next_id{1};
+
+unsigned long long* presum_flags_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    mxabi::set_error("mxfp8_gemm_nt_sum: no current device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(presum_mu);
+  if (!presum_flags_dev[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(presum_flags));
+    if (e != hipSuccess || !ptr) {
+      mxabi::set_error("mxfp8_gemm_nt_sum: hipGetSymbolAddress(presum_flags) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+      return nullptr;
+    }
+    presum_flags_dev[dev] = static_cast<unsigned long long*>(ptr);
+  }
+  return presum_flags_dev[dev];
+}
+
+}  // namespace
+
+extern "C" int mxfp8_gemm_nt_sum(const void* a, const void* sa, int64_t lda, const void* b, const void* sb,
+                                 int64_t ldb, int64_t M, int64_t N, int64_t K, void* c, int64_t ldc,
+                                 const float* part, int64_t n_parts, float part_scale, void* lora_p,
+                                 const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
+                                 int64_t wait_limit, void* stream) {
+  MX_CHECK_ARG(M > 0 && part && lora_p && lora_q && r == 16 && !(layout & MXFP8_GEMM_WIDE) && n_parts >= 1,
+               "mxfp8_gemm_nt_sum: needs M > 0, partials, P and Q, r == 16 and the 4-wave shape (r=%lld layout=%lld)",
+               (long long)r, (long long)layout);
+  MX_CHECK_ARG(mx_aligned(part, 16) && mx_aligned(lora_p, 16), "mxfp8_gemm_nt_sum: misaligned part or P");
+  const int64_t count4 = M * r / 4;
+  const int64_t blocks = ((count4 + 255) / 256 + 7) / 8 * 8;
+  MX_CHECK_ARG(blocks <= kPreSumMaxBlocks && n_parts < (1LL << 31), "mxfp8_gemm_nt_sum: M * r = %lld beyond %lld",
+               (long long)(M * r), (long long)(kPreSumMaxBlocks * 1024));
+  unsigned long long* flags = presum_flags_on_current_device();
+  if (!flags) return MXFP8_ERR_ARG;
+  PreSum pre{};
+  pre.part = part;
+  pre.out = (uint16_t*)lora_p;
+  pre.flags = flags;
+  pre.id = presum_next_id.fetch_add(1);
+  pre.count4 = count4;
+  pre.n_parts = (int)n_parts;
+  pre.blocks = (int)blocks;
+  pre.rows_per_block = (int)(1024 / r);
+  // polls of about 0.1 us each (s_sleep 2) before a tile sums its own rows: ~0.1 s by default, far beyond the
+  // sums' own time
+  pre.wait_limit = wait_limit < 0 ? (1 << 20) : (int)std::min<int64_t>(wait_limit, 1 << 30);
+  pre.scale = part_scale;
+  CSeg cs{};
+  cs.n = 1;
+  cs.ptr[0] = (uint16_t*)c;
+  cs.ld[0] = ldc;
+  return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, r, lora_q, ld_q, r, alpha, layout, nullptr, 0, stream,
+                   TnBatch{}, 0, pre);
 }
 
 extern "C" int mxfp8_gemm_nt_seg(const void* a, const void* sa, int64_t lda, const void* b, const void* sb,
@@ -1072,10 +1176,10 @@ extern "C" int mxfp8_gemm_swiglu_fwd(const void* a, const void* sa, const void* 
   const uint8_t *A = (const uint8_t*)a, *SA = (const uint8_t*)sa, *B = (const uint8_t*)b, *SB = (const uint8_t*)sb;
   if (r == 16)
     gemm_kernel<16, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(
-        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{}, TnBatch{});
+        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{}, TnBatch{}, PreSum{});
   else
     gemm_kernel<32, 1, kEpiSwiGluFwd><<<grid, Shape<1>::kThreads, 0, stm>>>(
-        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{}, TnBatch{});
+        A, SA, K, B, SB, K, (int)M, (int)(2 * N), (int)K, cs, Lora{}, plan, tiled, sw, SwBwd{}, TnBatch{}, PreSum{});
   MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_fwd");
   return MXFP8_OK;
 }
@@ -1113,7 +1217,7 @@ extern "C" int mxfp8_gemm_swiglu_bwd(const void* a, const void* sa, const void* 
   const int tiled = MXFP8_GEMM_A_TILED | MXFP8_GEMM_B_TILED;
   gemm_kernel<16, 1, kEpiSwiGluBwd><<<grid, Shape<1>::kThreads, 0, (hipStream_t)stream>>>(
       (const uint8_t*)a, (const uint8_t*)sa, K, (const uint8_t*)b, (const uint8_t*)sb, K, (int)M, (int)N, (int)K, cs,
-      Lora{}, plan, tiled, SwEpi{}, sw, TnBatch{});
+      Lora{}, plan, tiled, SwEpi{}, sw, TnBatch{}, PreSum{});
   MX_CHECK_LAUNCH("mxfp8_gemm_swiglu_bwd");
   return MXFP8_OK;
 }

@@ -45,6 +45,9 @@ WIDE_BWD = [os.environ.get("MXFP8_WIDE_BWD", "1") != "0"]
 # the backward's token reductions (dB_d, dA) folded into the dx GEMM's launch, in the slots its last round of tiles
 # leaves idle (mxfp8_gemm_nt_tn; False: their own launch before the GEMM)
 FOLD_TN = [os.environ.get("MXFP8_FOLD_TN", "1") != "0"]
+# the forward's xS_down partial sum computed by the first workgroups of the down GEMM's launch, which its tiles'
+# epilogues wait for (mxfp8_gemm_nt_sum; False: the sum_parts launch before the GEMM)
+FOLD_SUM = [os.environ.get("MXFP8_FOLD_SUM", "1") != "0"]
 # the SwiGLU backward in the epilogue of the dhm GEMM (False: the GEMM, then the separate backward kernel)
 FUSED_BWD_EPILOGUE = [os.environ.get("MXFP8_FUSED_BWD_EPILOGUE", "0") == "1"]
 ACTIVE = [False]  # the fused path ran at least once (read by the step engine to shrink per-layer activations)
@@ -252,9 +255,11 @@ class _MLP(torch.autograd.Function):
             gu, qh, sh, part = mxfp8.swiglu_gemm(q, sc, hold, xs, bg, bu, ad, s_g, s_u, T)
             del q, sc
             xsd = torch.empty((T, R), dtype=dt, device=x2.device)
-            _native.sum_parts(part, part.shape[0], T * R, xsd)
-            del part
+            if not (R == 16 and FOLD_SUM[0]):  # else summed in the down GEMM's launch below
+                _native.sum_parts(part, part.shape[0], T * R, xsd)
+                part = None
         else:
+            part = None
             # gu = gate | up [T, 2N] in the fused-tile layout the fused kernels read (32 x 32 blocks of 2 KB)
             gu = mxfp8.mx_mm(q, sc, hold.w_tl, hold.ws, layout=_LAYOUT_FT, m=T)
             del q, sc
@@ -262,12 +267,13 @@ class _MLP(torch.autograd.Function):
                 qh, sh, xsd = mlp_fwd(gu, xs, bg, bu, ad, s_g, s_u, True, tiled=True, gu_ft=True)
         if need_out:
             # y = bf16(bf16(MX(h)·W_downᵀ) + s_d · xS_down · B_dᵀ): the addmm_ of fused_mlp.py:284 in the epilogue
-            if B_PI[0] and "_mx_wp_tl" in down.__dict__:
-                y = mxfp8.mx_mm(qh, sh, down._mx_wp_tl, down._mx_wps, lora=(xsd, bd), alpha=s_d,
-                                layout=3 | _native.GEMM_B_PI, m=T)
+            w, ws, lay = ((down._mx_wp_tl, down._mx_wps, 3 | _native.GEMM_B_PI)
+                          if B_PI[0] and "_mx_wp_tl" in down.__dict__ else (down._mx_w_tl, down._mx_ws, 3))
+            if part is not None:  # xsd = bf16(Σ part) summed by the first workgroups of the same launch
+                y = mxfp8.mx_mm_sum(qh, sh, w, ws, part, xsd, bd, s_d, lay, T)
             else:
-                y = mxfp8.mx_mm(qh, sh, down._mx_w_tl, down._mx_ws, lora=(xsd, bd), alpha=s_d, layout=3, m=T)
-            del qh, sh, xsd
+                y = mxfp8.mx_mm(qh, sh, w, ws, lora=(xsd, bd), alpha=s_d, layout=lay, m=T)
+            del qh, sh, xsd, part
         else:  # graph only (checkpoint recompute / prefix backward): nobody reads y
             STATS["bỏ đầu ra"] = STATS.get("bỏ đầu ra", 0) + 1
             y = x2.new_empty(x2.shape[0], down.out_features)

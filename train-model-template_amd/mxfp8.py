@@ -284,6 +284,28 @@ def mx_mm(q, s, wq, ws, out=None, lora=None, alpha=1.0, layout=0, m=None):
     return out
 
 
+def mx_mm_sum(q, s, wq, ws, part, p_out, lq, alpha, layout, m, wait_limit=-1):
+    """mx_mm with the rank-16 epilogue lora = (p_out, lq), its P = p_out summed from the fp32 partials part [n, m, 16]
+    in the same launch (p_out = bf16(Σ part), as _native.sum_parts writes it): the MLP forward's xS_down sum and
+    down GEMM (/root/reference/scripts/fused_mlp.py:214, :283-284).  Same results as sum_parts then mx_mm."""
+    M, K = q.shape
+    M = m
+    N = wq.shape[0]
+    assert wq.shape[1] == K and q.stride(1) == 1 and wq.stride(1) == 1, (q.shape, wq.shape)
+    assert not (layout & 1) or q.shape[0] == tiled_rows(M), (q.shape, M)
+    out = torch.empty((ft_rows(M) if layout & 8 else M, N), dtype=torch.bfloat16, device=q.device)
+    ev = GEMM_EVENTS
+    if ev is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+    _native.gemm_nt_sum(q, s, q.stride(0), wq, ws, wq.stride(0), M, N, K, out, part, p_out, lq, alpha=alpha,
+                        layout=layout, wait_limit=wait_limit)
+    if ev is not None:
+        e1.record()
+        ev.append((e0, e1, 2 * M * N * K))
+    return out
+
+
 def mx_mm_tn(q, s, wq, ws, lora, alpha, layout, m, tn_jobs, part):
     """mx_mm with the rank-32 LoRA epilogue, and the token reductions _native.lora_tn_batch(tn_jobs, part) run in
     the same launch (in the workgroup slots the GEMM's last round of tiles leaves idle), plus their sums: the
