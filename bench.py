@@ -619,7 +619,9 @@ def _trace_summary(name, d, steps, cmd, layers=1):
                 "gating check; "
                 "dispatches before that forward's first MX GEMM (input generation, host-to-device copies, weight "
                 "preparation) are left out. 'per step' = median duration x round(launches / steps); kernels of the "
-                "gating forward alone show 0.\n\n| kernel | launches | median us | us per step | % |\n"
+                "gating forward alone, and the separate launches of the bench's fold-off roofline steps (a few "
+                "steps with the token reductions and the xS_down sum outside the GEMM launches), show 0.\n\n"
+                "| kernel | launches | median us | us per step | % |\n"
                 "|---|---|---|---|---|\n")
         for key, n, med, ps in rows:
             f.write(f"| {key} | {n} | {med:.1f} | {ps:.1f} | {100 * ps / tot if tot else 0:.1f} |\n")
@@ -753,6 +755,26 @@ def main():
     mxfp8.GEMM_EVENTS = None
     gemm_ms = sum(a.elapsed_time(b) for a, b, _ in ev)
     gemm_fl = sum(f for _, _, f in ev)
+    # The same instrumented steps with the folds off, so that each GEMM launch runs the GEMM alone: the dx and down
+    # launches otherwise also run the token reductions and the xS_down sum, and their events time that work as GEMM
+    # time.  Reported beside the main figures as roofline.gemm_alone; the timed steps above keep the folds.
+    folds = (fused_mlp.FOLD_TN[0], fused_mlp.FOLD_SUM[0])
+    gemm_alone = None
+    if any(folds):
+        fused_mlp.FOLD_TN[0] = fused_mlp.FOLD_SUM[0] = False
+        mxfp8.GEMM_EVENTS = []
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ev2 = mxfp8.GEMM_EVENTS
+        mxfp8.GEMM_EVENTS = None
+        fused_mlp.FOLD_TN[0], fused_mlp.FOLD_SUM[0] = folds
+        ms2 = sum(a.elapsed_time(b) for a, b, _ in ev2)
+        tf2 = sum(f for _, _, f in ev2) / (ms2 * 1e-3) / 1e12
+        gemm_alone = {"achieved": round(tf2, 2), "frac": round(tf2 / PEAK_MXFP8_TFLOPS, 4),
+                      "kernel_ms_per_step": round(ms2 / args.steps, 4),
+                      "note": "the same steps with the token reductions and the xS_down sum in launches of their "
+                              "own (MXFP8_FOLD_TN=0, MXFP8_FOLD_SUM=0), so the four GEMM launches run only GEMMs"}
     ms = wall * 1e3 / args.steps
     fl = workloads.flops(T, K, N) * len(mods)
     value = fl / (ms * 1e-3) / 1e12
@@ -786,7 +808,8 @@ def main():
                                 if fused_mlp.FOLD_SUM[0] else "") +
                                ("; timed as GEMM time" if fused_mlp.FOLD_TN[0] or fused_mlp.FOLD_SUM[0] else ""),
                      "launches": len(ev), "kernel_ms_per_step": round(gemm_ms / args.steps, 4),
-                     "instrumented_ms_per_step": round(wall_ev * 1e3 / args.steps, 4)},
+                     "instrumented_ms_per_step": round(wall_ev * 1e3 / args.steps, 4),
+                     "gemm_alone": gemm_alone},
     }
     del model, mods, params, x, dy
     torch.cuda.empty_cache()
