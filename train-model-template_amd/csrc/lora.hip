@@ -35,19 +35,21 @@ struct PrepArgs {
 
 // One thread per output element of: S [2r, K], Sᵀ [K, 2r], b_g, b_u [N, r], b_gᵀ, b_uᵀ [r, N], a_d [r, N],
 // a_dᵀ [N, r], b_d [K, r], b_dᵀ [r, K] (round to nearest even, as Tensor.to(bfloat16)).
-__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
-  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// I: the index type, 32-bit whenever the total fits (the per-element divisions are most of the kernel's work).
+template <typename I>
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, I total) {
+  I i = (I)blockIdx.x * 256 + threadIdx.x;
   if (i >= total) return;
-  const int64_t R = a.R, K = a.K, N = a.N;
-  int64_t n = 2 * R * K;
+  const I R = a.R, K = a.K, N = a.N;
+  I n = 2 * R * K;
   if (i < n) {
-    const int64_t r = i / K, k = i % K;
+    const I r = i / K, k = i % K;
     a.S[i] = bf(r < R ? a.Ag[r * K + k] : a.Au[(r - R) * K + k]);
     return;
   }
   i -= n;
   if (i < n) {
-    const int64_t k = i / (2 * R), r = i % (2 * R);
+    const I k = i / (2 * R), r = i % (2 * R);
     a.ST[i] = bf(r < R ? a.Ag[r * K + k] : a.Au[(r - R) * K + k]);
     return;
   }
@@ -58,13 +60,13 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
   if (i < n) { a.bu[i] = bf(a.Bu[i]); return; }
   i -= n;
   if (i < n) {
-    const int64_t r = i / N, j = i % N;
+    const I r = i / N, j = i % N;
     a.bgT[i] = bf(a.Bg[j * R + r]);
     return;
   }
   i -= n;
   if (i < n) {
-    const int64_t r = i / N, j = i % N;
+    const I r = i / N, j = i % N;
     a.buT[i] = bf(a.Bu[j * R + r]);
     return;
   }
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
   if (i < n) { a.ad[i] = bf(a.Ad[i]); return; }
   i -= n;
   if (i < n) {
-    const int64_t j = i / R, r = i % R;
+    const I j = i / R, r = i % R;
     a.adT[i] = bf(a.Ad[r * N + j]);
     return;
   }
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs a, int64_t total) {
   if (i < n) { a.bd[i] = bf(a.Bd[i]); return; }
   i -= n;
   if (i < n) {
-    const int64_t r = i / K, k = i % K;
+    const I r = i / K, k = i % K;
     a.bdT[i] = bf(a.Bd[k * R + r]);
   }
 }
@@ -794,7 +796,8 @@ extern "C" int mxfp8_lora_prep(const float* Ag, const float* Au, const float* Bg
   const int64_t total = 4 * R * K + 6 * N * R + 2 * K * R;
   PrepArgs a{Ag, Au, Bg, Bu, Ad, Bd, (uint16_t*)S, (uint16_t*)ST, (uint16_t*)bg, (uint16_t*)bu, (uint16_t*)bgT,
              (uint16_t*)buT, (uint16_t*)ad, (uint16_t*)adT, (uint16_t*)bd, (uint16_t*)bdT, (int)R, (int)K, (int)N};
-  prep_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total);
+  if (total < (1LL << 31) - 256) prep_kernel<int><<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, (int)total);
+  else prep_kernel<int64_t><<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(a, total);
   MX_CHECK_LAUNCH("mxfp8_lora_prep");
   return MXFP8_OK;
 }
