@@ -127,3 +127,39 @@ def test_mlp_step_with_and_without_the_forward_sum_fold(T, gpu, monkeypatch):
         outs.append([y.detach(), xi.grad] + [t.detach().clone() for t in _grads(mod)])
     for k, (a, b) in enumerate(zip(*outs)):
         assert torch.equal(a, b), k
+
+
+def test_gemm_nt_sum_on_two_streams_at_once(gpu):
+    """Two mxfp8_gemm_nt_sum launches in flight together on two streams (default priority), each with its own
+    inputs, K = 128 so that tiles reach their epilogue while summing workgroups still run: each launch publishes in
+    its own slice of the flag array, and both results are bit-identical to their separate references."""
+    M, N, K, n_parts = 4000, 512, 128, 12
+    g = torch.Generator().manual_seed(7)
+    cases = []
+    for _ in range(2):
+        a = (torch.randn(M, K, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+        b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+        qa, sa = mxfp8.mx_quant_tiled(a)
+        qb, sb = mxfp8.mx_quant_tiled(b)
+        part = torch.randn(n_parts, M, 16, generator=g).to(gpu)
+        Q = (torch.randn(N, 16, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+        p_ref = torch.empty((M, 16), dtype=torch.bfloat16, device=gpu)
+        _native.sum_parts(part, n_parts, M * 16, p_ref)
+        ref = mxfp8.mx_mm(qa, sa, qb, sb, lora=(p_ref, Q), alpha=1.0, layout=3, m=M)
+        cases.append((qa, sa, qb, sb, part, Q, p_ref, ref))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for rep in range(3):
+        res = [None, None]
+        for k, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                qa, sa, qb, sb, part, Q, _, _ = cases[k]
+                p_out = torch.empty((M, 16), dtype=torch.bfloat16, device=gpu)
+                res[k] = (p_out, mxfp8.mx_mm_sum(qa, sa, qb, sb, part, p_out, Q, 1.0, 3, M))
+        torch.cuda.synchronize()
+        outs.append(res)
+    for res in outs:
+        for k, (p_out, c) in enumerate(res):
+            assert torch.equal(p_out.view(torch.int16), cases[k][6].view(torch.int16)), k
+            assert torch.equal(c.view(torch.int16), cases[k][7].view(torch.int16)), k

@@ -1049,8 +1049,9 @@ extern "C" int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, cons
 // The publication flags of mxfp8_gemm_nt_sum's summing workgroups: one file-scope device array per GPU, held
 // until the process ends.  Host code uses its device address (hipGetSymbolAddress, looked up once per device with
 // that device current), never the array's name.  Flags hold launch ids, unique per process, so they need no
-// clearing; launches that overlap on one GPU may overwrite each other's flags, and then a tile sums its rows
-// itself after its polls run out (same results, slower).
+// clearing.  Each launch takes its own slice of the array, the slice after the previous launch's, so launches
+// that overlap on one GPU (other streams) use different flags unless more than the array's worth of blocks is in
+// flight; if they do collide, a tile sums its rows itself after its polls run out (same results, slower).
 constexpr int64_t kPreSumMaxBlocks = 1 << 16;
 static __device__ __align__(256) unsigned long long presum_flags[kPreSumMaxBlocks];
 
@@ -1101,8 +1102,8 @@ extern "C" int mxfp8_gemm_nt_sum(const void* a, const void* sa, int64_t lda, con
   PreSum pre{};
   pre.part = part;
   pre.out = (uint16_t*)lora_p;
-  pre.flags = flags;
   pre.id = presum_next_id.fetch_add(1);
+  pre.flags = flags + (int64_t)((pre.id * (unsigned long long)blocks) % (unsigned long long)(kPreSumMaxBlocks - blocks + 1));
   pre.count4 = count4;
   pre.n_parts = (int)n_parts;
   pre.blocks = (int)blocks;
