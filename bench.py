@@ -653,6 +653,9 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-quant", action="store_true", help="skip the standalone quantizer timings")
+    ap.add_argument("--no-gemm-alone", action="store_true",
+                    help="skip roofline.gemm_alone (the fold-off GEMM steps), e.g. for a kernel trace of a run with "
+                         "few steps, whose per-step accounting would count their launches")
     ap.add_argument("--cpu-tokens", type=int, default=1024)
     ap.add_argument("--copy-calib", action="store_true")
     ap.add_argument("--only", choices=("epilogues",), help="time only the LoRA epilogues and the grouped linears "
@@ -760,7 +763,7 @@ def main():
     # time.  Reported beside the main figures as roofline.gemm_alone; the timed steps above keep the folds.
     folds = (fused_mlp.FOLD_TN[0], fused_mlp.FOLD_SUM[0])
     gemm_alone = None
-    if any(folds):
+    if any(folds) and not args.no_gemm_alone:
         fused_mlp.FOLD_TN[0] = fused_mlp.FOLD_SUM[0] = False
         mxfp8.GEMM_EVENTS = []
         for _ in range(args.steps):
