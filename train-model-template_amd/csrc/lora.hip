@@ -196,19 +196,20 @@ __global__ __launch_bounds__(256) void nt_kernel(const uint16_t* __restrict__ X,
 // permuted column order that the W operand follows, to the 32x32x16 MFMA.  The waves' partial products are
 // added in LDS in a fixed order.  Rows past T read row T - 1 (and store its codes again, the same bytes).
 // Workgroups past the Tpad / 32 row blocks run the transpose job tp (mxfp8_quant_lora_tp), if any.
+// Ranks 16 and 32: a 3-stage ring (48 KB) and at most 168 VGPRs, so three workgroups share a CU; against the 4-stage
+// ring at two per CU, the same bytes and 0.6-0.9 us faster at configuration 3, cache warm or cold (two rounds, one
+// box).  RP = 64: a 16 KB W tile, 3 stages (72 KB), two workgroups per CU.
 template <int RP>
-__global__ __launch_bounds__(256) void quant_lora_kernel(const uint16_t* __restrict__ X, int64_t ldx, int T, int K,
-                                                         const uint16_t* __restrict__ W, uint8_t* __restrict__ q,
-                                                         uint8_t* __restrict__ s, float scale,
-                                                         uint16_t* __restrict__ out, uint16_t* __restrict__ outT,
-                                                         int Tpad, const TpJob tp) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RP > 32 ? 2 : 3, 8))) void quant_lora_kernel(
+    const uint16_t* __restrict__ X, int64_t ldx, int T, int K, const uint16_t* __restrict__ W,
+    uint8_t* __restrict__ q, uint8_t* __restrict__ s, float scale, uint16_t* __restrict__ out,
+    uint16_t* __restrict__ outT, int Tpad, const TpJob tp) {
   if ((int)blockIdx.x >= Tpad / 32) {  // the whole workgroup: before any barrier
     transpose_pad_job(tp, T, Tpad, (int)blockIdx.x - Tpad / 32);
     return;
   }
-  // RP = 64: a 16 KB W tile, so 3 stages (72 KB) keep two workgroups on a CU, and a second accumulator for
-  // W rows 32..63
-  constexpr int kStages = RP > 32 ? 3 : 4, kTileB = 32 * 256, kStageB = kTileB + (RP > 32 ? 2 : 1) * kTileB;
+  // RP = 64: a second accumulator for W rows 32..63
+  constexpr int kStages = 3, kTileB = 32 * 256, kStageB = kTileB + (RP > 32 ? 2 : 1) * kTileB;
   constexpr int kWDma = RP / 16;      // W DMAs per wave (RP rows x 256 B = RP / 4 KB per stage)
   constexpr int kDma = 2 + kWDma;     // X DMAs: 8 KB per stage, two per wave
   constexpr int kAcc = RP > 32 ? 2 : 1;
