@@ -241,6 +241,9 @@ def gemm_nt_seg(a, sa, lda, b, sb, ldb, M, N, K, outs, lora=None, alpha=1.0, lay
          ldq, r, rcols, float(alpha), layout, like=outs[0])
 
 
+GEMM_NT_SUM_MAX = 1 << 26  # M * r that mxfp8_gemm_nt_sum takes (64 K summing workgroups of 1024 values)
+
+
 def gemm_nt_sum(a, sa, lda, b, sb, ldb, M, N, K, c, part, p_out, q, alpha=1.0, layout=0, part_scale=1.0,
                 wait_limit=-1):
     """gemm_nt with the rank-16 epilogue whose P = p_out [M, 16] is summed from part [n, M, 16] in the same launch

@@ -255,7 +255,7 @@ class _MLP(torch.autograd.Function):
             gu, qh, sh, part = mxfp8.swiglu_gemm(q, sc, hold, xs, bg, bu, ad, s_g, s_u, T)
             del q, sc
             xsd = torch.empty((T, R), dtype=dt, device=x2.device)
-            if not (R == 16 and FOLD_SUM[0]):  # else summed in the down GEMM's launch below
+            if not (R == 16 and FOLD_SUM[0] and T * R <= _native.GEMM_NT_SUM_MAX):  # else in the down launch
                 _native.sum_parts(part, part.shape[0], T * R, xsd)
                 part = None
         else:
