@@ -418,14 +418,14 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
                 continue
             m = re.search(r"(\w*gemm_kernel<[^>]*>)", name)
             g.setdefault((m.group(1) if m else name[:60], grid), []).append(v)
-        return {k: sum(v) / len(v) for k, v in g.items()}
+        return {k: (sum(v) / len(v), len(v)) for k, v in g.items()}
 
     gf, gw = gemm_groups(fetch), gemm_groups(write)
     rows = []
-    for (name, grid), kib in sorted(gf.items()):
+    for (name, grid), (kib, n) in sorted(gf.items()):
         fb = kib * 1024 * f_scale
-        wb = gw.get((name, grid), 0.0) * 1024 * w_scale
-        rows.append({"kernel": name, "grid": grid, "fetch_bytes": round(fb), "write_bytes": round(wb)})
+        wb = gw.get((name, grid), (0.0, 0))[0] * 1024 * w_scale
+        rows.append({"kernel": name, "grid": grid, "dispatches": n, "fetch_bytes": round(fb), "write_bytes": round(wb)})
     if not rows:
         raise SystemExit("no gemm_kernel dispatches in the PMC output")
     # algorithmic bytes of each shape: read both MX operands and their scales once, write the bf16 output,
@@ -436,7 +436,9 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
         sc = lambda R, C: -(-R // 128) * (C // 128) * 512 // 4  # noqa: E731  (one scale per 32 along K)
         alg[nm] = M * Kk + Nn * Kk + sc(M, Kk) + sc(Nn, Kk) + M * Nn * 2 + (M + Nn) * rr * 2
     alg["gate|up"] += T * 2 * r * 2 + 3 * N * r * 2 + T * N + sc(T, N) + T * r * 2
-    per_launch = sum(x["fetch_bytes"] + x["write_bytes"] for x in rows) / len(rows)
+    # weighted by dispatches: the few launches of the bench's fold-off roofline steps count as few
+    per_launch = (sum((x["fetch_bytes"] + x["write_bytes"]) * x["dispatches"] for x in rows)
+                  / sum(x["dispatches"] for x in rows))
     alg_mean = sum(alg.values()) / len(alg)
     summary = {"config": cfg, "kernel": "mx_gemm (gate|up, down, dh, dx)",
                "bytes_per_launch": round(per_launch),
@@ -456,15 +458,25 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
                 f"1 GiB): FETCH x{f_scale:.4f}, WRITE x{w_scale:.4f}.  FETCH_SIZE counts what the L2 fetches from "
                 "beyond itself, so reads served by the 256 MB last-level cache count as well as HBM reads: the "
                 "columns are an upper bound on HBM bytes.\n\n")
-        f.write("| kernel | grid | beyond-L2 read MB | beyond-L2 write MB |\n|---|---|---|---|\n")
+        f.write("| kernel | shape | grid (threads) | dispatches | beyond-L2 read MB | beyond-L2 write MB |\n"
+                "|---|---|---|---|---|---|\n")
         for x in rows:
-            f.write(f"| {x['kernel']} | {x['grid']} | {x['fetch_bytes'] / 1e6:.1f} | {x['write_bytes'] / 1e6:.1f} |\n")
+            f.write(f"| {x['kernel']} | {_md(_kernel_key(x['kernel'], x['grid']).split('> ', 1)[-1])} | {x['grid']} | "
+                    f"{x['dispatches']} | {x['fetch_bytes'] / 1e6:.1f} | {x['write_bytes'] / 1e6:.1f} |\n")
         f.write("\n| shape | algorithmic MB (operands + scales once, bf16 output, LoRA operands) |\n|---|---|\n")
         for nm, b in alg.items():
-            f.write(f"| {nm} | {b / 1e6:.1f} |\n")
-        f.write(f"\nMean per launch: measured {per_launch / 1e6:.1f} MB, algorithmic {alg_mean / 1e6:.1f} MB.\n")
+            f.write(f"| {_md(nm)} | {b / 1e6:.1f} |\n")
+        f.write(f"\nMean per launch, weighted by dispatches: measured {per_launch / 1e6:.1f} MB, algorithmic "
+                f"{alg_mean / 1e6:.1f} MB (the GEMMs' own bytes; the default dx and down launches also carry the "
+                "token reductions, about 95 MB, and the xS_down sum, 66 MB).  The rows with few dispatches are the "
+                "bench's fold-off roofline steps.\n")
     print(json.dumps({"bytes_per_launch": summary["bytes_per_launch"],
                       "algorithmic_bytes_per_launch": summary["algorithmic_bytes_per_launch"]}))
+
+
+def _md(text):
+    """A markdown table cell: the label's '|' (gate|up) escaped."""
+    return text.replace("|", "\\|")
 
 
 def _kernel_key(name, grid):
@@ -566,7 +578,7 @@ def _counters_summary(name, dirs, cmds):
                 "instruments every dispatch, so they run a little longer than in the timed bench).\n\n")
         f.write("| kernel | " + " | ".join(cols) + " |\n|" + "---|" * (len(cols) + 1) + "\n")
         for key in sorted(table):
-            f.write(f"| {key} | " + " | ".join(str(table[key].get(c, "")) for c in cols) + " |\n")
+            f.write(f"| {_md(key)} | " + " | ".join(str(table[key].get(c, "")) for c in cols) + " |\n")
     print(json.dumps(table))
 
 
@@ -624,7 +636,7 @@ def _trace_summary(name, d, steps, cmd, layers=1):
                 "| kernel | launches | median us | us per step | % |\n"
                 "|---|---|---|---|---|\n")
         for key, n, med, ps in rows:
-            f.write(f"| {key} | {n} | {med:.1f} | {ps:.1f} | {100 * ps / tot if tot else 0:.1f} |\n")
+            f.write(f"| {_md(key)} | {n} | {med:.1f} | {ps:.1f} | {100 * ps / tot if tot else 0:.1f} |\n")
         f.write(f"\nSum of kernel time per step: {tot:.1f} us.\n")
         stats = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
         if stats:  # rocprofv3 --stats of the same run: every dispatch of the process, warmup and gating forward too

@@ -59,7 +59,7 @@ def test_trace_summary_counts_steps_from_the_backward_kernel(tmp_path, monkeypat
     md = (tmp_path / "profiles" / "t.md").read_text()
     assert "runs 7 steps" in md and "counted from the backward-kernel launches" in md
     # 8 gate|up launches over 7 steps round to one per step; the fill before the first GEMM is left out
-    assert "| gemm_kernel<16, 1, 1> gate|up + SwiGLU epilogue | 8 | 270.0 | 270.0 |" in md
+    assert "| gemm_kernel<16, 1, 1> gate\\|up + SwiGLU epilogue | 8 | 270.0 | 270.0 |" in md
     assert "| bwd_kernel<16, true, false, 2> | 7 | 150.0 | 150.0 |" in md
     assert "| gemm_kernel<32, 1, 0> dx | 7 | 237.0 | 237.0 |" in md
     assert "fill_kernel" not in md
