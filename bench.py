@@ -474,6 +474,53 @@ def _traffic_summary(cfg, fetch_dir, write_dir, cmd_fetch, cmd_write):
                       "algorithmic_bytes_per_launch": summary["algorithmic_bytes_per_launch"]}))
 
 
+_TABLE_CAPTIONS = {
+    "lora_epilogues_c3_kernel_trace":
+        "T = 10752 tokens, r = 16. The run times `lora_bwd` at dy [T, 2048] (grid y = 16) and [T, 6144] (y = 48) and "
+        "`res_lora` at [T, 2048] (50 calls each), then 13 steps (3 warmup + 10) of the attention-projection step "
+        "(q|k|v 2048/512/512 grouped, o_proj 2048 -> 2048 deferred into `residual_add`, forward + backward), then the "
+        "SwiGLU kernels alone on [T, 6144] and 13 steps of the unfused MLP (`shared_prefix._mlp` with the fused MLP "
+        "off: gate and up as one `group_linear`, the SwiGLU kernels, down as a `group_linear`; gate/up/down are not "
+        "in `mxfp8.FUSED_BWD`, as in the reference, so their backward is the per-layer one, whose bf16 LoRA products "
+        "run on hipBLASLt).  The two steps' kernels share some names and grids, so those rows mix both.  The bench "
+        "line's `lora_epilogues`, `grouped_linears` and `unfused_mlp` entries give the rates.",
+}
+
+
+def _kernel_table(name, d, cmd, min_calls=6):
+    """rocprofv3 --kernel-trace in `d` -> profiles/<name>.md: per (kernel, grid in workgroups) the calls and the
+    mean duration, kernels launched fewer than `min_calls` times (input generation, weight preparation) left out."""
+    files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {d}")
+    agg = {}
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                kname = r["Kernel_Name"]
+                if "at::native" in kname:
+                    m = re.search(r"at::native::(?:\(anonymous namespace\)::)?([A-Za-z_0-9]+)", kname)
+                    key = "torch " + (m.group(1) if m else kname[:30])
+                elif kname.startswith("Cijk_"):  # a hipBLASLt kernel: its macro tile
+                    m = re.search(r"_MT(\d+x\d+x\d+)_", kname)
+                    key = f"hipBLASLt GEMM (MT{m.group(1) if m else '?'})"
+                else:
+                    key = re.sub(r"\(anonymous namespace\)::", "", kname).split("(")[0].replace("void ", "")
+                wg = max(int(r.get("Workgroup_Size_X") or 1), 1)
+                grid = f"{int(r['Grid_Size_X']) // wg} x {r['Grid_Size_Y']}"
+                agg.setdefault((key, grid), []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    rows = sorted(((k, g, v) for (k, g), v in agg.items() if len(v) >= min_calls), key=lambda x: -sum(x[2]))
+    with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
+        f.write(f"# Kernel trace: {name}\n\nCommand (GPU box, repo root as `$GRAFT_REPO_ROOT`):\n\n```\ncd /tmp && "
+                f"export TMPDIR=/tmp\n{cmd}\npython3 bench.py --kernel-table {name} <trace dir>\n```\n\n")
+        if name in _TABLE_CAPTIONS:
+            f.write(_TABLE_CAPTIONS[name] + "\n\n")
+        f.write(f"Kernels launched fewer than {min_calls} times are left out.\n\n| kernel | grid (workgroups) | calls | "
+                "mean us |\n|---|---|---|---|\n")
+        for k, g, v in rows:
+            f.write(f"| {_md(k)} | {g} | {len(v)} | {sum(v) / len(v):.1f} |\n")
+
+
 def _md(text):
     """A markdown table cell: the label's '|' (gate|up) escaped."""
     return text.replace("|", "\\|")
@@ -681,6 +728,9 @@ def main():
                     help="summarize a rocprofv3 --kernel-trace run of STEPS steps into profiles/NAME.md")
     ap.add_argument("--trace-command", default="", help="the profiling command, for the summary")
     ap.add_argument("--trace-layers", type=int, default=1, help="MLP layers per step of the traced run (steps = 0)")
+    ap.add_argument("--kernel-table", nargs=2, metavar=("NAME", "DIR"),
+                    help="rocprofv3 --kernel-trace output -> profiles/NAME.md: calls and mean duration per kernel and "
+                         "grid (with --trace-command)")
     args = ap.parse_args()
     if args.trace_summary:
         _trace_summary(args.trace_summary[0], args.trace_summary[1], float(args.trace_summary[2]), args.trace_command,
@@ -688,6 +738,9 @@ def main():
         return
     if args.counters_summary:
         _counters_summary(args.counters_summary[0], args.counters_summary[1:], args.counters_commands)
+        return
+    if args.kernel_table:
+        _kernel_table(args.kernel_table[0], args.kernel_table[1], args.trace_command)
         return
     if args.traffic_summary:
         _traffic_summary(args.config, *args.traffic_summary, *args.traffic_commands)

@@ -91,3 +91,36 @@ def test_more_than_one_gpu_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_kernel_table_groups_by_kernel_and_grid(tmp_path, monkeypatch):
+    """--kernel-table: one row per (kernel, grid in workgroups) with calls and mean duration, hipBLASLt names cut to
+    their macro tile, torch kernels by their functor name, kernels launched fewer than six times left out."""
+    rows, t, i = [], 1000, 0
+    spec = [("void (anonymous namespace)::lora_bwd_kernel<16, true, true>(...)", 20.0, 31 * 256, 8),
+            ("void (anonymous namespace)::lora_bwd_kernel<16, true, true>(...)", 50.0, 11 * 256, 6),
+            ("Cijk_Ailk_Bjlk_BBS_BH_Bias_HA_S_SAV_UserArgs_MT16x64x256_MI16x16x1_SN_LDSB1", 60.0, 96 * 256, 7),
+            ("void at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<float>>(...)", 3.0, 48 * 256, 6),
+            ("void (anonymous namespace)::pack_kernel(...)", 6.0, 496 * 256, 5)]
+    for name, us, grid, n in spec:
+        for _ in range(n):
+            r = _row(i, name, t, us, grid)
+            r["Workgroup_Size_X"] = "256"
+            rows.append(r)
+            t += int(us * 1000) + 100
+            i += 1
+    d = tmp_path / "epi"
+    os.makedirs(d)
+    with open(d / "run_kernel_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=_FIELDS, quoting=csv.QUOTE_ALL)
+        w.writeheader()
+        w.writerows(rows)
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    os.makedirs(tmp_path / "profiles")
+    bench._kernel_table("lora_epilogues_c3_kernel_trace", str(d), "cmd")
+    md = (tmp_path / "profiles" / "lora_epilogues_c3_kernel_trace.md").read_text()
+    assert "| lora_bwd_kernel<16, true, true> | 31 x 1 | 8 | 20.0 |" in md
+    assert "| lora_bwd_kernel<16, true, true> | 11 x 1 | 6 | 50.0 |" in md
+    assert "| hipBLASLt GEMM (MT16x64x256) | 96 x 1 | 7 | 60.0 |" in md
+    assert "| torch vectorized_elementwise_kernel | 48 x 1 | 6 | 3.0 |" in md
+    assert "pack_kernel" not in md and "attention-projection step" in md
