@@ -450,7 +450,8 @@ int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, const void* b, 
  * mxfp8_gemm_nt.  Replaces, in the MLP forward, part.sum(0) of the xS_down partials and the down projection's
  * _scaled_mm + addmm_ (/root/reference/scripts/fused_mlp.py:214, :283-284), separate kernels there.  r must be 16,
  * M > 0, M · r ≤ 2^26; part and lora_p 16-byte aligned.  Launches that overlap on one GPU stay correct but may
- * fall back to the per-tile sums.
+ * fall back to the per-tile sums.  On a stream under graph capture it records mxfp8_sum_parts and then
+ * mxfp8_gemm_nt, two launches (a replayed launch would repeat the id its flags are matched against).
  */
 int mxfp8_gemm_nt_sum(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
                       int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const float* part, int64_t n_parts,

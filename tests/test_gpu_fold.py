@@ -5,7 +5,10 @@ calls compute, with the same kernels' arithmetic in the same order, so the bar i
   - the GEMM output and both reductions against mxfp8_gemm_nt followed by mxfp8_lora_tn_batch, at the MLP's
     configuration-3 dx shape (672 tiles: the reductions run in the last round's idle slots), at a small shape
     whose few tiles leave most slots free from the start, with T not a multiple of 32 or 128, and at T = 1;
-  - the whole fused MLP step with the fold on and off (fused_mlp.FOLD_TN): output, dx and every LoRA gradient."""
+  - the whole fused MLP step with the fold on and off (fused_mlp.FOLD_TN): output, dx and every LoRA gradient.
+The same bar for mxfp8_gemm_nt_sum (the forward's down GEMM whose launch also sums its epilogue operand from the
+xS_down partials, :214, :283-284) against mxfp8_sum_parts then mxfp8_gemm_nt, and for both entry points captured
+into a HIP graph and replayed with new inputs."""
 import pytest
 import torch
 
@@ -163,3 +166,93 @@ def test_gemm_nt_sum_on_two_streams_at_once(gpu):
         for k, (p_out, c) in enumerate(res):
             assert torch.equal(p_out.view(torch.int16), cases[k][6].view(torch.int16)), k
             assert torch.equal(c.view(torch.int16), cases[k][7].view(torch.int16)), k
+
+
+def _capture(fn):
+    """fn() captured into a HIP graph (after one warm-up call on the capture stream); returns (graph, its output)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    return graph, out
+
+
+def test_gemm_nt_sum_under_graph_capture(gpu):
+    """mxfp8_gemm_nt_sum captured into a HIP graph and replayed four times, new partials copied in eagerly before
+    each replay and the eager references computed between replays: every replay's P and GEMM output bit-identical
+    to mxfp8_sum_parts then mxfp8_gemm_nt on that replay's partials.  A replay repeats the captured launch's
+    arguments, so a flag matched against a captured launch id would already hold it from the replay before (K =
+    128: the tiles reach their epilogue while the sums run), and a tile would read the previous replay's P."""
+    M, N, K, n_parts = 4000, 512, 128, 12
+    gen = torch.Generator().manual_seed(11)
+    a = (torch.randn(M, K, generator=gen) * 0.1).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=gen) * 0.02).to(torch.bfloat16).to(gpu)
+    qa, sa = mxfp8.mx_quant_tiled(a)
+    qb, sb = mxfp8.mx_quant_tiled(b)
+    Q = (torch.randn(N, 16, generator=gen) * 0.1).to(torch.bfloat16).to(gpu)
+    part = torch.randn(n_parts, M, 16, generator=gen).to(gpu)
+    p_out = torch.empty((M, 16), dtype=torch.bfloat16, device=gpu)
+    graph, c = _capture(lambda: mxfp8.mx_mm_sum(qa, sa, qb, sb, part, p_out, Q, 1.5, 3, M))
+    for it in range(4):
+        part.copy_(torch.randn(n_parts, M, 16, generator=gen).to(gpu))
+        p_ref = torch.empty((M, 16), dtype=torch.bfloat16, device=gpu)
+        _native.sum_parts(part, n_parts, M * 16, p_ref)
+        ref = mxfp8.mx_mm(qa, sa, qb, sb, lora=(p_ref, Q), alpha=1.5, layout=3, m=M)
+        torch.cuda.synchronize()
+        p_out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(p_out.view(torch.int16), p_ref.view(torch.int16)), it
+        assert torch.equal(c.view(torch.int16), ref.view(torch.int16)), it
+    del graph
+
+
+def test_gemm_nt_tn_under_graph_capture(gpu):
+    """mxfp8_gemm_nt_tn captured into a HIP graph and replayed three times with new token-side inputs copied in
+    before each replay: the GEMM output and both reductions bit-identical to the separate eager calls."""
+    M, N, K, Kt = 1000, 256, 512, 768
+    gen = torch.Generator().manual_seed(12)
+    a = (torch.randn(M, K, generator=gen) * 0.1).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=gen) * 0.02).to(torch.bfloat16).to(gpu)
+    qa, sa = mxfp8.mx_quant_tiled(a)
+    qb, sb = mxfp8.mx_quant_tiled(b)
+    P = (torch.randn(M, 32, generator=gen) * 0.1).to(torch.bfloat16).to(gpu)
+    Q = (torch.randn(N, 32, generator=gen) * 0.1).to(torch.bfloat16).to(gpu)
+    x0 = torch.empty((M, Kt), dtype=torch.bfloat16, device=gpu)
+    p0 = torch.empty((M, 16), dtype=torch.bfloat16, device=gpu)
+    x1 = torch.empty((M, Kt), dtype=torch.bfloat16, device=gpu)
+    p1 = torch.empty((M, 32), dtype=torch.bfloat16, device=gpu)
+    chunks = _native.lora_tn_chunks(M, Kt)
+    part = torch.empty(chunks * 48 * Kt, device=gpu)
+    o0 = torch.empty((Kt, 16), dtype=torch.bfloat16, device=gpu)
+    o1 = torch.empty((32, Kt), dtype=torch.float32, device=gpu)
+
+    def fill():
+        x0.copy_(torch.randn(M, Kt, generator=gen).to(torch.bfloat16))
+        p0.copy_((torch.randn(M, 16, generator=gen) * 0.1).to(torch.bfloat16))
+        x1.copy_(torch.randn(M, Kt, generator=gen).to(torch.bfloat16))
+        p1.copy_((torch.randn(M, 32, generator=gen) * 0.1).to(torch.bfloat16))
+
+    fill()
+    graph, c = _capture(lambda: mxfp8.mx_mm_tn(qa, sa, qb, sb, (P, Q), 2.0, 3, M,
+                                               [(x0, p0, o0, 2.0, True), (x1, p1, o1, 1.0, False)], part))
+    for it in range(3):
+        fill()
+        ref_c = mxfp8.mx_mm(qa, sa, qb, sb, lora=(P, Q), alpha=2.0, layout=3, m=M)
+        r0 = torch.empty((Kt, 16), dtype=torch.bfloat16, device=gpu)
+        r1 = torch.empty((32, Kt), dtype=torch.float32, device=gpu)
+        _native.lora_tn_batch([(x0, p0, r0, 2.0, True), (x1, p1, r1, 1.0, False)], torch.empty_like(part))
+        torch.cuda.synchronize()
+        o0.fill_(float("nan"))
+        o1.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c.view(torch.int16), ref_c.view(torch.int16)), it
+        assert torch.equal(o0.view(torch.int16), r0.view(torch.int16)), it
+        assert torch.equal(o1.view(torch.int32), r1.view(torch.int32)), it
+    del graph

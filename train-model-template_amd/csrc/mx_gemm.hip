@@ -1097,6 +1097,21 @@ extern "C" int mxfp8_gemm_nt_sum(const void* a, const void* sa, int64_t lda, con
   const int64_t blocks = ((count4 + 255) / 256 + 7) / 8 * 8;
   MX_CHECK_ARG(blocks <= kPreSumMaxBlocks && n_parts < (1LL << 31), "mxfp8_gemm_nt_sum: M * r = %lld beyond %lld",
                (long long)(M * r), (long long)(kPreSumMaxBlocks * 1024));
+  CSeg cs{};
+  cs.n = 1;
+  cs.ptr[0] = (uint16_t*)c;
+  cs.ld[0] = ldc;
+  // A launch captured into a graph would keep its launch id on every replay: a tile of the second replay could
+  // find its flags already holding that id from the first and read P before this replay's sums.  A captured call
+  // (or one on a stream whose capture state cannot be read) therefore sums P in a launch of its own, the same
+  // bits, before the plain GEMM.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    const int rc = mxfp8_sum_parts(part, n_parts, M * r, part_scale, lora_p, 1, stream);
+    if (rc != MXFP8_OK) return rc;
+    return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, r, lora_q, ld_q, r, alpha, layout, nullptr, 0,
+                     stream);
+  }
   unsigned long long* flags = presum_flags_on_current_device();
   if (!flags) return MXFP8_ERR_ARG;
   PreSum pre{};
@@ -1112,10 +1127,6 @@ extern "C" int mxfp8_gemm_nt_sum(const void* a, const void* sa, int64_t lda, con
   // sums' own time
   pre.wait_limit = wait_limit < 0 ? (1 << 20) : (int)std::min<int64_t>(wait_limit, 1 << 30);
   pre.scale = part_scale;
-  CSeg cs{};
-  cs.n = 1;
-  cs.ptr[0] = (uint16_t*)c;
-  cs.ld[0] = ldc;
   return gemm_impl(a, sa, lda, b, sb, ldb, M, N, K, cs, lora_p, r, lora_q, ld_q, r, alpha, layout, nullptr, 0, stream,
                    TnBatch{}, 0, pre);
 }
