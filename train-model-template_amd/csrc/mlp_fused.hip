@@ -185,10 +185,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kFwdWavesPe
 //     dB_g, dB_u, dA_dᵀ contributions D[j][ρ] (16x16x32 MFMA, k = rows): the wave writes its dg, then du,
 //     then h rows to its LDS tile and reads each back column-wise with ds_read_b64_tr_b16; accumulated over
 //     the super-block in registers and stored after it.
-// The large operands of the next row block (gu, dhm) are loaded one row block ahead; the small per-row
-// operands (xs, dxd and their transposed copies, L2-resident) are issued first in each row block, so waiting
-// for them leaves the prefetch in flight.  Rows past T quantize row T - 1 again (the same bytes) and then
-// zero their values, so they add nothing to dB / dA_d.
+// The large operands of the next row block (gu, dhm) are loaded one row block ahead.  The small per-row operands
+// (xs, dxd and their transposed copies, L2-resident; the same 6 KB at r = 16 for every wave of the workgroup):
+//   r = 16 (kStage): staged in LDS one row block ahead, by global_load_lds DMAs issued at the start of the row
+//     block before (each 1 KB DMA lands as the lane-ordered MFMA operand, so the reads are conflict-free
+//     ds_read_b128), one copy per workgroup instead of one per wave.  Each wave drains its memory counter before
+//     the row block's barrier, and the block's code, scale and partial stores are issued after that barrier:
+//     the memory counter completes in issue order, so a wait for a load issued behind a store also waits for
+//     the store, and the previous form's first wait of every row block (for the small loads, issued behind the
+//     previous block's stores) paid the stores' latency.  Configuration 3, graph timing, two alternating pairs
+//     on one box, outputs bit-identical: 148.1-149.6 against 140.8-144.4 us;
+//   r = 32: loaded per wave at the start of each row block, before the next block's large operands, so
+//     waiting for them leaves the prefetch in flight (the staged form's 24 KB would lower the 4-wave kernel's
+//     workgroups per CU).
+// Rows past T quantize row T - 1 again (the same bytes) and then zero their values, so they add nothing to
+// dB / dA_d.
 // Register budget: two waves per SIMD (<= 256 VGPRs; with three the kernel spills), i.e. two workgroups per
 // CU (58 KB of LDS each at r = 16).
 // kQ = 2: 8 waves, two quads side by side (wave w on tile 8o + w of the column group): the dxa products are
@@ -215,10 +226,16 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
   // kRB buffers of the per-wave products: with two, row block b fills buffer b % 2 while the waves still sum
   // block b - 1's, so one barrier per row block suffices; taken where they fit the LDS of the workgroups a CU
   // holds now (one with 8 waves, two with 4)
+  constexpr bool kStage = R == 16;                                      // small operands staged in LDS
+  constexpr int kOps = 6 * (R / 16), kOpDma = (kOps + kW - 1) / kW;  // 1 KB operand images, DMAs per wave
   constexpr int kRedBytes = kW * 32 * (3 * R + 1) * 4, kTrBytes = kW * 32 * kTrLd * 2;
-  constexpr int kRB = 2 * kRedBytes + kTrBytes <= (kQ == 2 ? 160 : 80) * 1024 ? 2 : 1;
+  constexpr int kStageBytes = kStage ? 2 * kOps * 1024 : 0, kLdsCap = (kQ == 2 ? 160 : 80) * 1024;
+  constexpr int kRB = 2 * kRedBytes + kTrBytes + kStageBytes <= kLdsCap ? 2 : 1;
+  static_assert(kRB * kRedBytes + kTrBytes + kStageBytes <= kLdsCap, "LDS of the workgroups a CU holds");
   __shared__ float red[kRB][kW][32][3 * R + 1];                        // per-wave dxa | dxa_u | xS products
   __shared__ __attribute__((aligned(16))) uint16_t trt[kW][32 * kTrLd];  // per-wave dg, then du, then h rows
+  // two row blocks' small operands: images xg, xu, xd, tg, tu, td (R / 16 each), lane l's 16 bytes at 16 l
+  __shared__ __attribute__((aligned(16))) uint8_t sop[kStage ? 2 : 1][kStage ? kOps : 1][kStage ? 1024 : 16];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   const int r0 = blockIdx.x * SB, r1 = min(r0 + SB, Tpad);
   const int c0 = blockIdx.y * CG;
@@ -266,21 +283,56 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
 #endif
       load16_rc(dhm, mc, jb + lg * 16, N, gu_ft, in.d);
     };
+    // DMA of row block rbn's small operands into sop[sb]: wave w issues images w * kOpDma + j (modulo kOps: the
+    // slots past the last image repeat one, the same bytes to the same place), so every wave issues kOpDma DMAs
+    // and one memory-counter wait fits all.  Lane l fetches exactly the 16 bytes that it reads back as its MFMA
+    // operand (the per-wave loads of the r = 32 form below): xs / dxd rows min(rbn + l % 32, T - 1), xsᵀ / dxdᵀ
+    // rows 16 h + l % 16 at columns rbn + 8 (l / 16) (rbn + 32 <= Tpad, the padded width).
+    auto stage = [&](int rbn, int sb) {
+#pragma unroll
+      for (int j = 0; j < kOpDma; ++j) {
+        const int o = (w * kOpDma + j) % kOps, kind = o / (R / 16), h = o % (R / 16);
+        const int mcn = min(rbn + (lane & 31), T - 1);
+        const int rr = h * 16 + (lane & 15), mo = rbn + (lane >> 4) * 8;
+        const uint16_t* src;
+        if (kind == 0) src = xs + (int64_t)mcn * 2 * R + h * 16 + lg * 8;
+        else if (kind == 1) src = xs + (int64_t)mcn * 2 * R + R + h * 16 + lg * 8;
+        else if (kind == 2) src = dxd + (int64_t)mcn * R + h * 16 + lg * 8;
+        else if (kind == 3) src = xsT + (int64_t)rr * Tpad + mo;
+        else if (kind == 4) src = xsT + (int64_t)(R + rr) * Tpad + mo;
+        else src = dxdT + (int64_t)rr * Tpad + mo;
+        dma16(src, lds_addr(&sop[sb][o][0]));
+      }
+    };
+    auto sop_read = [&](int sb, int o) { return as_bf8(*reinterpret_cast<const uint4*>(&sop[sb][o][lane * 16])); };
     auto block = [&](int rb, const RowIn& cur, RowIn& nxt, const int buf) {
       const int m = rb + (lane & 31);
       const bool live = m < T;
       const int mc = live ? m : T - 1;
+      const int sb = ((rb - r0) >> 5) & 1;  // staged operands of this row block (kStage)
       // small operands of this row block first (see above), then the next row block's large ones
       v8bf xg[R / 16], xu[R / 16], xd[R / 16], tg[R / 16], tu[R / 16], td[R / 16];
+      if constexpr (kStage) {
+        // the next row block's DMA goes to the other buffer, which the waves finished reading before the
+        // previous row block's barrier
+        stage(min(rb + 32, r1 - 32), sb ^ 1);
 #pragma unroll
-      for (int h = 0; h < R / 16; ++h) {
-        xg[h] = load_bf8(xs + (int64_t)mc * 2 * R + h * 16 + lg * 8);
-        xu[h] = load_bf8(xs + (int64_t)mc * 2 * R + R + h * 16 + lg * 8);
-        xd[h] = load_bf8(dxd + (int64_t)mc * R + h * 16 + lg * 8);
-        const int rr = h * 16 + (lane & 15), mo = rb + (lane >> 4) * 8;
-        tg[h] = load_bf8(xsT + (int64_t)rr * Tpad + mo);
-        tu[h] = load_bf8(xsT + (int64_t)(R + rr) * Tpad + mo);
-        td[h] = load_bf8(dxdT + (int64_t)rr * Tpad + mo);
+        for (int h = 0; h < R / 16; ++h) {
+          xg[h] = sop_read(sb, 0 * (R / 16) + h);
+          xu[h] = sop_read(sb, 1 * (R / 16) + h);
+          xd[h] = sop_read(sb, 2 * (R / 16) + h);
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < R / 16; ++h) {
+          xg[h] = load_bf8(xs + (int64_t)mc * 2 * R + h * 16 + lg * 8);
+          xu[h] = load_bf8(xs + (int64_t)mc * 2 * R + R + h * 16 + lg * 8);
+          xd[h] = load_bf8(dxd + (int64_t)mc * R + h * 16 + lg * 8);
+          const int rr = h * 16 + (lane & 15), mo = rb + (lane >> 4) * 8;
+          tg[h] = load_bf8(xsT + (int64_t)rr * Tpad + mo);
+          tu[h] = load_bf8(xsT + (int64_t)(R + rr) * Tpad + mo);
+          td[h] = load_bf8(dxdT + (int64_t)rr * Tpad + mo);
+        }
       }
       fetch(min(rb + 32, r1 - 32), nxt);  // past the super-block's end this reloads a row block, unused
       __builtin_amdgcn_sched_barrier(0);
@@ -334,9 +386,16 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
         o2[0] = make_uint4(duw[0], duw[1], duw[2], duw[3]);
         o2[1] = make_uint4(duw[4], duw[5], duw[6], duw[7]);
       }
+      // MX codes of dg and du: stored now, or (kStage) after the row block's barrier
+      uint4 cg = {}, cu = {};
+      uint32_t eg = 0, eu = 0;
       if (kQuant) {
-        quant16(dgw, lane, m, live, q, mc, 2 * N, q_tiled, jb + lg * 16, s, 2 * N / 128);
-        quant16(duw, lane, m, live, q, mc, 2 * N, q_tiled, N + jb + lg * 16, s, 2 * N / 128);
+        eg = quant16_codes(dgw, cg);
+        eu = quant16_codes(duw, cu);
+        if (!kStage) {
+          quant16_store(cg, eg, m, live, q, mc, 2 * N, q_tiled, jb + lg * 16, s, 2 * N / 128);
+          quant16_store(cu, eu, m, live, q, mc, 2 * N, q_tiled, N + jb + lg * 16, s, 2 * N / 128);
+        }
       }
       if (!live) {  // padded rows add nothing to the sums below
 #pragma unroll
@@ -382,12 +441,28 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
           for (int h = 0; h < R / 16; ++h) acc[jh][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, tf[h], acc[jh][h], 0, 0, 0);
         }
       };
+      if constexpr (kStage) {
+#pragma unroll
+        for (int h = 0; h < R / 16; ++h) {  // read where used: not held in registers across the block
+          tg[h] = sop_read(sb, 3 * (R / 16) + h);
+          tu[h] = sop_read(sb, 4 * (R / 16) + h);
+          td[h] = sop_read(sb, 5 * (R / 16) + h);
+        }
+      }
       tr_pass(dgw, tg, dbg);
       tr_pass(duw, tu, dbu);
       tr_pass(hw, td, dad);
+      // kStage: this wave's DMA of the next row block's operands has landed (a drain: the count needs no
+      // knowledge of what the compiler issued in between; the block's own stores come after the barrier, so
+      // only older ones are waited for); after the barrier every wave's DMA has
+      if constexpr (kStage) wait_vmcnt<0>();
       // sum the waves' products (fixed order) into the pass's own partial (stores only: a read-modify-write
       // here would wait behind the next row block's prefetch, the memory counter completing in order)
       __syncthreads();
+      if (kStage && kQuant) {
+        quant16_store(cg, eg, m, live, q, mc, 2 * N, q_tiled, jb + lg * 16, s, 2 * N / 128);
+        quant16_store(cu, eu, m, live, q, mc, 2 * N, q_tiled, N + jb + lg * 16, s, 2 * N / 128);
+      }
       float* qpart = dxa_part + ((int64_t)(blockIdx.y * (CG / kCols) + oc) * T + rb) * 3 * R;
       for (int idx = threadIdx.x; idx < 32 * 3 * R; idx += 256 * kQ) {
         const int mm = idx / (3 * R), cc = idx % (3 * R);
@@ -400,6 +475,11 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
     };
     RowIn b0, b1;  // alternating buffers: no register copies between row blocks
     fetch(r0, b0);
+    if constexpr (kStage) {  // the first row block's operands
+      stage(r0, 0);
+      wait_vmcnt<0>();
+      __syncthreads();
+    }
     int rb = r0;
     for (; rb + 32 < r1; rb += 64) {
       block(rb, b0, b1, 0);
@@ -408,6 +488,12 @@ __global__ __launch_bounds__(256 * kQ) __attribute__((amdgpu_waves_per_eu(2, 8))
     if (rb < r1) {
       block(rb, b0, b1, 0);
       if (kRB == 2) __syncthreads();  // an odd count: the next pass's first row block refills buffer 0
+    }
+    if constexpr (kStage) {
+      // the last row block's DMA (a repeat of its own operands) has landed in every wave before the next pass
+      // stages into either buffer
+      wait_vmcnt<0>();
+      __syncthreads();
     }
     // dB partials of this super-block: D[j][ρ], lane l: ρ = 16 h + l % 16, j = jb + 16 jh + (l / 16) * 4 + i
 #pragma unroll

@@ -248,13 +248,19 @@ __device__ __forceinline__ uint32_t quant16_codes(const uint32_t* w, uint4& c) {
   return e;
 }
 
+// The stores of quant16: codes c of row mc, scale byte e of row m (0 for padded rows)
+__device__ __forceinline__ void quant16_store(uint4 c, uint32_t e, int m, bool live, uint8_t* q, int64_t mc,
+                                              int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
+  store_codes<MX_NT_FUSED>(q + (tiled ? tiled_offset(mc, k0, Kq) : mc * Kq + k0), c);
+  // both lanes of the pair store the same byte (no divergent branch in the loop)
+  store_scale<MX_NT_FUSED>(s + blocked_offset(m, k0 >> 5, s_col_tiles), live ? (uint8_t)e : (uint8_t)0);
+}
+
 __device__ __forceinline__ void quant16(const uint32_t* w, int lane, int m, bool live, uint8_t* q, int64_t mc,
                                         int64_t Kq, bool tiled, int64_t k0, uint8_t* s, int64_t s_col_tiles) {
   uint4 c;
   const uint32_t e = quant16_codes(w, c);
-  store_codes<MX_NT_FUSED>(q + (tiled ? tiled_offset(mc, k0, Kq) : mc * Kq + k0), c);
-  // both lanes of the pair store the same byte (no divergent branch in the loop)
-  store_scale<MX_NT_FUSED>(s + blocked_offset(m, k0 >> 5, s_col_tiles), live ? (uint8_t)e : (uint8_t)0);
+  quant16_store(c, e, m, live, q, mc, Kq, tiled, k0, s, s_col_tiles);
 }
 
 typedef float v2f __attribute__((ext_vector_type(2)));
