@@ -215,7 +215,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RP > 32 ? 2
   constexpr int kAcc = RP > 32 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
-  const int r0 = blockIdx.x * 32, nt = K / 128;
+  // Row block of this workgroup: the 4 row blocks of one 128-row scale tile go to workgroups b, b + 8, b + 16,
+  // b + 24 of a group of 32, which run on one XCD (workgroup b runs on XCD b % 8), so each 512-byte scale tile
+  // is written from one L2; a trailing partial group keeps the identity order.  Numbered in order, the four
+  // writers sat on four XCDs: configuration 3, graph timing, two rounds on one box, rp 32 17.5-17.7 -> 15.8-15.9
+  // us and rp 16 16.0 -> 14.5 us, the same bytes.
+  int rbk = blockIdx.x;
+  {
+    const int b = blockIdx.x, g = b / 32;
+    if ((g + 1) * 32 <= Tpad / 32) rbk = 32 * g + 4 * (b % 8) + (b / 8) % 4;
+  }
+  const int r0 = rbk * 32, nt = K / 128;
   // DMA sources (element pointers at tile 0)
   const int pc = lane & 15;
   const uint16_t* xsrc[2];
