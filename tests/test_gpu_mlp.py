@@ -201,6 +201,31 @@ def test_bwd_kernel_elementwise_and_codes(cfg, T, gpu):
     assert _rel(dxa, b["dxa_raw"]) <= TOL and _rel(dbg, b["dBg_raw"]) <= TOL and _rel(dad, b["dAd"]) <= TOL
 
 
+@pytest.mark.parametrize("wide,sb,cg", [(True, 128, 512), (True, 384, 1792), (False, 256, 256), (False, 128, 896)])
+def test_bwd_kernel_grids_with_several_column_passes(wide, sb, cg, gpu, monkeypatch):
+    """The backward kernel with grids whose workgroups walk several column passes (CG > 128 · waves / 4) and
+    super-blocks of several sizes, T = 300 (rows past T in the last super-block): its staged small operands
+    restart at each pass.  The MX codes and scales of dg | du and the dxa partials' column partition do not depend
+    on the grid, so codes, scales and (8-wave, one partial per 256 columns either way) dxa are bit-identical to
+    the default grid's; the dB / dA_d sums group the rows by super-block, so they agree to fp32 rounding."""
+    inp, W, (S, bg, bu, ad, bd), f, b, g = _kernel_inputs(2, 300, gpu)
+    s = inp["s"]
+    args = (g(f["gu"]), g(f["xs"]), g(b["dhm"]), g(b["dxd"]), g(bg), g(bu), g(ad), s, s, True)
+    monkeypatch.setattr(fused_mlp, "WIDE_BWD", [wide])
+    ref = fused_mlp.mlp_bwd(*args, tiled=True)
+    assert fused_mlp.LAST["bwd"]["wide"] == wide
+    monkeypatch.setattr(fused_mlp, "_bwd_grid", lambda T, N, R, wide=False: (sb, cg))
+    out = fused_mlp.mlp_bwd(*args, tiled=True)
+    assert (fused_mlp.LAST["bwd"]["SB"], fused_mlp.LAST["bwd"]["CG"]) == (sb, cg)
+    T, N = 300, inp["N"]
+    assert np.array_equal(mx.from_tiled(out[0].view(torch.uint8).cpu().numpy().reshape(-1), T, 2 * N),
+                          mx.from_tiled(ref[0].view(torch.uint8).cpu().numpy().reshape(-1), T, 2 * N))
+    assert torch.equal(out[1], ref[1])
+    assert torch.equal(out[2], ref[2])
+    for a_, b_ in zip(out[3:], ref[3:]):
+        assert _rel(a_, b_.cpu().double()) <= 1e-6
+
+
 def test_need_out_false_saves_same_and_backward_matches(gpu):
     # checkpoint recompute: need_out=False leaves the saved set and therefore every gradient unchanged
     _, _, out1 = _run_model(2, 384, gpu, need_out=True)
