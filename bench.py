@@ -250,7 +250,9 @@ def _lora_epilogues(T, K, N, r, dev):
 def _grouped_linears(T, K, r, alpha, dev, steps=10):
     """Attention projections through fused_linear (q|k|v grouped with the concatenated Wᵀ, o_proj deferred into the
     residual add), forward + backward per step.  q 2048 and k, v 512 outputs for d_model 2048 (GQA shape).  FLOPs
-    counted: the MX GEMMs only (forward x·Wᵀ and backward dx, 2·T·K·N each)."""
+    counted: the MX GEMMs only (forward x·Wᵀ and backward dx, 2·T·K·N each).  Timed eagerly (steps enqueued by
+    Python and autograd, the figure a training loop without graphs sees) and as replays of the step captured into
+    a HIP graph."""
     import torch
 
     import fused_linear
@@ -295,8 +297,31 @@ def _grouped_linears(T, K, r, alpha, dev, steps=10):
     ms = e0.elapsed_time(e1) / steps
     assert fused_linear.STATS.get("lan ngược gộp", 0) - before == 2 * steps  # both groups took the fused backward
     fl = 2 * 2 * T * K * (nq + 2 * nkv) + 2 * 2 * T * nq * K
-    del m, x, resid, dy
+    # the same step captured into a HIP graph (warmed up on a side stream, as capture needs) and replayed: the
+    # kernels' own pace, without the Python and autograd work that the eager step enqueues them with
+    # (tests/test_gpu_graph.py checks replays bit for bit against eager steps)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    gms = e0.elapsed_time(e1) / steps
+    del graph, m, x, resid, dy
     return {"ms_per_step": round(ms, 4), "MX_GEMM_TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 1),
+            "graph_ms_per_step": round(gms, 4), "graph_MX_GEMM_TFLOP/s": round(fl / (gms * 1e-3) / 1e12, 1),
             "shape": f"T={T} d_model={K} q={nq} k=v={nkv} o={nq}->{K} r={r}",
             "note": "fwd+bwd of q|k|v (one group) and o_proj (deferred, residual_add) on q; seeded upstream grads"}
 

@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define MXFP8_MLP_ABI_VERSION 13
+#define MXFP8_MLP_ABI_VERSION 14
 #define MXFP8_OK 0
 #define MXFP8_ERR_ARG (-1)
 /* mxfp8_gemm_nt layout bits */
@@ -406,7 +406,7 @@ typedef struct {
   const void* x;     /* [T, K] bf16, row stride ld_x (>= K, a multiple of 8), 16-byte aligned */
   int64_t ld_x;
   const void* p;     /* [T, rp] bf16, 16-byte aligned */
-  int64_t rp;        /* 16 or 32 */
+  int64_t rp;        /* 16, 32 or 64 */
   float scale;
   int64_t transpose; /* out [rp, K] (0) or [K, rp] (1) */
   int64_t out_f32;   /* out holds fp32 values of the bf16 result (1) or bf16 (0) */
@@ -426,13 +426,14 @@ int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T
                         float* part, void* stream);
 
 /*
- * mxfp8_gemm_nt (4-wave shape, rank-32 LoRA epilogue, no workspace) and mxfp8_lora_tn_batch in one launch plus
- * the batch's sums: the token reductions run in workgroups numbered after every GEMM tile, so the dispatcher
- * starts them only once each tile has started, in the workgroup slots the GEMM's last round of tiles leaves
- * idle.  Results bit for bit those of the two calls one after the other (jobs, T_tn, K_tn, chunks and part as
- * in mxfp8_lora_tn_batch).  The jobs must not read c.  Replaces, in the MLP backward, the dx GEMM with its
- * dxa·S addmm_ and the token GEMMs dB_d, dA (/root/reference/scripts/fused_mlp.py:331, :316-318, :333), which
- * the reference runs as separate kernels.  r must be 32, layout without MXFP8_GEMM_WIDE, M > 0.
+ * mxfp8_gemm_nt (4-wave shape, rank-16, 32 or 48 LoRA epilogue, no workspace) and mxfp8_lora_tn_batch in one
+ * launch plus the batch's sums: the token reductions run in workgroups numbered after every GEMM tile, so the
+ * dispatcher starts them only once each tile has started, in the workgroup slots the GEMM's last round of tiles
+ * leaves idle.  Results bit for bit those of the two calls one after the other (jobs, T_tn, K_tn, chunks and part
+ * as in mxfp8_lora_tn_batch).  The jobs must not read c.  Replaces, in the MLP backward, the dx GEMM with its
+ * dxa·S addmm_ and the token GEMMs dB_d, dA (/root/reference/scripts/fused_mlp.py:331, :316-318, :333), and in
+ * the grouped linears' backward the dx GEMM with its dS·S addmm_ and dA = dSᵀ·x2 (fused_linear.py:269, :271), which
+ * the reference runs as separate kernels.  r in {16, 32, 48}, layout without MXFP8_GEMM_WIDE, M > 0.
  */
 int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, const void* b, const void* sb, int64_t ldb,
                      int64_t M, int64_t N, int64_t K, void* c, int64_t ldc, const void* lora_p, int64_t ld_p,

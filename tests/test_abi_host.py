@@ -78,14 +78,15 @@ def test_argument_checks_reject_before_launch(lib):
     # allocation-free token reduction: rp * K * 4 bytes beyond its 16 MiB static scratch (checked first, no GPU call)
     assert lib.mxfp8_lora_tn_noalloc(p, 64, 65536 + 128, 65536 + 128, p, 64, 1.0, 0, 0, p, None) == -1
     assert b"static scratch" in lib.mxfp8_last_error()
-    # GEMM with folded token reductions: only the rank-32 epilogue of the 4-wave shape, and the batch's own checks
+    # GEMM with folded token reductions: only the rank-16, 32 or 48 epilogue of the 4-wave shape, and the batch's own
+    # checks (ranks 16, 32 and 64)
     job = _native.LoraTnJob(16, 2048, 16, 32, 1.0, 0, 0, 16)
     jobs = (_native.LoraTnJob * 1)(job)
     gemm = lambda r, layout, jb: lib.mxfp8_gemm_nt_tn(p, p, 2048, p, p, 2048, 256, 2048, 2048, p, 2048, p, 32, p, 32,  # noqa: E731
                                                       r, 1.0, layout, jb, 1, 256, 2048, 8, p, None)
-    assert gemm(16, 0, jobs) == -1 and b"rank-32" in lib.mxfp8_last_error()
+    assert gemm(64, 0, jobs) == -1 and b"rank-16, 32 or 48" in lib.mxfp8_last_error()
     assert gemm(32, _native.GEMM_WIDE, jobs) == -1 and b"4-wave" in lib.mxfp8_last_error()
-    bad = (_native.LoraTnJob * 1)(_native.LoraTnJob(16, 2048, 16, 64, 1.0, 0, 0, 16))
+    bad = (_native.LoraTnJob * 1)(_native.LoraTnJob(16, 2048, 16, 48, 1.0, 0, 0, 16))
     assert gemm(32, 0, bad) == -1 and b"mxfp8_gemm_nt_tn: job 0" in lib.mxfp8_last_error()
     # GEMM with its epilogue operand summed in the launch: rank 16 and the 4-wave shape only, aligned buffers
     gsum = lambda r, layout, part: lib.mxfp8_gemm_nt_sum(p, p, 2048, p, p, 2048, 256, 2048, 2048, p, 2048, part, 96,  # noqa: E731

@@ -55,6 +55,51 @@ def test_gemm_nt_tn_matches_separate_calls(M, N, K, Kt, gpu):
     assert torch.equal(o1.view(torch.int32), r1.view(torch.int32))
 
 
+@pytest.mark.parametrize("r,M,N,K,Kt,rps,layout", [
+    (48, 10752, 2048, 3072, 2048, (64,), 2),  # the grouped q|k|v dx GEMM at configuration 3 and its dA
+    (16, 10752, 2048, 2048, 2048, (16,), 2),  # the o_proj dx GEMM and its dA
+    (48, 300, 256, 512, 1024, (64, 16), 3),
+    (16, 1, 128, 256, 128, (64, 32, 16), 3),
+    (32, 2000, 1024, 2048, 768, (64, 32), 2)])
+def test_gemm_nt_tn_other_ranks_match_separate_calls(r, M, N, K, Kt, rps, layout, gpu):
+    """The epilogue ranks 16 and 48 and the rank-64 reduction (the grouped linears' backward): the GEMM with its
+    epilogue operands as column views of wider buffers whose columns past r hold NaN (the padded dS and Sᵀ), and
+    the reductions, against mx_mm then lora_tn_batch."""
+    g = torch.Generator().manual_seed(M + N + K + r)
+    a = (torch.randn(M, K, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    b = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    qa, sa = mxfp8.mx_quant_tiled(a) if layout & 1 else mxfp8.mx_quant(a)
+    qb, sb = mxfp8.mx_quant_tiled(b)
+    P = (torch.randn(M, 64, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    Q = (torch.randn(N, 64, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    P[:, r:] = float("nan")
+    Q[:, r:] = float("nan")
+    lora = (P[:, :r], Q[:, :r])
+    xs = [torch.randn(M, Kt, generator=g).to(torch.bfloat16).to(gpu) for _ in rps]
+    ps = [(torch.randn(M, rp, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for rp in rps]
+    part = torch.empty(_native.lora_tn_chunks(M, Kt) * sum(rps) * Kt, device=gpu)
+
+    def outs(fill):
+        return [torch.full(((Kt, rp) if j % 2 else (rp, Kt)), fill, dtype=torch.bfloat16 if j % 2 else torch.float32,
+                           device=gpu) for j, rp in enumerate(rps)]
+
+    def jobs(o):
+        return [(x, p, oo, 2.0 if j % 2 else 1.0, bool(j % 2)) for j, (x, p, oo) in enumerate(zip(xs, ps, o))]
+
+    ref_c = mxfp8.mx_mm(qa, sa, qb, sb, lora=lora, alpha=1.0, layout=layout, m=M)
+    ref = outs(0.0)
+    _native.lora_tn_batch(jobs(ref), part)
+    torch.cuda.synchronize()
+    got = outs(float("nan"))
+    part.fill_(float("nan"))
+    c = mxfp8.mx_mm_tn(qa, sa, qb, sb, lora, 1.0, layout, M, jobs(got), part)
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), ref_c.view(torch.int16))
+    assert not torch.isnan(c).any()
+    for j, (o, w) in enumerate(zip(got, ref)):
+        assert torch.equal(o.view(torch.int16), w.view(torch.int16)), j
+
+
 def _grads(m):
     return [m.gate_proj.lora_A["default"].weight.grad, m.gate_proj.lora_B["default"].weight.grad,
             m.up_proj.lora_A["default"].weight.grad, m.up_proj.lora_B["default"].weight.grad,

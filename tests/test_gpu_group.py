@@ -445,3 +445,39 @@ def test_backward_after_next_step_keeps_its_own_weights(gpu):
     for k, (a, b) in enumerate(zip(got, want)):
         assert a is not None and torch.equal(a, b), k
     del outs2, xx2
+
+
+@pytest.mark.parametrize("names", [("q_proj", "k_proj", "v_proj"), ("o_proj",)])
+def test_group_backward_with_and_without_the_dx_fold(names, gpu, monkeypatch):
+    """The grouped backward's dA = dSᵀ·x2 in its dx GEMM's launch (fused_linear.FOLD_TN: mxfp8_gemm_nt_tn with the
+    rank-48 epilogue and a rank-64 reduction at q|k|v, rank 16 and 16 at o_proj) against its own launch after the
+    GEMM: bit-identical dx and LoRA gradients, and the folded entry point called once per backward."""
+    import mxfp8
+    m, _ = _build(gpu, seed=5)
+    mods = [getattr(m.attn, n) for n in names]
+    g = torch.Generator().manual_seed(17)
+    x = (torch.randn(T, mods[0].base_layer.in_features, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    dys = [(torch.randn(T, mod.base_layer.out_features, generator=g) * 1e-2).to(torch.bfloat16).to(gpu)
+           for mod in mods]
+    calls = []
+    real = mxfp8.mx_mm_tn
+    monkeypatch.setattr(mxfp8, "mx_mm_tn", lambda *a, **k: calls.append(1) or real(*a, **k))
+
+    def run(fold):
+        monkeypatch.setattr(fused_linear, "FOLD_TN", [fold])
+        fused_linear.new_step()
+        for p in m.parameters():
+            p.grad = None
+        xg = x.clone().requires_grad_(True)
+        outs = fused_linear.group_linear(xg, mods)
+        torch.autograd.backward(list(outs), dys)
+        torch.cuda.synchronize()
+        return [xg.grad] + [p.grad.clone() for mod in mods
+                            for p in (mod.lora_A["default"].weight, mod.lora_B["default"].weight)]
+
+    off = run(False)
+    assert not calls
+    on = run(True)
+    assert len(calls) == 1
+    for k, (a, b) in enumerate(zip(on, off)):
+        assert a is not None and torch.equal(a, b), k

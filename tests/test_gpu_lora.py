@@ -365,3 +365,26 @@ def test_lora_tn_batch_matches_single_calls(T, K, gpu):
                               torch.empty(chunks * 48 * K, device=gpu))
         torch.cuda.synchronize()
         assert torch.equal(a0, b0) and torch.equal(a1, b1), (dt0, dt1)
+
+
+@pytest.mark.parametrize("T,K", [(10752, 2048), (300, 1024), (1, 128)])
+def test_lora_tn_batch_rank_64_matches_single_calls(T, K, gpu):
+    """mxfp8_lora_tn_batch with a rank-64 job (the grouped linears' dA at q|k|v, whose dS is padded to 64 columns)
+    beside ranks 16 and 32, against mxfp8_lora_tn per job with the same chunking: bit-identical outputs."""
+    g = torch.Generator().manual_seed(T + K + 64)
+    rps = (64, 16, 32)
+    xs = [torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu) for _ in rps]
+    ps = [(torch.randn(T, rp, generator=g) * 0.1).to(torch.bfloat16).to(gpu) for rp in rps]
+    chunks = _native.lora_tn_chunks(T, K)
+    want, got = [], []
+    for j, (x, p, rp) in enumerate(zip(xs, ps, rps)):
+        shape = (K, rp) if j == 1 else (rp, K)
+        want.append(torch.empty(shape, dtype=torch.float32, device=gpu))
+        got.append(torch.full(shape, float("nan"), dtype=torch.float32, device=gpu))
+        _native.lora_tn(x, p, want[j], torch.empty(chunks * rp * K, device=gpu), scale=2.0 if j == 1 else 1.0,
+                        transpose=j == 1)
+    _native.lora_tn_batch([(x, p, o, 2.0 if j == 1 else 1.0, j == 1) for j, (x, p, o) in enumerate(zip(xs, ps, got))],
+                          torch.full((chunks * sum(rps) * K,), float("nan"), device=gpu))
+    torch.cuda.synchronize()
+    for j, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), j

@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmxfp8_mlp.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 GEMM_A_TILED, GEMM_B_TILED, GEMM_WIDE, GEMM_C_FT, GEMM_B_PI = 1, 2, 4, 8, 16  # mxfp8_gemm_nt layout bits
 
 _i64, _ptr, _f32, _int = ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_int
@@ -387,8 +387,9 @@ def _tn_table(jobs, part, chunks):
 
 
 def gemm_nt_tn(a, sa, lda, b, sb, ldb, M, N, K, c, lora, jobs, part, alpha=1.0, layout=0, chunks=None):
-    """gemm_nt (rank-32 lora = (P, Q), 4-wave shape) and lora_tn_batch(jobs, part, chunks) in one launch, plus the
-    batch's sums (include/mxfp8_mlp.h, mxfp8_gemm_nt_tn): the token reductions fill the GEMM's idle tail slots."""
+    """gemm_nt (rank-16, 32 or 48 lora = (P, Q), 4-wave shape) and lora_tn_batch(jobs, part, chunks) in one launch,
+    plus the batch's sums (include/mxfp8_mlp.h, mxfp8_gemm_nt_tn): the token reductions fill the GEMM's idle tail
+    slots."""
     p, q = lora
     arr, n, T, Kt, chunks = _tn_table(jobs, part, chunks)
     _gpu(c, "mxfp8_gemm_nt_tn")

@@ -708,11 +708,12 @@ __global__ __launch_bounds__(256) void tn_kernel(const uint16_t* __restrict__ X,
   tn_body<RP, kD>(X, ldx, P, T, K, chunk, part, blockIdx.x, blockIdx.y, lds);
 }
 
-// The token reductions of mxfp8_lora_tn_batch in one flat grid (TnBatch, tn_device.h).
-template <int kD>
+// The token reductions of mxfp8_lora_tn_batch in one flat grid (TnBatch, tn_device.h); kWide when a job has
+// rank 64, so that batches of ranks 16 and 32 keep the smaller LDS footprint.
+template <int kD, bool kWide>
 __global__ __launch_bounds__(256) void tn_batch_kernel(const TnBatch a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[kTnBatchLdsElems];
-  tn_batch_block<kD>(a, blockIdx.x, lds);
+  __shared__ __attribute__((aligned(16))) uint16_t lds[tn_batch_lds_elems<kWide>()];
+  tn_batch_block<kD, kWide>(a, blockIdx.x, lds);
 }
 
 // out = bf16(Σ_c part[c, ρ, k]) (then bf16(· scale) when scale != 1), written as [RP, K] or transposed
@@ -985,13 +986,14 @@ int tn_batch_tables(const char* who, const mxfp8_lora_tn_job* jobs, int64_t n_jo
   nb = ns = 0;
   for (int64_t j = 0; j < n_jobs; ++j) {
     const mxfp8_lora_tn_job& jb = jobs[j];
-    MX_CHECK_ARG(jb.x && jb.p && jb.out && (jb.rp == 16 || jb.rp == 32) && jb.ld_x >= K && jb.ld_x % 8 == 0 &&
-                     mx_aligned(jb.x, 16) && mx_aligned(jb.p, 16),
-                 "%s: job %lld: null pointer, rp not in {16, 32} or bad x stride / alignment", who, (long long)j);
+    MX_CHECK_ARG(jb.x && jb.p && jb.out && (jb.rp == 16 || jb.rp == 32 || jb.rp == 64) && jb.ld_x >= K &&
+                     jb.ld_x % 8 == 0 && mx_aligned(jb.x, 16) && mx_aligned(jb.p, 16),
+                 "%s: job %lld: null pointer, rp not in {16, 32, 64} or bad x stride / alignment", who, (long long)j);
     a.x[j] = (const uint16_t*)jb.x;
     a.ldx[j] = jb.ld_x;
     a.p[j] = (const uint16_t*)jb.p;
     a.rp[j] = (int)jb.rp;
+    a.wide |= jb.rp == 64;
     a.part[j] = part + off;
     a.first[j] = (int)nb;
     sa.part[j] = part + off;
@@ -1036,8 +1038,10 @@ extern "C" int mxfp8_lora_tn_batch(const mxfp8_lora_tn_job* jobs, int64_t n_jobs
   const int rc = tn_batch_tables("mxfp8_lora_tn_batch", jobs, n_jobs, T, K, chunks, part, a, sa, nb, ns);
   if (rc != MXFP8_OK) return rc;
   hipStream_t stm = (hipStream_t)stream;
-  if (a.kd == 2) tn_batch_kernel<2><<<(unsigned)nb, 256, 0, stm>>>(a);
-  else tn_batch_kernel<1><<<(unsigned)nb, 256, 0, stm>>>(a);
+  if (a.kd == 2 && a.wide) tn_batch_kernel<2, true><<<(unsigned)nb, 256, 0, stm>>>(a);
+  else if (a.kd == 2) tn_batch_kernel<2, false><<<(unsigned)nb, 256, 0, stm>>>(a);
+  else if (a.wide) tn_batch_kernel<1, true><<<(unsigned)nb, 256, 0, stm>>>(a);
+  else tn_batch_kernel<1, false><<<(unsigned)nb, 256, 0, stm>>>(a);
   MX_CHECK_LAUNCH("mxfp8_lora_tn_batch");
   return tn_sum_batch_launch(sa, ns, stm, "mxfp8_lora_tn_batch");
 }

@@ -187,16 +187,18 @@ __device__ __forceinline__ void tile_coords(int t, int tm, int tn, int& mt, int&
   nt = r / rows;
 }
 
-// The instance that can run token reductions past its tiles (mxfp8_gemm_nt_tn): the plain 4-wave GEMM with the
-// rank-32 LoRA epilogue, the fused MLP's dx GEMM at r = 16 (its tiles fill the slots 1.3 times at configuration
-// 3).  Other instances do not compile the reduction.
+// The instances that can run token reductions past their tiles (mxfp8_gemm_nt_tn): the plain 4-wave GEMM with
+// the rank-16, 32 or 48 LoRA epilogue, the dx GEMMs of the fused MLP (r = 32 at r = 16 adapters) and of the
+// grouped linears (q|k|v: 48, o_proj: 16).  At configuration 3 each has 672 tiles, 1.3 rounds of the workgroup
+// slots.  Other instances do not compile the reduction.
 template <int kR, int kNW, int kEpi>
-constexpr bool kFoldTn = kR == 32 && kNW == 1 && kEpi == 0;
+constexpr bool kFoldTn = (kR == 16 || kR == 32 || kR == 48) && kNW == 1 && kEpi == 0;
 // The instance whose epilogue operand P can be summed in its own launch (mxfp8_gemm_nt_sum): the plain 4-wave GEMM
 // with the rank-16 epilogue, the fused MLP's down GEMM at r = 16.
 template <int kR, int kNW, int kEpi>
 constexpr bool kFoldSum = kR == 16 && kNW == 1 && kEpi == 0;
-static_assert(kTnBatchLdsElems * 2 <= 3 * 26 * 1024, "the folded token reduction borrows the 4-wave ring's LDS");
+static_assert(tn_batch_lds_elems<true>() * 2 <= 3 * 26 * 1024,
+              "the folded token reduction borrows the 4-wave ring's LDS");
 
 // 32 bytes of one operand row for the stage's 64-wide K step: chunk c0 (k 16*(l/32)..) and c0 + 2 (k 32 + ..)
 __device__ __forceinline__ v8i frag(const uint8_t* base, int row, int c0, int sw) {
@@ -237,8 +239,8 @@ __global__ __launch_bounds__(Shape<kNW>::kThreads) __attribute__((amdgpu_waves_p
     const int first = 8 * (plan.per_full + plan.per_split);
     if (bid >= first) {
       uint16_t* tl = reinterpret_cast<uint16_t*>(lds);
-      if (tnb.kd == 2) tn_batch_block<2>(tnb, bid - first, tl);
-      else tn_batch_block<1>(tnb, bid - first, tl);
+      if (tnb.kd == 2) tn_batch_block<2, true>(tnb, bid - first, tl);
+      else tn_batch_block<1, true>(tnb, bid - first, tl);
       return;
     }
   }
@@ -1026,8 +1028,9 @@ extern "C" int mxfp8_gemm_nt_tn(const void* a, const void* sa, int64_t lda, cons
                                 int64_t ld_p, const void* lora_q, int64_t ld_q, int64_t r, float alpha, int64_t layout,
                                 const mxfp8_lora_tn_job* jobs, int64_t n_jobs, int64_t T_tn, int64_t K_tn,
                                 int64_t chunks, float* part, void* stream) {
-  MX_CHECK_ARG(M > 0 && lora_p && r == 32 && !(layout & MXFP8_GEMM_WIDE),
-               "mxfp8_gemm_nt_tn: needs M > 0, the rank-32 LoRA epilogue and the 4-wave shape (r=%lld layout=%lld)",
+  MX_CHECK_ARG(M > 0 && lora_p && (r == 16 || r == 32 || r == 48) && !(layout & MXFP8_GEMM_WIDE),
+               "mxfp8_gemm_nt_tn: needs M > 0, a rank-16, 32 or 48 LoRA epilogue and the 4-wave shape (r=%lld "
+               "layout=%lld)",
                (long long)r, (long long)layout);
   TnBatch tnb;
   TnSumBatch sa_tn;

@@ -115,7 +115,7 @@ __device__ __forceinline__ void tn_body(const uint16_t* __restrict__ X, int64_t 
       }
 }
 
-// The token reductions of mxfp8_lora_tn_batch (rank 16 or 32 each) as one flat grid: job j owns blocks
+// The token reductions of mxfp8_lora_tn_batch (rank 16, 32 or 64 each) as one flat grid: job j owns blocks
 // first[j] .. first[j + 1] - 1, `cols` = K / 128 column blocks per token chunk; every job shares T, K and the
 // chunking.  kd: the ring depth (1 or 2) of tn_body.
 struct TnBatch {
@@ -126,19 +126,26 @@ struct TnBatch {
   int rp[MXFP8_LORA_TN_MAX_JOBS];
   int first[MXFP8_LORA_TN_MAX_JOBS + 1];
   int n, T, K, chunk, cols, kd;
+  int wide;  // some job has rank 64
 };
 
-// LDS the batch body needs (ranks 16 and 32)
-constexpr int kTnBatchLdsElems = tn_lds_elems<32>();
+// LDS the batch body needs: ranks 16 and 32 (kWide false), or also 64 (kWide true)
+template <bool kWide>
+constexpr int tn_batch_lds_elems() {
+  return tn_lds_elems<kWide ? 64 : 32>();
+}
 
-// Block b of the batch's flat grid.
-template <int kD>
+// Block b of the batch's flat grid.  Rank 64 is compiled only with kWide (its LDS is half again as large).
+template <int kD, bool kWide>
 __device__ __forceinline__ void tn_batch_block(const TnBatch& a, int b, uint16_t* __restrict__ lds) {
   int j = 0;
   while (j + 1 < a.n && a.first[j + 1] <= b) ++j;
   const int l = b - a.first[j], bx = l % a.cols, by = l / a.cols;
   if (a.rp[j] == 16) tn_body<16, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by, lds);
-  else tn_body<32, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by, lds);
+  else if (!kWide || a.rp[j] == 32)
+    tn_body<32, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by, lds);
+  else
+    tn_body<64, kD>(a.x[j], a.ldx[j], a.p[j], a.T, a.K, a.chunk, a.part[j], bx, by, lds);
 }
 
 // The sums of the batch's jobs in one flat grid (job j: blocks first[j] .. first[j + 1] - 1).

@@ -26,6 +26,9 @@ from torch import nn
 _THIN = 64  # a plain frozen Linear with at most this many outputs joins the thin product (in_proj_b/a: 16)
 # the per-step bf16 weight forms of a group from one mxfp8_pack_bf16 launch (False: one torch operation each)
 PACK_FORMS = [os.environ.get("MXFP8_PACK_FORMS", "1") != "0"]
+# the grouped backward's dA = dSᵀ·x2 in the workgroup slots its dx GEMM's last round of tiles leaves idle, one
+# launch (mxfp8_gemm_nt_tn; False: its own launch after the GEMM)
+FOLD_TN = [os.environ.get("MXFP8_GROUP_FOLD_TN", "1") != "0"]
 STATS = {"gộp": 0, "gọi thẳng": 0}  # path counters, the reference's keys (grouped / called directly)
 
 
@@ -556,7 +559,18 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
             dB.mul_(sl.scale)
             dS[:, sl.cols].mul_(sl.scale)
         grads[2 * sl.index + 1] = dB
-    dx = None
+    dx = dA = None
+    a32 = bool(spec.adapters) and all(spec.parts[sl.layer][1].dtype == torch.float32 for sl in spec.adapters)
+
+    def tn_job():
+        # bf16(dSᵀ·x2), held in fp32 when every A is an fp32 parameter: autograd would cast each bf16 slice to its
+        # parameter's dtype anyway (exactly), one kernel per adapter.  (job, its partial-sum scratch)
+        import _native
+        out = torch.empty((width, K), dtype=torch.float32 if a32 else dt, device=dev)
+        n_part = _native.lora_tn_chunks(T, K) * width * K
+        part = _native.scratch_f32(n_part, dev)[:n_part]  # partial sums, read by the launch's sum kernel
+        return (x2, dS, out, 1.0, False), part
+
     if need_x:
         wq, ws, lay = wt
         for sl in spec.thin:
@@ -575,7 +589,15 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
                     pad = torch.cat([S, S.new_zeros(width - S.shape[0], S.shape[1])]) if width > S.shape[0] else S
                     ent = _CAST[skey + ("padT", width)] = (S, pad.t().contiguous())
                 St = ent[1]
-            dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=(dS[:, :r_dx], St[:, :r_dx]), alpha=1.0)
+            lora = (dS[:, :r_dx], St[:, :r_dx])
+            import _native
+            if spec.adapters and FOLD_TN[0] and r_dx in (16, 32, 48) and not lay & _native.GEMM_WIDE:
+                # the dA reduction in the dx GEMM's launch: the same bits as the two calls below
+                job, part = tn_job()
+                dA = job[2]
+                dx = mxfp8.mx_mm_tn(*codes, wq, ws, lora, 1.0, lay, T, [job], part)
+            else:
+                dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay, lora=lora, alpha=1.0)
         else:
             dx = mxfp8.mx_mm(*codes, wq, ws, layout=lay)
             for i in spec.plain:  # plain bf16 linears (neither MX nor thin)
@@ -584,16 +606,12 @@ def _fused_backward(spec, skey, x2, xS, S, Bs, flat, plan, need_x, dt):
                 dx.addmm_(dS, S)
         del codes, q, sbuf
     if spec.adapters:
-        if native:
+        if native and dA is None:
             import _native
-            # bf16(dSᵀ·x2), held in fp32 when every A is an fp32 parameter: autograd would cast each bf16 slice
-            # to its parameter's dtype anyway (exactly), one kernel per adapter
-            a32 = all(spec.parts[sl.layer][1].dtype == torch.float32 for sl in spec.adapters)
-            dA = torch.empty((width, K), dtype=torch.float32 if a32 else dt, device=dev)
-            n_part = _native.lora_tn_chunks(T, K) * width * K
-            part = _native.scratch_f32(n_part, dev)[:n_part]  # partial sums, read by the launch's sum kernel
+            job, part = tn_job()
+            dA = job[2]
             _native.lora_tn(x2, dS, dA, part)
-        else:
+        elif not native:
             dA = dS[:, :spec.adapter_cols].t() @ x2
         for sl in spec.adapters:
             grads[2 * sl.index] = dA[sl.cols]

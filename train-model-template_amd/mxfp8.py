@@ -307,10 +307,11 @@ def mx_mm_sum(q, s, wq, ws, part, p_out, lq, alpha, layout, m, wait_limit=-1):
 
 
 def mx_mm_tn(q, s, wq, ws, lora, alpha, layout, m, tn_jobs, part):
-    """mx_mm with the rank-32 LoRA epilogue, and the token reductions _native.lora_tn_batch(tn_jobs, part) run in
-    the same launch (in the workgroup slots the GEMM's last round of tiles leaves idle), plus their sums: the
-    MLP backward's dx GEMM and its dB_d / dA reductions (/root/reference/scripts/fused_mlp.py:331, :316-318,
-    :333).  Same results as mx_mm then lora_tn_batch."""
+    """mx_mm with the rank-16, 32 or 48 LoRA epilogue, and the token reductions _native.lora_tn_batch(tn_jobs,
+    part) run in the same launch (in the workgroup slots the GEMM's last round of tiles leaves idle), plus their
+    sums: the MLP backward's dx GEMM and its dB_d / dA reductions (/root/reference/scripts/fused_mlp.py:331,
+    :316-318, :333), and the grouped linears' dx GEMM and dA (/root/reference/scripts/fused_linear.py:269, :271).
+    Same results as mx_mm then lora_tn_batch."""
     M, K = q.shape
     M = m
     N = wq.shape[0]
