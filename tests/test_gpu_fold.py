@@ -1,7 +1,9 @@
-"""GPU checks of mxfp8_gemm_nt_tn: the rank-32 LoRA-epilogue MX GEMM whose launch also runs the token reductions
-of mxfp8_lora_tn_batch in workgroups past its tiles (the MLP backward's dx GEMM with its dB_d / dA reductions,
-/root/reference/scripts/fused_mlp.py:331, :316-318, :333).  The folded launch computes what the two separate
-calls compute, with the same kernels' arithmetic in the same order, so the bar is bit-identical outputs:
+"""GPU checks of mxfp8_gemm_nt_tn: the LoRA-epilogue MX GEMM whose launch also runs the token reductions of
+mxfp8_lora_tn_batch in workgroups past its tiles (the MLP backward's dx GEMM with its dB_d / dA reductions,
+/root/reference/scripts/fused_mlp.py:331, :316-318, :333, at epilogue rank 32; the grouped linears' dx GEMMs with
+dA, fused_linear.py:269, :271, at ranks 16 and 48 with a rank-64 reduction).  The folded launch computes what the
+two separate calls compute, with the same kernels' arithmetic in the same order, so the bar is bit-identical
+outputs:
   - the GEMM output and both reductions against mxfp8_gemm_nt followed by mxfp8_lora_tn_batch, at the MLP's
     configuration-3 dx shape (672 tiles: the reductions run in the last round's idle slots), at a small shape
     whose few tiles leave most slots free from the start, with T not a multiple of 32 or 128, and at T = 1;
