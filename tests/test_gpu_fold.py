@@ -62,7 +62,8 @@ def test_gemm_nt_tn_matches_separate_calls(M, N, K, Kt, gpu):
     (16, 10752, 2048, 2048, 2048, (16,), 2),  # the o_proj dx GEMM and its dA
     (48, 300, 256, 512, 1024, (64, 16), 3),
     (16, 1, 128, 256, 128, (64, 32, 16), 3),
-    (32, 2000, 1024, 2048, 768, (64, 32), 2)])
+    (32, 2000, 1024, 2048, 768, (64, 32), 2),
+    (48, 50000, 256, 256, 2048, (64, 16), 3)])  # x of 205 MB: the reductions' one-step register ring
 def test_gemm_nt_tn_other_ranks_match_separate_calls(r, M, N, K, Kt, rps, layout, gpu):
     """The epilogue ranks 16 and 48 and the rank-64 reduction (the grouped linears' backward): the GEMM with its
     epilogue operands as column views of wider buffers whose columns past r hold NaN (the padded dS and Sᵀ), and

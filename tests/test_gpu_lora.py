@@ -367,10 +367,11 @@ def test_lora_tn_batch_matches_single_calls(T, K, gpu):
         assert torch.equal(a0, b0) and torch.equal(a1, b1), (dt0, dt1)
 
 
-@pytest.mark.parametrize("T,K", [(10752, 2048), (300, 1024), (1, 128)])
+@pytest.mark.parametrize("T,K", [(10752, 2048), (300, 1024), (1, 128), (50000, 2048)])
 def test_lora_tn_batch_rank_64_matches_single_calls(T, K, gpu):
     """mxfp8_lora_tn_batch with a rank-64 job (the grouped linears' dA at q|k|v, whose dS is padded to 64 columns)
-    beside ranks 16 and 32, against mxfp8_lora_tn per job with the same chunking: bit-identical outputs."""
+    beside ranks 16 and 32, against mxfp8_lora_tn per job with the same chunking: bit-identical outputs.  At
+    T = 50000 each x holds 205 MB, past the size that takes the two-step register ring."""
     g = torch.Generator().manual_seed(T + K + 64)
     rps = (64, 16, 32)
     xs = [torch.randn(T, K, generator=g).to(torch.bfloat16).to(gpu) for _ in rps]
