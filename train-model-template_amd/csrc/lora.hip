@@ -214,6 +214,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RP > 32 ? 2
   constexpr int kDma = 2 + kWDma;     // X DMAs: 8 KB per stage, two per wave
   constexpr int kAcc = RP > 32 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kStages * kStageB];
+  // The scale bytes of a step, [2 steps][32 rows][4 waves]: the 4 waves' bytes of a row are one word of the 128 x 4
+  // scale tile, stored on the next step (see the loop).
+  __shared__ uint32_t sbuf[2][32];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lg = lane >> 5;
   // Row block of this workgroup: the 4 row blocks of one 128-row scale tile go to workgroups b, b + 8, b + 16,
   // b + 24 of a group of 32, which run on one XCD (workgroup b runs on XCD b % 8), so each 512-byte scale tile
@@ -257,40 +260,65 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RP > 32 ? 2
   v16f acc[kAcc];
 #pragma unroll
   for (int h = 0; h < kAcc; ++h) acc[h] = v16f{};
+  // Scale words: at step t each wave puts its 32 rows' scale bytes (block 4t + w) into sbuf[t & 1]; the next step
+  // reads them beside its tile (after its barrier) and, at its end, wave w stores the words of rows 8w..8w+7 (lanes 0..7; the other lanes repeat them), one
+  // 128-byte line of the scale tile, instead of every lane storing its byte (four waves x 32 bytes in 16-byte steps
+  // over four lines).  The last step's words leave after the loop.
+  uint8_t* const srow = s + (((int64_t)(r0 >> 7) * (K / 128)) << 9) + ((r0 & 127) >> 5) * 4;  // + tile t * 512
+  const int frow = 8 * w + (lane & 7);  // the row whose word this lane stores
+  auto flush = [&](int t, uint32_t word) {  // the words of step t (read from sbuf[t & 1])
+    store_codes<MX_NT_FUSED>(srow + ((int64_t)t << 9) + frow * 16, word);
+  };
   // Stages past the end re-load the last tile into the slot just consumed (no later step reads it).  The memory
-  // counter also counts this lane's stores (one code store and one scale store per tile), in issue order.  Behind
-  // tile t's DMAs come the (kStages - 2) later tiles' DMAs and, from step kStages - 1 on, the stores of the last
-  // kStages - 1 steps; the wait leaves exactly those in flight.  (Counting the DMAs alone made every step wait
-  // for the previous steps' stores to be acknowledged.)  The first kStages - 1 steps, with fewer stores behind
-  // their tile, wait for the DMAs alone, which covers them.
+  // counter also counts this lane's stores (two per step: the codes of tile t and the scale words of tile t - 1,
+  // none at step 0), in issue order.  Behind tile t's DMAs come the (kStages - 2) later tiles' DMAs and, from step
+  // kStages on, the stores of the last kStages - 1 steps; the wait leaves exactly those in flight.  (Counting the
+  // DMAs alone made every step wait for the previous steps' stores to be acknowledged.)  The first kStages steps,
+  // with fewer stores behind their tile, wait for the DMAs alone, which covers them.  The wait also drains this
+  // wave's LDS operations, so the scale bytes written at step t - 1 are in LDS before the barrier.
   constexpr int kSt = 2;
 #pragma unroll
   for (int j = 0; j < kStages - 1; ++j) issue(min(j, nt - 1), j);
   int slot = 0;
   for (int t = 0; t < nt; ++t) {
-    if (t < kStages - 1) wait_vmcnt<(kStages - 2) * kDma>();
+    if (t < kStages) wait_vmcnt<(kStages - 2) * kDma>();
     else wait_vmcnt<(kStages - 2) * kDma + (kStages - 1) * kSt>();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();  // every wave's DMA of tile t landed; every wave is done with tile t - 1's slot
     issue(min(t + kStages - 1, nt - 1), slot == 0 ? kStages - 1 : slot - 1);
     const uint8_t* st = lds + slot * kStageB;
     const uint4 a = *reinterpret_cast<const uint4*>(st + row * 256 + sx0);
     const uint4 b = *reinterpret_cast<const uint4*>(st + row * 256 + sx1);
-    const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    quant16(v, lane, m, live, q, mc, K, true, (int64_t)t * 128 + 32 * w + 16 * lg, s, K / 128);
-    // D[ρ][t] += W[ρ, cols] · X[t, cols] over the lane pair's 32 columns (rows ρ >= RP of the W tile: zero); W row
-    // 32h + row has the swizzle of row (same row % 16)
+    // W row 32h + row has the swizzle of row (same row % 16).  Its fragments are read here, beside X's, so their
+    // LDS latency runs under the quantization below (read after it, each MFMA waited for its own read).
+    uint4 wa[kAcc], wb[kAcc];
 #pragma unroll
     for (int h = 0; h < kAcc; ++h) {
-      const uint4 wa = *reinterpret_cast<const uint4*>(st + kTileB + (32 * h + row) * 256 + sx0);
-      const uint4 wb = *reinterpret_cast<const uint4*>(st + kTileB + (32 * h + row) * 256 + sx1);
-      const bool wl = 32 * h + row < RP;
-      acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl ? as_bf8(wa) : v8bf{}, as_bf8(a), acc[h], 0, 0, 0);
-      acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl ? as_bf8(wb) : v8bf{}, as_bf8(b), acc[h], 0, 0, 0);
+      wa[h] = *reinterpret_cast<const uint4*>(st + kTileB + (32 * h + row) * 256 + sx0);
+      wb[h] = *reinterpret_cast<const uint4*>(st + kTileB + (32 * h + row) * 256 + sx1);
     }
+    const uint32_t sword = sbuf[(t + 1) & 1][frow];  // step t - 1's word (read at t = 0 too, unused there)
+    const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    {
+      uint4 c;
+      const uint32_t e = quant16_codes(v, c);
+      store_codes<MX_NT_FUSED>(q + tiled_offset(mc, (int64_t)t * 128 + 32 * w + 16 * lg, K), c);
+      // both lanes of the pair write the same byte (scale 0 in the padded rows of the last scale tile)
+      reinterpret_cast<uint8_t*>(sbuf[t & 1])[row * 4 + w] = live ? (uint8_t)e : (uint8_t)0;
+    }
+    // D[ρ][t] += W[ρ, cols] · X[t, cols] over the lane pair's 32 columns (rows ρ >= RP of the W tile: zero)
+#pragma unroll
+    for (int h = 0; h < kAcc; ++h) {
+      const bool wl = 32 * h + row < RP;
+      acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl ? as_bf8(wa[h]) : v8bf{}, as_bf8(a), acc[h], 0, 0, 0);
+      acc[h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl ? as_bf8(wb[h]) : v8bf{}, as_bf8(b), acc[h], 0, 0, 0);
+    }
+    if (t > 0) flush(t - 1, sword);
     slot = slot + 1 == kStages ? 0 : slot + 1;
   }
   wait_vmcnt<0>();       // the tail's repeated DMAs have landed: the ring can be reused
   __syncthreads();
+  flush(nt - 1, sbuf[(nt - 1) & 1][frow]);
   float(*red)[32][RP + 1] = reinterpret_cast<float(*)[32][RP + 1]>(lds);  // [4 waves][32 rows t][RP]
   static_assert(4 * 32 * (RP + 1) * 4 <= kStages * kStageB, "reduction tile inside the ring");
   // acc[h] lane l: t = l % 32, ρ = 32 h + (i/4)*8 + (l/32)*4 + i%4
