@@ -488,11 +488,20 @@ __device__ __forceinline__ void lora_bwd_body(const uint16_t* __restrict__ dy, i
     const int mc = live ? m : T - 1;
     v16f p = v16f{};
     uint32_t epack = 0;  // the row's four scale bytes (groups 0..3), 0 past T
+    // The lane's two 16-byte pieces of group g (its first logical chunk cx = 4 g + 2 lg of the row).  Group g + 1's
+    // pieces are read before group g's work, so their LDS latency runs under it (read at the top of each group,
+    // every group waited for its own reads).
+    auto piece = [&](int g, int k) {
+      return *reinterpret_cast<const uint4*>(tile + row * 256 + (((4 * g + 2 * lg + k) ^ (row & 15)) << 4));
+    };
+    uint4 na = piece(0, 0), nc = piece(0, 1);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int cx = 4 * g + 2 * lg;  // the lane's first logical 16-byte chunk of the row
-      const uint4 a = *reinterpret_cast<const uint4*>(tile + row * 256 + ((cx ^ (row & 15)) << 4));
-      const uint4 c = *reinterpret_cast<const uint4*>(tile + row * 256 + (((cx + 1) ^ (row & 15)) << 4));
+      const uint4 a = na, c = nc;
+      if (g < 3) {
+        na = piece(g + 1, 0);
+        nc = piece(g + 1, 1);
+      }
       uint32_t v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
       if constexpr (kQuant) {
         // codes into the wave's code tile (row stride 128 B, 16-byte chunk k at k ^ (row % 8)); scales by row
