@@ -119,7 +119,8 @@ def test_bwd_finish_matches_reference_reduction(gpu):
 
 @pytest.mark.parametrize("T,K,rp,scale", [(300, 1024, 32, 1.0), (4096, 2048, 16, 2.0), (1, 128, 16, 1.0),
                                           (8896, 2048, 32, 1.0), (520, 1280, 32, 1.0), (130, 3072, 16, 2.0),
-                                          (1100, 2048, 64, 1.0), (130, 3072, 64, 2.0), (1, 128, 64, 1.0)])
+                                          (1100, 2048, 64, 1.0), (130, 3072, 64, 2.0), (1, 128, 64, 1.0),
+                                          (260, 256, 32, 1.0), (129, 384, 16, 2.0)])
 def test_quant_lora_matches_quantizer_and_product(T, K, rp, scale, gpu):
     # one read of x: codes and scales bit-identical to mxfp8_quant_tiled; out / outT as lora_nt's contract
     import mxfp8
@@ -142,6 +143,34 @@ def test_quant_lora_matches_quantizer_and_product(T, K, rp, scale, gpu):
     tpad = -(-T // 128) * 128
     assert outT.shape == (rp, tpad) and torch.equal(outT[:, :T].t().cpu(), out.cpu())
     assert int(torch.count_nonzero(outT[:, T:])) == 0
+
+
+@pytest.mark.parametrize("T,K,rp", [(300, 256, 32), (129, 2048, 16), (77, 384, 64)])
+def test_quant_lora_special_blocks(T, K, rp, gpu):
+    """Codes and scale bytes of blocks that are zero, -0, inf, NaN, at the E4M3 saturation boundary (448 * 2^k) or
+    huge, at rows of every 32-row block of a scale tile and in the first and last K steps (the scale words leave one
+    step late, the last ones after the loop): byte for byte mxfp8_quant_tiled's."""
+    import numpy as np
+    import mxfp8
+    from oracle import mx
+    g = torch.Generator().manual_seed(T * K + rp)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    xi = x.view(torch.int16)
+    for row, col in ((0, 0), (33, K - 32), (66, 32), (T - 1, K - 64)):
+        row = min(row, T - 1)
+        xi[row, col:col + 32] = 0
+    xi[min(5, T - 1), K - 96:K - 64] = -32768  # -0.0
+    xi[min(40, T - 1), 64:96] = 0x7F80  # +inf
+    xi[min(70, T - 1), K - 32:K] = 0x7FC0  # NaN
+    xi[min(100, T - 1), 0:32] = -128  # -inf (0xFF80)
+    x[min(9, T - 1), 96:128] = 448.0 * 2.0 ** -7
+    x[min(10, T - 1), K - 128:K - 96] = torch.randn(32, generator=g).to(torch.bfloat16) * 3e38
+    w = (torch.randn(rp, K, generator=g) * 0.02).to(torch.bfloat16)
+    q, s, _, _ = mxfp8.mx_quant_lora(x.to(gpu), w.to(gpu))
+    qr, sr = mxfp8.mx_quant_tiled(x.to(gpu))
+    live = lambda qq: mx.from_tiled(qq.view(torch.uint8).cpu().numpy().reshape(-1), T, K)  # noqa: E731
+    assert np.array_equal(live(q), live(qr))
+    assert torch.equal(s.view(torch.uint8), sr.view(torch.uint8))
 
 
 @pytest.mark.parametrize("T,N,r,scale", [(300, 2048, 16, 2.0), (4096, 1024, 32, 0.5), (1, 128, 16, 1.0),
