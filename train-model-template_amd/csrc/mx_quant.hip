@@ -63,11 +63,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(6, 8))
   const int64_t rt = blockIdx.y;  // row tile
   const int64_t col = ct * kTile + ch * 8;
   const int rl0 = 32 * w + 8 * rg;  // the first of this lane's 8 rows within the tile
+  // Every load is issued (rows past the end re-read the last row): loads under a bounds branch each made the
+  // compiler wait for all eight before the first row's work.  The row axis never uses those rows' values (their
+  // codes are not stored, their scale byte is 0); the column axis takes them as zeros, through a mask (a select
+  // let the compiler put the load back under a branch).
   uint4 v[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int64_t r = rt * kTile + rl0 + k;
-    v[k] = r < rows ? *reinterpret_cast<const uint4*>(x + r * ld_x + col) : make_uint4(0, 0, 0, 0);
+    const uint4 t = *reinterpret_cast<const uint4*>(x + min(r, rows - 1) * ld_x + col);
+    if constexpr (kCols) {
+      const uint32_t m = r < rows ? ~0u : 0u;
+      v[k] = make_uint4(t.x & m, t.y & m, t.z & m, t.w & m);
+    } else {
+      v[k] = t;
+    }
   }
   if (kRows) {
     // every byte of the scale tile is written (0 for rows past `rows`), so the tile needs no clearing
